@@ -1,0 +1,189 @@
+"""Drop-in PathOrderedGeometricMHA backed by the gfx950 HIP kernels.
+
+Usage in the reference's experiment scripts (their plugin API is a module
+name resolved with importlib, experiments/session_cherry.py:278,445):
+
+    python session_cherry.py --attn-module holonomyawareattention_amd.attention_kernel
+
+Interface (kernel/attention_fast_chunked.py:43-61, kernel/attention_kernel.py:193-218):
+  PathOrderedGeometricMHA(d_model, n_heads=4, dropout=0.0, edge_scale=0.1, mode="causal")
+  forward(x (B,L,D), attn_mask (L,L) bool | None, return_geometry=False)
+      -> (y (B,L,D), None | {"C": P (B,H,L,d,d), "H": Hol (B,H,d,d)})
+  attributes h, d, m_dim, edge_scale, scale, mode, link_mode, qkv, out,
+  gqproj, gkproj, edge_mlp, dropout (same state_dict keys).
+
+Rotation model: each head's d dims carry floor(d/3) SO(3) blocks (dims
+3b..3b+2); the generator emits m_dim = 3*floor(d/3) link parameters per head,
+block b's three being the skew entries (0,1), (0,2), (1,2) of its 3x3 block in
+the reference's row-major upper-triangle order (core/utils.py:20-26). Leftover
+dims (d mod 3) are not rotated. This is the reference's dense SO(d) model
+restricted to block-diagonal generators.
+
+The kernel path runs when mode == "causal", attn_mask is exactly tril(L),
+dropout is inactive and x is on the GPU (the conditions of
+kernel/attention_kernel.py:203-208; return_geometry is also supported).
+Anything else raises NotImplementedError, as the guarded reference does
+(kernel/attention_fast_chunked.py:106-114): there is no second code path.
+Forward only: the backward of the fused path raises NotImplementedError.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import kernels
+
+
+def _is_exact_tril(mask: Optional[torch.Tensor], L: int) -> bool:
+    """True iff mask is exactly tril(L) (kernel/attention_kernel.py:193-199)."""
+    if mask is None or tuple(mask.shape) != (L, L):
+        return False
+    tril = torch.ones(L, L, dtype=torch.bool, device=mask.device).tril()
+    return torch.equal(mask.bool(), tril)
+
+
+class _ForwardOnly(torch.autograd.Function):
+    """Attaches the kernel output to the autograd graph; its backward is the
+    unfused-recompute counterpart of kernel/attention_kernel.py:174-187, which
+    this build does not provide yet."""
+
+    @staticmethod
+    def forward(ctx, y, *inputs):
+        return y.view_as(y)
+
+    @staticmethod
+    def backward(ctx, grad):
+        raise NotImplementedError(
+            "holonomyawareattention_amd: the fused path is forward-only "
+            "(backward is not implemented)")
+
+
+class PathOrderedGeometricMHA(nn.Module):
+    def __init__(self, d_model: int, n_heads: int = 4, dropout: float = 0.0,
+                 edge_scale: float = 0.1, mode: str = "causal"):
+        super().__init__()
+        if d_model % n_heads != 0:
+            raise ValueError("d_model must be divisible by n_heads")
+        if mode not in ("causal", "inert"):
+            raise ValueError("mode must be 'causal' or 'inert'")
+        self.h = n_heads
+        self.d = d_model // n_heads
+        self.n_blocks = self.d // 3
+        self.m_dim = 3 * self.n_blocks
+        self.edge_scale = edge_scale
+        self.scale = 1.0 / math.sqrt(self.d)
+        self.mode = mode
+
+        self.qkv = nn.Linear(d_model, 3 * d_model, bias=False)
+        self.out = nn.Linear(d_model, d_model, bias=False)
+        self.dropout = nn.Dropout(dropout)
+        self.gqproj = nn.Linear(d_model, self.m_dim * n_heads, bias=False)
+        self.gkproj = nn.Linear(d_model, self.m_dim * n_heads, bias=False)
+        self.edge_mlp = nn.Sequential(
+            nn.Linear(2 * d_model, 4 * d_model), nn.GELU(),
+            nn.Linear(4 * d_model, self.m_dim * n_heads),
+        )
+        self.link_mode = "interaction"
+        self._wcat_key = None
+        self._wcat = None
+        self._mask_ok = None
+
+    # ---- dispatch predicate (kernel/attention_kernel.py:203-208) ----
+    def _unsupported_reason(self, x, attn_mask) -> Optional[str]:
+        if self.mode != "causal":
+            return f"mode={self.mode!r} (only 'causal' runs on the kernel path)"
+        if not x.is_cuda:
+            return "input is not on the GPU"
+        if self.dropout.p != 0.0 and self.training:
+            return "attention dropout is active (the kernel applies none)"
+        if x.dtype not in (torch.float32, torch.bfloat16):
+            return f"dtype {x.dtype} (float32 and bfloat16 are supported)"
+        if self.link_mode not in ("additive", "interaction"):
+            return f"link_mode={self.link_mode!r}"
+        L = x.shape[1]
+        key = None if attn_mask is None else (attn_mask.data_ptr(), attn_mask._version,
+                                              tuple(attn_mask.shape), attn_mask.device)
+        if key is None or key != self._mask_ok:
+            if not _is_exact_tril(attn_mask, L):
+                return "attn_mask is not exactly tril(L)"
+            self._mask_ok = key
+        return None
+
+    def _kernel_supported(self, x, attn_mask, return_geometry=False) -> bool:
+        return self._unsupported_reason(x, attn_mask) is None
+
+    def _cat_weight(self, mods) -> torch.Tensor:
+        """Row-concatenated weights of `mods` for one GEMM, rebuilt only when a
+        weight changes."""
+        ws = tuple(mod.weight for mod in mods)
+        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+        if key != self._wcat_key:
+            with torch.no_grad():
+                self._wcat = torch.cat([w.detach() for w in ws], dim=0)
+            self._wcat_key = key
+        return self._wcat
+
+    def _link_inputs(self, x: torch.Tensor):
+        """q, k, v views (B,L,H,d) and generator views gq, gk (B,L,H,m).
+
+        The generator leaves the GEMM in fp32 whatever x's dtype: link angle
+        errors accumulate along the path, so the link parameters are never
+        rounded to bf16 (additive: one extra GEMM with an fp32 output;
+        interaction: the edge MLP's last layer)."""
+        B, L, D = x.shape
+        H, d, m = self.h, self.d, self.m_dim
+        x2 = x.reshape(B * L, D)
+        if self.link_mode == "additive":
+            if x.dtype == torch.float32:
+                y5 = F.linear(x, self._cat_weight((self.qkv, self.gqproj, self.gkproj)))
+                qkv = y5[..., :3 * D].view(B, L, H, 3 * d)
+                g = y5[..., 3 * D:]
+            else:
+                qkv = F.linear(x, self.qkv.weight).view(B, L, H, 3 * d)
+                wg = self._cat_weight((self.gqproj, self.gkproj))
+                g = torch.mm(x2, wg.t(), out_dtype=torch.float32).view(B, L, 2 * H * m)
+            gq = g[..., :H * m].view(B, L, H, m)
+            gk = g[..., H * m:].view(B, L, H, m)
+        else:
+            qkv = F.linear(x, self.qkv.weight).view(B, L, H, 3 * d)
+            pair = torch.cat([x, torch.roll(x, shifts=-1, dims=1)], dim=-1)
+            hid = self.edge_mlp[1](self.edge_mlp[0](pair)).reshape(B * L, -1)
+            lin2 = self.edge_mlp[2]
+            if x.dtype == torch.float32:
+                g = F.linear(hid, lin2.weight, lin2.bias)
+            else:
+                g = torch.mm(hid, lin2.weight.t(), out_dtype=torch.float32)
+                if lin2.bias is not None:
+                    g = g + lin2.bias.float()
+            gq = g.view(B, L, H, m)                              # a_t = es * g_t
+            gk = None
+        return qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], gq, gk
+
+    def forward(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor] = None,
+                return_geometry: bool = False
+                ) -> Tuple[torch.Tensor, Optional[Dict[str, torch.Tensor]]]:
+        reason = self._unsupported_reason(x, attn_mask)
+        if reason is not None:
+            raise NotImplementedError(
+                f"holonomyawareattention_amd kernel path does not support this call: {reason}")
+        B, L, D = x.shape
+        params = [p for p in self.parameters() if p.requires_grad]
+        track = torch.is_grad_enabled() and (x.requires_grad or bool(params))
+        with torch.no_grad():
+            q, k, v, gq, gk = self._link_inputs(x)
+            kh, vh_t, P, hol = kernels.geom_scan(k, v, gq, gk, self.edge_scale,
+                                                 want_hol=return_geometry)
+            o = kernels.attention(q, kh, vh_t, P, self.scale)
+            y = F.linear(o.view(B, L, D), self.out.weight)
+        if track:
+            y = _ForwardOnly.apply(y, x, *params)
+        if not return_geometry:
+            return y, None
+        d = self.d
+        C = kernels.quat_to_dense(P, d).to(x.dtype)
+        Hm = kernels.quat_to_dense(hol, d).to(x.dtype)
+        return y, {"C": C, "H": Hm}

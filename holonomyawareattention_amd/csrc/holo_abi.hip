@@ -1,0 +1,171 @@
+// C ABI of the gfx950 path-ordered attention forward (include/holo_mi355x.h):
+// argument validation, status codes and kernel launches. Nothing here
+// allocates device memory or synchronises the host.
+#include <cstdio>
+#include <cstdarg>
+#include <string>
+
+#include "holo_kernels.h"
+#include "../../include/holo_mi355x.h"
+
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+constexpr int kMaxHeadDim = 96;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// element (b, t, h, c < width) at ptr[(b*T + t)*rs + h*hs + c] must not alias
+// across heads/rows in a way the kernels cannot handle: strides positive and
+// rows wide enough for all heads.
+int check_layout(const char* name, int64_t rs, int64_t hs, int H, int width) {
+  if (hs < width || rs < (int64_t)(H - 1) * hs + width)
+    return fail(HOLO_ERR_INVALID_ARG, "%s: strides (row %lld, head %lld) too small for %d heads of width %d",
+                name, (long long)rs, (long long)hs, H, width);
+  return HOLO_OK;
+}
+
+int check_common(int B, int64_t T, int H, int d) {
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0)
+    return fail(HOLO_ERR_BAD_SHAPE, "B, T, H, d must be positive (got %d, %lld, %d, %d)",
+                B, (long long)T, H, d);
+  if (d > kMaxHeadDim)
+    return fail(HOLO_ERR_UNSUPPORTED, "head dimension %d above the supported maximum %d", d, kMaxHeadDim);
+  if ((int64_t)B * H > 0x7fffffff || T > ((int64_t)1 << 31))
+    return fail(HOLO_ERR_UNSUPPORTED, "B*H or T too large");
+  return HOLO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* holo_last_error(void) { return g_last_error.c_str(); }
+
+int holo_abi_version(void) { return (1 << 16) | 0; }
+
+int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
+
+int64_t holo_padded_seq_len(int64_t T) { return holo::padded_seq(T); }
+
+size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d) {
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0) return 0;
+  int64_t nch = holo::padded_seq(T) / holo::kChunk;
+  return (size_t)2 * B * H * nch * (d / 3) * 4 * sizeof(float);
+}
+
+int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
+                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                       const void* gq, int64_t gq_rs, int64_t gq_hs,
+                       const void* gk, int64_t gk_rs, int64_t gk_hs,
+                       const void* k, int64_t k_rs, int64_t k_hs,
+                       const void* v, int64_t v_rs, int64_t v_hs,
+                       void* kh, void* vh_t, float* P, float* hol,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  int rc = check_common(B, T, H, d);
+  if (rc) return rc;
+  if (io_dtype != HOLO_F32 && io_dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "io_dtype %d is not HOLO_F32 or HOLO_BF16", io_dtype);
+  if (gen_dtype != HOLO_F32 && gen_dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "gen_dtype %d is not HOLO_F32 or HOLO_BF16", gen_dtype);
+  if (io_dtype == HOLO_F32 && gen_dtype != HOLO_F32)
+    return fail(HOLO_ERR_UNSUPPORTED, "fp32 keys/values need an fp32 generator");
+  if (gen_mode != HOLO_GEN_ADDITIVE && gen_mode != HOLO_GEN_DIRECT)
+    return fail(HOLO_ERR_INVALID_ARG, "gen_mode %d unknown", gen_mode);
+  const int nb = d / 3;
+  if (!gq || !k || !v || !kh || !vh_t || (nb > 0 && !P))
+    return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if (gen_mode == HOLO_GEN_ADDITIVE && !gk)
+    return fail(HOLO_ERR_INVALID_ARG, "additive generator needs gk");
+  if (gen_mode == HOLO_GEN_DIRECT && gk)
+    return fail(HOLO_ERR_INVALID_ARG, "direct generator takes no gk");
+  if (nb > 0) {
+    if ((rc = check_layout("gq", gq_rs, gq_hs, H, 3 * nb))) return rc;
+    if (gk && (rc = check_layout("gk", gk_rs, gk_hs, H, 3 * nb))) return rc;
+  }
+  if ((rc = check_layout("k", k_rs, k_hs, H, d))) return rc;
+  if ((rc = check_layout("v", v_rs, v_hs, H, d))) return rc;
+  if (!aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)) || (hol && !aligned16(hol)))
+    return fail(HOLO_ERR_INVALID_ARG, "kh, vh_t, P and hol must be 16-byte aligned");
+  size_t need = holo_geom_scan_workspace_size(B, T, H, d);
+  if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+    return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
+                need, workspace ? workspace_bytes : (size_t)0);
+
+  holo::ScanArgs a;
+  a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d);
+  a.nbx = (a.Dp + 2) / 3; a.gen_mode = gen_mode;
+  a.T = T; a.Tp = holo::padded_seq(T); a.nch = a.Tp / holo::kChunk;
+  a.edge_scale = edge_scale;
+  a.gq = gq; a.gq_rs = gq_rs; a.gq_hs = gq_hs;
+  a.gk = gk; a.gk_rs = gk_rs; a.gk_hs = gk_hs;
+  a.k = k; a.k_rs = k_rs; a.k_hs = k_hs;
+  a.v = v; a.v_rs = v_rs; a.v_hs = v_hs;
+  a.kh = kh; a.vh_t = vh_t; a.P = P; a.hol = hol;
+  a.totals = static_cast<float*>(workspace);
+  a.carry = a.totals ? a.totals + (size_t)B * H * a.nch * nb * 4 : nullptr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = io_dtype == HOLO_F32 ? holo::launch_scan<float, float>(a, s)
+                 : gen_dtype == HOLO_F32 ? holo::launch_scan<holo::bf16, float>(a, s)
+                                         : holo::launch_scan<holo::bf16, holo::bf16>(a, s);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "scan launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
+                  const void* q, int64_t q_rs, int64_t q_hs,
+                  const void* kh, const void* vh_t, const float* P,
+                  void* o, int64_t o_rs, int64_t o_hs, void* stream) {
+  g_last_error.clear();
+  int rc = check_common(B, T, H, d);
+  if (rc) return rc;
+  if (dtype != HOLO_F32 && dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "dtype %d is not HOLO_F32 or HOLO_BF16", dtype);
+  const int nb = d / 3;
+  if (!q || !kh || !vh_t || !o || (nb > 0 && !P))
+    return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if ((rc = check_layout("q", q_rs, q_hs, H, d))) return rc;
+  if ((rc = check_layout("o", o_rs, o_hs, H, d))) return rc;
+  if (!aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)))
+    return fail(HOLO_ERR_INVALID_ARG, "kh, vh_t and P must be 16-byte aligned");
+  if (!(scale > 0.f) || !(scale < 1e30f))
+    return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
+
+  holo::AttnArgs a;
+  a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d);
+  a.T = T; a.Tp = holo::padded_seq(T); a.nch = a.Tp / holo::kChunk;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.q = q; a.q_rs = q_rs; a.q_hs = q_hs;
+  a.kh = kh; a.vh_t = vh_t; a.P = P;
+  a.o = o; a.o_rs = o_rs; a.o_hs = o_hs;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = dtype == HOLO_F32 ? holo::launch_attn<float>(a, s)
+                                   : holo::launch_attn<holo::bf16>(a, s);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "attention launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+int holo_quat_to_dense(int64_t n, int d, const float* quat, float* dense, void* stream) {
+  g_last_error.clear();
+  if (n < 0 || d <= 0) return fail(HOLO_ERR_BAD_SHAPE, "n must be >= 0 and d > 0");
+  if (n > 0 && ((d >= 3 && !quat) || !dense)) return fail(HOLO_ERR_INVALID_ARG, "null pointer");
+  if (quat && !aligned16(quat)) return fail(HOLO_ERR_INVALID_ARG, "quat must be 16-byte aligned");
+  hipError_t e = holo::launch_quat_to_dense(n, d, quat, dense, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "quat_to_dense launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+}  // extern "C"

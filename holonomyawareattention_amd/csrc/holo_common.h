@@ -1,0 +1,107 @@
+// Shared device helpers for the gfx950 path-ordered attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace holo {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 64;   // scan chunk = key tile = padding granule of T
+
+__host__ __device__ inline int padded_head_dim(int d) { return (d + 31) / 32 * 32; }
+__host__ __device__ inline int64_t padded_seq(int64_t T) { return (T + kChunk - 1) / kChunk * kChunk; }
+
+__device__ inline float to_f32(float x) { return x; }
+__device__ inline float to_f32(bf16 x) { return (float)x; }
+template <typename T> __device__ inline T from_f32(float x);
+template <> __device__ inline float from_f32<float>(float x) { return x; }
+template <> __device__ inline bf16 from_f32<bf16>(float x) { return (bf16)x; }
+
+// Quaternion (w, x, y, z); R(a (x) b) = R(a) R(b).
+struct quat { float w, x, y, z; };
+
+__device__ inline quat qmul(const quat& a, const quat& b) {
+  quat r;
+  r.w = a.w * b.w - a.x * b.x - a.y * b.y - a.z * b.z;
+  r.x = a.w * b.x + a.x * b.w + a.y * b.z - a.z * b.y;
+  r.y = a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x;
+  r.z = a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w;
+  return r;
+}
+
+__device__ inline quat qident() { return quat{1.f, 0.f, 0.f, 0.f}; }
+
+// exp of the skew block A = [[0,a0,a1],[-a0,0,a2],[-a1,-a2,0]]. A is the cross-
+// product matrix of w = (-a2, a1, -a0), so exp(A) is the rotation by |w| about
+// w: quaternion (cos(th/2), sin(th/2)/th * w). Below th = 1e-4 the two
+// coefficients use their Taylor series (error O(th^4) < 1e-16).
+__device__ inline quat qexp_skew(float a0, float a1, float a2) {
+  float th2 = a0 * a0 + a1 * a1 + a2 * a2;
+  float c, s;   // c = cos(th/2), s = sin(th/2)/th
+  if (th2 < 1e-8f) {
+    c = 1.f - 0.125f * th2;
+    s = 0.5f - th2 * (1.f / 48.f);
+  } else {
+    float th = sqrtf(th2);
+    float sh, ch;
+    sincosf(0.5f * th, &sh, &ch);
+    c = ch;
+    s = sh / th;
+  }
+  return quat{c, -a2 * s, a1 * s, -a0 * s};
+}
+
+// Rotation matrix of q scaled by 1/|q|^2 (exactly orthogonal for any q != 0).
+struct rot3 { float m[3][3]; };
+
+__device__ inline rot3 qmat(const quat& q) {
+  float ww = q.w * q.w, xx = q.x * q.x, yy = q.y * q.y, zz = q.z * q.z;
+  float inv = 1.f / (ww + xx + yy + zz);
+  float xy = q.x * q.y, xz = q.x * q.z, yz = q.y * q.z;
+  float wx = q.w * q.x, wy = q.w * q.y, wz = q.w * q.z;
+  rot3 r;
+  r.m[0][0] = (ww + xx - yy - zz) * inv;
+  r.m[0][1] = 2.f * (xy - wz) * inv;
+  r.m[0][2] = 2.f * (xz + wy) * inv;
+  r.m[1][0] = 2.f * (xy + wz) * inv;
+  r.m[1][1] = (ww - xx + yy - zz) * inv;
+  r.m[1][2] = 2.f * (yz - wx) * inv;
+  r.m[2][0] = 2.f * (xz - wy) * inv;
+  r.m[2][1] = 2.f * (yz + wx) * inv;
+  r.m[2][2] = (ww - xx - yy + zz) * inv;
+  return r;
+}
+
+// y = R^T u
+__device__ inline void rot_t_apply(const rot3& R, float u0, float u1, float u2,
+                                   float& y0, float& y1, float& y2) {
+  y0 = R.m[0][0] * u0 + R.m[1][0] * u1 + R.m[2][0] * u2;
+  y1 = R.m[0][1] * u0 + R.m[1][1] * u1 + R.m[2][1] * u2;
+  y2 = R.m[0][2] * u0 + R.m[1][2] * u1 + R.m[2][2] * u2;
+}
+
+// y = R u
+__device__ inline void rot_apply(const rot3& R, float u0, float u1, float u2,
+                                 float& y0, float& y1, float& y2) {
+  y0 = R.m[0][0] * u0 + R.m[0][1] * u1 + R.m[0][2] * u2;
+  y1 = R.m[1][0] * u0 + R.m[1][1] * u1 + R.m[1][2] * u2;
+  y2 = R.m[2][0] * u0 + R.m[2][1] * u1 + R.m[2][2] * u2;
+}
+
+__device__ inline quat load_quat(const float* p) {
+  f32x4 v = *reinterpret_cast<const f32x4*>(p);
+  return quat{v[0], v[1], v[2], v[3]};
+}
+
+__device__ inline void store_quat(float* p, const quat& q) {
+  f32x4 v = {q.w, q.x, q.y, q.z};
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+
+}  // namespace holo

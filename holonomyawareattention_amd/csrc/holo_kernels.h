@@ -1,0 +1,34 @@
+// Kernel argument blocks and launchers shared by the C ABI and the kernels.
+#pragma once
+
+#include "holo_common.h"
+
+namespace holo {
+
+struct ScanArgs {
+  int B, H, d, nb, nbx, Dp, gen_mode;
+  int64_t T, Tp, nch;
+  float edge_scale;
+  const void* gq; int64_t gq_rs, gq_hs;
+  const void* gk; int64_t gk_rs, gk_hs;
+  const void* k; int64_t k_rs, k_hs;
+  const void* v; int64_t v_rs, v_hs;
+  void* kh; void* vh_t; float* P; float* hol;
+  float* totals;   // (B, H, nch, nb, 4) chunk totals
+  float* carry;    // (B, H, nch, nb, 4) prefix product at each chunk start
+};
+
+struct AttnArgs {
+  int B, H, d, nb, Dp;
+  int64_t T, Tp, nch;
+  float scale_log2;                       // scale * log2(e)
+  const void* q; int64_t q_rs, q_hs;
+  const void* kh; const void* vh_t; const float* P;
+  void* o; int64_t o_rs, o_hs;
+};
+
+template <typename IO, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
+template <typename T> hipError_t launch_attn(const AttnArgs& a, hipStream_t s);
+hipError_t launch_quat_to_dense(int64_t n, int d, const float* q, float* out, hipStream_t s);
+
+}  // namespace holo

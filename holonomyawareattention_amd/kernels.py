@@ -1,0 +1,150 @@
+"""Tensor-level wrappers of the C ABI (device memory and streams come from torch).
+
+``geom_scan``  -> holo_geom_scan_fwd : link rotations, prefix products, kh/vh
+``attention``  -> holo_attn_fwd      : q transport, causal attention, back-rotation
+``quat_to_dense`` -> holo_quat_to_dense
+
+Each wrapper checks devices, dtypes and strides on the host before the launch
+(the kernels index exactly what these shapes describe), allocates its outputs
+on the input's device and launches on the current HIP stream.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: _lib.HOLO_F32, torch.bfloat16: _lib.HOLO_BF16}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _token_view(t: torch.Tensor, B: int, T: int, H: int, width: int, name: str):
+    """(B, T, H, width) view with unit inner stride and row-major (b, t) rows.
+    Returns (row_stride, head_stride) in elements."""
+    if t.dim() != 4 or tuple(t.shape) != (B, T, H, width):
+        raise ValueError(f"{name}: expected shape {(B, T, H, width)}, got {tuple(t.shape)}")
+    sb, st, sh, sc = t.stride()
+    if width > 1 and sc != 1:
+        raise ValueError(f"{name}: needs unit inner stride (strides {t.stride()})")
+    hs = sh if H > 1 else width
+    if T > 1:
+        rs = st
+        if B > 1 and sb != T * st:
+            raise ValueError(f"{name}: (b, t) rows must be evenly strided (strides {t.stride()})")
+    else:
+        rs = sb if B > 1 else (H - 1) * hs + width
+    return rs, hs
+
+
+def padded_head_dim(d: int) -> int:
+    return int(_lib.load().holo_padded_head_dim(d))
+
+
+def padded_seq_len(T: int) -> int:
+    return int(_lib.load().holo_padded_seq_len(T))
+
+
+def geom_scan(k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor, gk: Optional[torch.Tensor],
+              edge_scale: float, want_hol: bool = False
+              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """k, v: (B,T,H,d) views; gq, gk: (B,T,H,3*nb) views (gk None: gq is the
+    full link parameter g and a_t = edge_scale * g_t). The generator may be
+    fp32 with bf16 k/v (link parameters are composed in fp32 either way).
+    Returns kh (B,H,Tp,Dp), vh_t (B,H,Tp/64,Dp,64), P (B,H,T,nb,4) fp32,
+    Hol (B,H,nb,4) fp32 or None."""
+    lib = _lib.load()
+    B, T, H, d = k.shape
+    nb = d // 3
+    dev = k.device
+    if dev.type != "cuda":
+        raise ValueError("geom_scan: tensors must be on a GPU")
+    dt = k.dtype
+    if dt not in _DT:
+        raise ValueError(f"geom_scan: unsupported dtype {dt}")
+    if v.dtype != dt or v.device != dev:
+        raise ValueError(f"geom_scan: v must be {dt} on {dev}")
+    gdt = gq.dtype
+    if gdt not in _DT or (dt == torch.float32 and gdt != torch.float32):
+        raise ValueError(f"geom_scan: generator dtype {gdt} with {dt} keys is not supported")
+    for name, t in (("gq", gq), ("gk", gk)):
+        if t is not None and (t.dtype != gdt or t.device != dev):
+            raise ValueError(f"geom_scan: {name} must be {gdt} on {dev}")
+    k_rs, k_hs = _token_view(k, B, T, H, d, "k")
+    v_rs, v_hs = _token_view(v, B, T, H, d, "v")
+    gq_rs, gq_hs = _token_view(gq, B, T, H, 3 * nb, "gq")
+    gk_rs, gk_hs = (0, 0) if gk is None else _token_view(gk, B, T, H, 3 * nb, "gk")
+    Dp, Tp = padded_head_dim(d), padded_seq_len(T)
+    kh = torch.empty((B, H, Tp, Dp), dtype=dt, device=dev)
+    vh_t = torch.empty((B, H, Tp // 64, Dp, 64), dtype=dt, device=dev)
+    P = torch.empty((B, H, T, nb, 4), dtype=torch.float32, device=dev)
+    hol = torch.empty((B, H, nb, 4), dtype=torch.float32, device=dev) if want_hol else None
+    ws_bytes = int(lib.holo_geom_scan_workspace_size(B, T, H, d))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    rc = lib.holo_geom_scan_fwd(
+        B, T, H, d, _lib.HOLO_GEN_DIRECT if gk is None else _lib.HOLO_GEN_ADDITIVE,
+        float(edge_scale), _DT[dt], _DT[gdt],
+        _ptr(gq), gq_rs, gq_hs, _ptr(gk), gk_rs, gk_hs,
+        _ptr(k), k_rs, k_hs, _ptr(v), v_rs, v_hs,
+        _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(hol),
+        _ptr(ws), ws_bytes, _stream(dev))
+    _lib.check(rc, "holo_geom_scan_fwd")
+    return kh, vh_t, P, hol
+
+
+def attention(q: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
+              scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """q: (B,T,H,d) view of raw queries; kh, vh_t, P from geom_scan.
+    Returns o as a (B,T,H,d) tensor (contiguous (B,T,H*d) storage unless
+    `out` is given)."""
+    lib = _lib.load()
+    B, T, H, d = q.shape
+    nb = d // 3
+    dev, dt = q.device, q.dtype
+    if dev.type != "cuda" or dt not in _DT:
+        raise ValueError(f"attention: q must be a float32/bfloat16 GPU tensor (got {dt} on {dev})")
+    Dp, Tp = padded_head_dim(d), padded_seq_len(T)
+    if tuple(kh.shape) != (B, H, Tp, Dp) or not kh.is_contiguous() or kh.dtype != dt:
+        raise ValueError("attention: kh does not match the geom_scan layout")
+    if tuple(vh_t.shape) != (B, H, Tp // 64, Dp, 64) or not vh_t.is_contiguous() or vh_t.dtype != dt:
+        raise ValueError("attention: vh_t does not match the geom_scan layout")
+    if tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous() or P.dtype != torch.float32:
+        raise ValueError("attention: P does not match the geom_scan layout")
+    for t in (kh, vh_t, P):
+        if t.device != dev:
+            raise ValueError("attention: all tensors must be on one device")
+    q_rs, q_hs = _token_view(q, B, T, H, d, "q")
+    if out is None:
+        out = torch.empty((B, T, H, d), dtype=dt, device=dev)
+    elif out.dtype != dt or out.device != dev:
+        raise ValueError("attention: out must match q's dtype and device")
+    o_rs, o_hs = _token_view(out, B, T, H, d, "out")
+    rc = lib.holo_attn_fwd(B, T, H, d, _DT[dt], float(scale),
+                           _ptr(q), q_rs, q_hs, _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
+                           _ptr(out), o_rs, o_hs, _stream(dev))
+    _lib.check(rc, "holo_attn_fwd")
+    return out
+
+
+def quat_to_dense(quat: torch.Tensor, d: int) -> torch.Tensor:
+    """(..., nb, 4) fp32 quaternions -> (..., d, d) fp32 block rotations."""
+    lib = _lib.load()
+    nb = d // 3
+    if quat.shape[-2:] != (nb, 4) or quat.dtype != torch.float32 or not quat.is_contiguous():
+        raise ValueError(f"quat_to_dense: expected contiguous fp32 (..., {nb}, 4)")
+    lead = quat.shape[:-2]
+    n = 1
+    for s in lead:
+        n *= int(s)
+    out = torch.empty((*lead, d, d), dtype=torch.float32, device=quat.device)
+    rc = lib.holo_quat_to_dense(n, d, _ptr(quat) if nb else None, _ptr(out), _stream(quat.device))
+    _lib.check(rc, "holo_quat_to_dense")
+    return out

@@ -1,0 +1,146 @@
+/*
+ * holo_mi355x.h -- C ABI of the MI355X (gfx950) path-ordered attention forward.
+ *
+ * The reference (SiddhiMali/HolonomyAwareAttention) exposes this path as a
+ * PyTorch module and one Triton operator; it has no native ABI. The entry
+ * points below replace, one for one, the pieces of that path:
+ *
+ *   holo_geom_scan_fwd  replaces PathOrderedGeometricMHA._geometry after the
+ *                       projections (link rotations, prefix products,
+ *                       holonomy: core/attention_fast_chunked.py:73-96) and
+ *                       the key/value transports (:109-110);
+ *   holo_attn_fwd       replaces HoloAttnFn.apply / run_fwd_kernel /
+ *                       fwd_kernel (kernel/attention_kernel.py:40-134,166-172):
+ *                       query transport, causal online-softmax attention and
+ *                       the back-rotation out_i = P_i o_i
+ *                       (core/attention_fast_chunked.py:108,119-171);
+ *   holo_quat_to_dense  expands the stored rotations to the reference's dense
+ *                       geometry tensors {"C": P, "H": Hol}
+ *                       (core/attention_fast_chunked.py:175-177).
+ *
+ * Conventions
+ *   - Every pointer is a device pointer owned by the caller; no entry point
+ *     allocates device memory. Work that needs scratch takes a caller
+ *     workspace whose size comes from the matching *_workspace_size query.
+ *   - `stream` is a hipStream_t (0 = the null stream). Calls are asynchronous,
+ *     never synchronise the host and keep no state between calls.
+ *   - Return value 0 is success; otherwise one of holo_status, with a message
+ *     available from holo_last_error() (thread-local).
+ *   - Rotation model: head dimension d holds nb = floor(d/3) SO(3) blocks on
+ *     dims 3b..3b+2; the remaining d - 3nb dims are not rotated. A block's
+ *     three link parameters (a0, a1, a2) are the skew entries A[0][1], A[0][2],
+ *     A[1][2] (row-major upper triangle, core/utils.py:20-26).
+ *   - Rotations are stored as quaternions (w, x, y, z), fp32, one per block:
+ *     P (B, H, T, nb, 4). The rotation matrix of q is the homogeneous map
+ *     R(q) = (1/|q|^2) * [...]; exp(A) for a block is the quaternion
+ *     (cos(th/2), sin(th/2)/th * (-a2, a1, -a0)), th = |a|.
+ */
+#ifndef HOLO_MI355X_H
+#define HOLO_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define HOLO_API __attribute__((visibility("default")))
+#else
+#define HOLO_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum holo_status {
+  HOLO_OK = 0,
+  HOLO_ERR_INVALID_ARG = 1,   /* null pointer, bad stride or dtype          */
+  HOLO_ERR_BAD_SHAPE = 2,     /* inconsistent sizes (ValueError upstream)   */
+  HOLO_ERR_UNSUPPORTED = 3,   /* outside the kernel path (NotImplementedError) */
+  HOLO_ERR_WORKSPACE = 4,     /* workspace missing or too small             */
+  HOLO_ERR_LAUNCH = 5         /* HIP reported an error at launch            */
+} holo_status;
+
+typedef enum holo_dtype {
+  HOLO_F32 = 0,
+  HOLO_BF16 = 1
+} holo_dtype;
+
+typedef enum holo_gen_mode {
+  /* a_t = edge_scale * (gq_t + gk_{(t+1) mod T})  (core/attention_fast_chunked.py:80-84) */
+  HOLO_GEN_ADDITIVE = 0,
+  /* a_t = edge_scale * g_t, g supplied by the caller in `gq`, e.g. the
+     interaction edge-MLP output (core/attention_fast_chunked.py:73-79)       */
+  HOLO_GEN_DIRECT = 1
+} holo_gen_mode;
+
+/* Message for the last failing call on this thread ("" if none). */
+HOLO_API const char* holo_last_error(void);
+
+/* ABI version: (major << 16) | minor. */
+HOLO_API int holo_abi_version(void);
+
+/* Padded head dimension used by the kh / vh_t layouts (d rounded up to 32). */
+HOLO_API int holo_padded_head_dim(int d);
+
+/* Padded sequence length used by the kh / vh_t layouts (T rounded up to 64). */
+HOLO_API int64_t holo_padded_seq_len(int64_t T);
+
+/* Workspace bytes for holo_geom_scan_fwd. */
+HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
+
+/*
+ * Link rotations, chunked prefix-product scan and key/value transport.
+ *
+ * Inputs (token-major as the projections produce them):
+ *   gq, gk : dtype `gen_dtype` (fp32, or bf16 with bf16 k/v), element (b, t, h, j)
+ *            at ptr[(b*T + t)*row_stride + h*head_stride + j], j < 3*nb.
+ *            In HOLO_GEN_DIRECT mode gk must be NULL. Link parameters are
+ *            accumulated and composed in fp32 whatever their storage type.
+ *   k, v   : dtype `io_dtype`.
+ *            element (b, t, h, c) at ptr[(b*T + t)*row_stride + h*head_stride + c], c < d.
+ * Outputs:
+ *   kh   (B, H, Tp, Dp)        io_dtype, kh[t] = P_t^T k_t   (Tp = padded T, Dp = padded d)
+ *   vh_t (B, H, Tp/64, Dp, 64) io_dtype, key tiles of 64 stored transposed:
+ *                               vh_t[b][h][t/64][c][t%64] = (P_t^T v_t)[c]
+ *        Padding (t >= T or c >= d) is written as zero.
+ *   P    (B, H, T, nb, 4)      fp32 quaternions of the prefix products
+ *                               P_0 = I, P_{t+1} = G_t P_t   (:89-94)
+ *   hol  (B, H, nb, 4)         fp32 holonomy G_close P_{T-1} (:95), or NULL.
+ * The scan composes within chunks of 64 links and re-anchors each chunk on the
+ * product of all earlier chunks.
+ */
+HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
+                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                       const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
+                       const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
+                       const void* k, int64_t k_row_stride, int64_t k_head_stride,
+                       const void* v, int64_t v_row_stride, int64_t v_head_stride,
+                       void* kh, void* vh_t, float* P, float* hol,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Causal path-ordered attention on transported keys/values.
+ *   q    : raw queries, element (b, t, h, c) at q[(b*T + t)*q_row_stride + h*q_head_stride + c]
+ *   kh, vh_t, P : as written by holo_geom_scan_fwd (same B, T, H, d, dtype)
+ *   o    : output, element (b, t, h, c) at o[(b*T + t)*o_row_stride + h*o_head_stride + c]
+ *          o_i = P_i * sum_{j<=i} softmax_j(scale * (P_i^T q_i).kh_j) * vh_j
+ * dtype is the dtype of q, kh, vh_t and o (HOLO_BF16: bf16 MFMA with fp32
+ * accumulation and softmax; HOLO_F32: fp32 MFMA throughout).
+ */
+HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
+                  const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                  const void* kh, const void* vh_t, const float* P,
+                  void* o, int64_t o_row_stride, int64_t o_head_stride,
+                  void* stream);
+
+/*
+ * Expand quaternions (n, nb, 4) to dense fp32 rotation matrices (n, d, d):
+ * block b on dims 3b..3b+2, identity on the leftover dims.
+ */
+HOLO_API int holo_quat_to_dense(int64_t n, int d, const float* quat, float* dense, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HOLO_MI355X_H */

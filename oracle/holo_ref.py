@@ -1,0 +1,378 @@
+"""CPU oracle for the path-ordered (holonomy) attention forward.
+
+TEST INFRASTRUCTURE ONLY. Nothing in the product imports this module: only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and only
+as the checker (or, in bench.py, as the timed CPU baseline), never as the code
+path being measured or shipped.
+
+Three restatements of the reference algorithm (SiddhiMali/HolonomyAwareAttention),
+all written from the reference's behaviour, not copied:
+
+* ``forward_chunked`` follows ``core/attention_fast_chunked.py`` step by step in
+  the caller's dtype (fp32 or fp64): per-head interleaved QKV split (:69-71),
+  generator times ``edge_scale`` (:73-84), dense skew (``core/utils.py:4-27``)
+  and ``torch.matrix_exp`` (``core/utils.py:30-52``), strictly sequential
+  left-multiplied prefix products (:89-95), P^T transports (:108-110), the
+  wrap branch with Hol^T (:112-117), key blocks of BLOCK_K=64 with an online
+  softmax and ``finfo.min`` masking (:119-166), normalisation, P back-rotation
+  and the out-projection (:168-173). The SO(3)-block rotation model is run by
+  scattering the block parameters into the dense skew layout (every other
+  entry zero), which the reference's own code then computes exactly.
+* ``forward_blocks`` computes the same function in fp64 with the structure made
+  explicit: closed-form Rodrigues 3x3 blocks, a 3x3 sequential scan, plain
+  causal softmax (the wrap branch is always masked under tril). It is the fast
+  checker for large slices; it is pinned against ``forward_chunked`` and the
+  golden fixtures at small sizes.
+* ``forward_arc_walk`` is the brute-force O(L^3) definition of
+  ``core/attention.py:156-192`` (walk the ring arc j -> i composing edge
+  rotations), for tiny L.
+
+Pinning (every function has at least one independent check in tests/):
+  skew_from_vec / block scatter / geometry / forward_chunked
+        -> golden vectors written by importing the reference
+           (tests/golden/make_golden.py), both link modes, fp64 and fp32;
+  rodrigues -> torch.linalg.matrix_exp in fp64, G^T G = I, det = +1,
+           exp(0)=I, exp(A)exp(-A)=I, small-angle series, angle pi;
+  scan  -> brute-force products, P_0 = I, orthogonality;
+  forward_blocks -> forward_chunked (fp64), flat-connection reduction
+           (edge_scale = 0 gives torch's causal scaled_dot_product_attention),
+           gauge invariance, causal prefix consistency, forward_arc_walk.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+import torch
+
+BLOCK_K = 64          # key-block width of core/attention_fast_chunked.py:33
+
+
+# --------------------------------------------------------------------------
+# rotation-model helpers
+# --------------------------------------------------------------------------
+def n_blocks(d: int) -> int:
+    """Number of SO(3) blocks per head: floor(d/3); leftover dims are identity."""
+    return d // 3
+
+
+def block_param_count(d: int) -> int:
+    return 3 * n_blocks(d)
+
+
+def dense_index(i: int, j: int, d: int) -> int:
+    """Position of entry (i, j), i < j, in the row-major upper-triangle vector
+    that core/utils.py:20-26 reads (i outer, j inner)."""
+    return i * d - i * (i + 1) // 2 + (j - i - 1)
+
+
+def block_to_dense_map(d: int) -> np.ndarray:
+    """dense index of each block parameter: block b, component c in
+    (a01, a02, a12) of A_b = [[0,a01,a02],[-a01,0,a12],[-a02,-a12,0]]."""
+    out = []
+    for b in range(n_blocks(d)):
+        r = 3 * b
+        out += [dense_index(r, r + 1, d), dense_index(r, r + 2, d),
+                dense_index(r + 1, r + 2, d)]
+    return np.asarray(out, dtype=np.int64)
+
+
+def dense_rows_from_block(w_blk: torch.Tensor, n_heads: int, d: int) -> torch.Tensor:
+    """Scatter a block-layout generator matrix (H*m_blk, ...) into the
+    reference's dense layout (H*d(d-1)/2, ...), zeros elsewhere."""
+    mb, md = block_param_count(d), d * (d - 1) // 2
+    mp = torch.as_tensor(block_to_dense_map(d))
+    w = w_blk.reshape(n_heads, mb, *w_blk.shape[1:])
+    out = w.new_zeros(n_heads, md, *w_blk.shape[1:])
+    out[:, mp] = w
+    return out.reshape(n_heads * md, *w_blk.shape[1:])
+
+
+def skew_from_vec(v: torch.Tensor, d: int) -> torch.Tensor:
+    """Row-major upper-triangle vector -> skew matrix (core/utils.py:4-27):
+    A[i,j] = v[idx], A[j,i] = -v[idx], idx running i-major over i < j."""
+    *prefix, m = v.shape
+    if m != d * (d - 1) // 2:
+        raise ValueError(f"Expected last dim {d * (d - 1) // 2}, got {m}")
+    rows, cols = torch.triu_indices(d, d, offset=1)
+    A = v.new_zeros(*prefix, d, d)
+    A[..., rows, cols] = v
+    A[..., cols, rows] = -v
+    return A
+
+
+def so_exp(A: torch.Tensor) -> torch.Tensor:
+    """core/utils.py:30-52: the matrix exponential (torch's routine)."""
+    return torch.matrix_exp(A)
+
+
+# --------------------------------------------------------------------------
+# restatement of core/attention_fast_chunked.py
+# --------------------------------------------------------------------------
+def _linear(x, w, b=None):
+    y = x @ w.transpose(0, 1)
+    return y if b is None else y + b
+
+
+def generator_params(x: torch.Tensor, W: Dict[str, torch.Tensor], n_heads: int,
+                     edge_scale: float, link_mode: str) -> torch.Tensor:
+    """Block-layout link parameters a (B, H, T, m_blk) for the T edges
+    t -> t+1 (mod T); edge T-1 is the closing edge.
+    additive:    a_t = (gq(x_t) + gk(x_{t+1})) * edge_scale     (:80-84)
+    interaction: a_t = edge_mlp([x_t ; x_{t+1}]) * edge_scale   (:73-79)
+    """
+    B, T, D = x.shape
+    d = D // n_heads
+    m = block_param_count(d)
+    if link_mode == "additive":
+        gq = _linear(x, W["gqproj.weight"]).view(B, T, n_heads, m).transpose(1, 2)
+        gk = _linear(x, W["gkproj.weight"]).view(B, T, n_heads, m).transpose(1, 2)
+        return (gq + torch.roll(gk, shifts=-1, dims=2)) * edge_scale
+    if link_mode == "interaction":
+        pair = torch.cat([x, torch.roll(x, shifts=-1, dims=1)], dim=-1)
+        h = torch.nn.functional.gelu(_linear(pair, W["edge_mlp.0.weight"], W["edge_mlp.0.bias"]))
+        a = _linear(h, W["edge_mlp.2.weight"], W["edge_mlp.2.bias"])
+        return a.view(B, T, n_heads, m).transpose(1, 2) * edge_scale
+    raise ValueError(f"unknown link_mode {link_mode!r}")
+
+
+def split_qkv(x: torch.Tensor, w_qkv: torch.Tensor, n_heads: int):
+    """Per-head interleaved split of x W_qkv^T: columns [q_h | k_h | v_h] for
+    each head h (core/attention_fast_chunked.py:69-71). Returns (B,H,T,d) x3."""
+    B, T, D = x.shape
+    d = D // n_heads
+    qkv = _linear(x, w_qkv).view(B, T, n_heads, 3 * d)
+    q, k, v = qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:]
+    return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+
+
+def geometry_chunked(x: torch.Tensor, W: Dict[str, torch.Tensor], n_heads: int,
+                     edge_scale: float, link_mode: str = "additive",
+                     a: Optional[torch.Tensor] = None):
+    """q, k, v, P, Hol as core/attention_fast_chunked.py:63-96 computes them,
+    on the dense d x d layout. `a` (B,H,T,m_blk) overrides the generator."""
+    B, T, D = x.shape
+    d = D // n_heads
+    q, k, v = split_qkv(x, W["qkv.weight"], n_heads)
+    if a is None:
+        a = generator_params(x, W, n_heads, edge_scale, link_mode)
+    md = d * (d - 1) // 2
+    a_dense = a.new_zeros(B, n_heads, T, md)
+    a_dense[..., torch.as_tensor(block_to_dense_map(d))] = a
+    G_adj = so_exp(skew_from_vec(a_dense[:, :, :-1], d))
+    G_close = so_exp(skew_from_vec(a_dense[:, :, -1], d))
+    eye = torch.eye(d, dtype=x.dtype)
+    P = torch.empty(B, n_heads, T, d, d, dtype=x.dtype)
+    P[:, :, 0] = eye
+    Pt = eye.expand(B, n_heads, d, d).clone()
+    for t in range(T - 1):
+        Pt = G_adj[:, :, t] @ Pt                 # left-multiply (:93)
+        P[:, :, t + 1] = Pt
+    Hol = G_close @ P[:, :, T - 1]
+    return q, k, v, P, Hol
+
+
+def attention_core_chunked(q, k, v, P, Hol, scale: float, block_k: int = BLOCK_K):
+    """Transport, key-block online softmax with the (masked) wrap branch, and
+    back-rotation, as core/attention_fast_chunked.py:105-171 with a tril mask.
+    Returns the per-head outputs (B, H, T, d) before the out-projection."""
+    B, H, L, d = q.shape
+    dtype = q.dtype
+    qh = torch.einsum("bhide,bhid->bhie", P, q)          # P_i^T q_i
+    kh_all = torch.einsum("bhjde,bhjd->bhje", P, k)
+    vh_all = torch.einsum("bhjde,bhjd->bhje", P, v)
+    kh_wrap = torch.einsum("bhef,bhje->bhjf", Hol, kh_all)
+    vh_wrap = torch.einsum("bhef,bhje->bhjf", Hol, vh_all)
+    neg = torch.finfo(dtype).min
+    m_run = torch.full((B, H, L), neg, dtype=dtype)
+    l_run = torch.zeros((B, H, L), dtype=dtype)
+    o_run = torch.zeros((B, H, L, d), dtype=dtype)
+    idx = torch.arange(L)
+    for k0 in range(0, L, block_k):
+        k1 = min(k0 + block_k, L)
+        jj = idx[k0:k1]
+        base = (idx.view(L, 1) >= jj.view(1, -1)).view(1, 1, L, -1)
+        s_base = torch.einsum("bhie,bhje->bhij", qh, kh_all[:, :, k0:k1]) * scale
+        s_wrap = torch.einsum("bhie,bhje->bhij", qh, kh_wrap[:, :, k0:k1]) * scale
+        s = torch.where(base, s_base, s_wrap)
+        s = s.masked_fill(~base, neg)            # tril: allowed == (i >= j)
+        m_new = torch.maximum(m_run, s.max(dim=-1).values)
+        corr = torch.exp(m_run - m_new)
+        p = torch.exp(s - m_new.unsqueeze(-1))
+        l_run = l_run * corr + p.sum(dim=-1)
+        cb = torch.einsum("bhij,bhje->bhie", p * base, vh_all[:, :, k0:k1])
+        cw = torch.einsum("bhij,bhje->bhie", p * ~base, vh_wrap[:, :, k0:k1])
+        o_run = o_run * corr.unsqueeze(-1) + cb + cw
+        m_run = m_new
+    o_run = o_run / l_run.clamp_min(1e-20).unsqueeze(-1)
+    return torch.einsum("bhide,bhie->bhid", P, o_run)   # P_i o_i
+
+
+def forward_chunked(x: torch.Tensor, W: Dict[str, torch.Tensor], n_heads: int,
+                    edge_scale: float, link_mode: str = "additive",
+                    a: Optional[torch.Tensor] = None, return_geometry: bool = False):
+    """y = PathOrderedGeometricMHA.forward(x, tril) of the reference chunked
+    implementation, in x's dtype. W holds block-layout weights (torch tensors
+    of x's dtype)."""
+    B, T, D = x.shape
+    d = D // n_heads
+    q, k, v, P, Hol = geometry_chunked(x, W, n_heads, edge_scale, link_mode, a)
+    o = attention_core_chunked(q, k, v, P, Hol, 1.0 / math.sqrt(d))
+    y = _linear(o.transpose(1, 2).reshape(B, T, D), W["out.weight"])
+    if return_geometry:
+        return y, {"C": P, "H": Hol}
+    return y
+
+
+# --------------------------------------------------------------------------
+# block-structured fp64 restatement (fast checker for large slices)
+# --------------------------------------------------------------------------
+def rodrigues(a: np.ndarray) -> np.ndarray:
+    """exp of A = [[0,a0,a1],[-a0,0,a2],[-a1,-a2,0]] for a (..., 3), float64:
+    I + (sin th / th) A + ((1 - cos th) / th^2) A^2, th = |a|, with the
+    Taylor series of both coefficients below th = 1e-4."""
+    a = np.asarray(a, dtype=np.float64)
+    a0, a1, a2 = a[..., 0], a[..., 1], a[..., 2]
+    z = np.zeros_like(a0)
+    A = np.stack([np.stack([z, a0, a1], -1),
+                  np.stack([-a0, z, a2], -1),
+                  np.stack([-a1, -a2, z], -1)], -2)
+    th2 = a0 * a0 + a1 * a1 + a2 * a2
+    th = np.sqrt(th2)
+    small = th < 1e-4
+    ths = np.where(small, 1.0, th)
+    s1 = np.where(small, 1.0 - th2 / 6.0 + th2 * th2 / 120.0, np.sin(ths) / ths)
+    s2 = np.where(small, 0.5 - th2 / 24.0 + th2 * th2 / 720.0, (1.0 - np.cos(ths)) / (ths * ths))
+    eye = np.broadcast_to(np.eye(3), A.shape)
+    return eye + s1[..., None, None] * A + s2[..., None, None] * (A @ A)
+
+
+def prefix_blocks(G: np.ndarray) -> np.ndarray:
+    """P_0 = I, P_{t+1} = G_t P_t along axis -4 of G (..., T-1, nb, 3, 3);
+    returns (..., T, nb, 3, 3)."""
+    *lead, Tm1, nb, _, _ = G.shape
+    P = np.empty((*lead, Tm1 + 1, nb, 3, 3), dtype=np.float64)
+    cur = np.broadcast_to(np.eye(3), (*lead, nb, 3, 3)).copy()
+    P[..., 0, :, :, :] = cur
+    for t in range(Tm1):
+        cur = G[..., t, :, :, :] @ cur
+        P[..., t + 1, :, :, :] = cur
+    return P
+
+
+def apply_blocks_T(P: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """u^_t = P_t^T u_t on the block dims of u (..., T, d); leftover dims pass."""
+    nb = P.shape[-3]
+    out = u.copy()
+    ub = u[..., :3 * nb].reshape(*u.shape[:-1], nb, 3)
+    out[..., :3 * nb] = np.einsum("...bij,...bi->...bj", P, ub).reshape(*u.shape[:-1], 3 * nb)
+    return out
+
+
+def apply_blocks(P: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """u_t = P_t u^_t on the block dims."""
+    nb = P.shape[-3]
+    out = u.copy()
+    ub = u[..., :3 * nb].reshape(*u.shape[:-1], nb, 3)
+    out[..., :3 * nb] = np.einsum("...bij,...bj->...bi", P, ub).reshape(*u.shape[:-1], 3 * nb)
+    return out
+
+
+def causal_attention64(qh: np.ndarray, kh: np.ndarray, vh: np.ndarray, scale: float,
+                       q_block: int = 256) -> np.ndarray:
+    """softmax(q k^T * scale + causal) v over (..., T, d), float64, query-blocked."""
+    T = qh.shape[-2]
+    out = np.empty_like(qh)
+    for i0 in range(0, T, q_block):
+        i1 = min(T, i0 + q_block)
+        s = np.einsum("...id,...jd->...ij", qh[..., i0:i1, :], kh[..., :i1, :]) * scale
+        mask = np.arange(i0, i1)[:, None] >= np.arange(i1)[None, :]
+        s = np.where(mask, s, -np.inf)
+        s = s - s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        out[..., i0:i1, :] = np.einsum("...ij,...jd->...id", p, vh[..., :i1, :])
+    return out
+
+
+def geometry_blocks(a: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    """a (B,H,T,m_blk) -> P (B,H,T,nb,3,3) and Hol (B,H,nb,3,3), float64."""
+    B, H, T, m = a.shape
+    nb = m // 3
+    G = rodrigues(a.reshape(B, H, T, nb, 3))
+    P = prefix_blocks(G[:, :, :-1])
+    Hol = G[:, :, -1] @ P[:, :, -1]
+    return P, Hol
+
+
+def forward_blocks(x: np.ndarray, W: Dict[str, np.ndarray], n_heads: int,
+                   edge_scale: float, link_mode: str = "additive",
+                   a: Optional[np.ndarray] = None, return_parts: bool = False):
+    """float64 forward on the block structure. x (B,T,D); W block-layout."""
+    x = np.asarray(x, dtype=np.float64)
+    B, T, D = x.shape
+    H = n_heads
+    d = D // H
+    Wt = {k: torch.as_tensor(np.asarray(w, dtype=np.float64)) for k, w in W.items()}
+    xt = torch.as_tensor(x)
+    q, k, v = (t.numpy() for t in split_qkv(xt, Wt["qkv.weight"], H))
+    if a is None:
+        a = generator_params(xt, Wt, H, edge_scale, link_mode).numpy()
+    P, Hol = geometry_blocks(np.asarray(a, dtype=np.float64))
+    qh, kh, vh = (apply_blocks_T(P, u) for u in (q, k, v))
+    oh = causal_attention64(qh, kh, vh, 1.0 / math.sqrt(d))
+    o = apply_blocks(P, oh)
+    y = o.transpose(0, 2, 1, 3).reshape(B, T, D) @ np.asarray(W["out.weight"], np.float64).T
+    if return_parts:
+        return y, dict(q=q, k=k, v=v, a=a, P=P, Hol=Hol, qh=qh, kh=kh, vh=vh, oh=oh, o=o)
+    return y
+
+
+def blocks_to_dense(Pb: np.ndarray, d: int) -> np.ndarray:
+    """(..., nb, 3, 3) block rotations -> (..., d, d) with identity leftovers."""
+    nb = Pb.shape[-3]
+    out = np.zeros((*Pb.shape[:-3], d, d), dtype=Pb.dtype)
+    for b in range(nb):
+        out[..., 3 * b:3 * b + 3, 3 * b:3 * b + 3] = Pb[..., b, :, :]
+    for r in range(3 * nb, d):
+        out[..., r, r] = 1.0
+    return out
+
+
+# --------------------------------------------------------------------------
+# brute-force definition (core/attention.py:156-192), tiny L only
+# --------------------------------------------------------------------------
+def forward_arc_walk(x: np.ndarray, W: Dict[str, np.ndarray], n_heads: int,
+                     edge_scale: float, link_mode: str = "additive") -> np.ndarray:
+    """Transport key/value j to query i by walking the ring arc j -> j+1 -> ...
+    -> i with the edge rotations (crossing the closing edge when i < j), then
+    softmax over the allowed (tril) keys. float64, O(L^3)."""
+    x = np.asarray(x, dtype=np.float64)
+    B, T, D = x.shape
+    H = n_heads
+    d = D // H
+    Wt = {k: torch.as_tensor(np.asarray(w, dtype=np.float64)) for k, w in W.items()}
+    xt = torch.as_tensor(x)
+    q, k, v = (t.numpy() for t in split_qkv(xt, Wt["qkv.weight"], H))
+    a = generator_params(xt, Wt, H, edge_scale, link_mode).numpy()
+    G = blocks_to_dense(rodrigues(a.reshape(B, H, T, -1, 3)), d)     # (B,H,T,d,d)
+    out = np.zeros((B, H, T, d))
+    for i in range(T):
+        Kt = np.zeros((B, H, T, d))
+        Vt = np.zeros((B, H, T, d))
+        for j in range(T):
+            U = np.broadcast_to(np.eye(d), (B, H, d, d)).copy()
+            t = j
+            while t != i:
+                U = G[:, :, t] @ U
+                t = (t + 1) % T
+            Kt[:, :, j] = np.einsum("bhdf,bhf->bhd", U, k[:, :, j])
+            Vt[:, :, j] = np.einsum("bhdf,bhf->bhd", U, v[:, :, j])
+        s = np.einsum("bhd,bhjd->bhj", q[:, :, i], Kt) / math.sqrt(d)
+        s[..., i + 1:] = -np.inf
+        s = s - s.max(-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(-1, keepdims=True)
+        out[:, :, i] = np.einsum("bhj,bhjd->bhd", p, Vt)
+    return out.transpose(0, 2, 1, 3).reshape(B, T, D) @ np.asarray(W["out.weight"], np.float64).T

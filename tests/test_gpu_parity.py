@@ -1,0 +1,238 @@
+"""GPU parity of the HIP path against the CPU oracle and the golden fixtures.
+
+Tolerances (written in each test):
+  fp32 path   -- end to end <= 1e-5 max-abs against the reference fp32
+                 forward at config 1; stage outputs within fp32 rounding.
+  bf16 path   -- the inputs the oracle sees are the bf16-rounded x and weights;
+                 the kernel path additionally rounds q/k/v (projection output),
+                 the transported qh/kh/vh, the softmax weights (PV MFMA operand)
+                 and o (out-projection operand) to bf16. Each of these alone
+                 moves y by up to ~7e-3 where |o| ~ 3.5 (the first positions,
+                 which attend to one or two keys), so the bound is
+                 max-abs <= 2.5e-2, rms <= 1e-3 and relative Frobenius <= 1e-2.
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from holonomyawareattention_amd import kernels
+from oracle import holo_ref as R
+from tests._util import layer, make_module, run_module, round_to
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _unpack_vh(vh_t, T, d):
+    B, H, nch, Dp, C = vh_t.shape
+    return vh_t.permute(0, 1, 2, 4, 3).reshape(B, H, nch * C, Dp)[:, :, :T, :d]
+
+
+def _projections(x, W, H, dtype):
+    """GPU projections as the module computes them (additive; fp32 generator)."""
+    B, T, D = x.shape
+    d = D // H
+    m = 3 * (d // 3)
+    xt = torch.as_tensor(x).to(DEV, dtype)
+    qkv = torch.nn.functional.linear(xt, torch.as_tensor(W["qkv.weight"]).to(DEV, dtype)).view(B, T, H, 3 * d)
+    wg = torch.cat([torch.as_tensor(W[k]) for k in ("gqproj.weight", "gkproj.weight")]).to(DEV, dtype)
+    g = torch.mm(xt.reshape(B * T, D), wg.t(), out_dtype=torch.float32).view(B, T, 2 * H * m)
+    gq = g[..., :H * m].view(B, T, H, m)
+    gk = g[..., H * m:].view(B, T, H, m)
+    return qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], gq, gk
+
+
+def _scan_oracle(k, v, gq, gk, es):
+    """fp64 oracle of the scan stage on the exact values the kernel read."""
+    kk, vv, q_, k_ = (_np(t).transpose(0, 2, 1, 3) for t in (k, v, gq, gk))
+    a = (q_ + np.roll(k_, -1, axis=2)) * es
+    P, Hol = R.geometry_blocks(a)
+    return P, Hol, R.apply_blocks_T(P, kk), R.apply_blocks_T(P, vv)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,T,D,H,es", [(2, 150, 96, 2, 0.5), (1, 1, 48, 4, 1.5), (1, 65, 32, 2, 1.5),
+                                        (2, 64, 36, 3, 0.05)])
+def test_scan_stage(dtype, B, T, D, H, es):
+    x, W = layer(21, B, T, D, H, dtype=dtype)
+    d = D // H
+    q, k, v, gq, gk = _projections(x, W, H, dtype)
+    kh, vh_t, P, hol = kernels.geom_scan(k, v, gq, gk, es, want_hol=True)
+    torch.cuda.synchronize()
+    Pr, Holr, khr, vhr = _scan_oracle(k, v, gq, gk, es)
+    Pd = _np(kernels.quat_to_dense(P, d))
+    Hd = _np(kernels.quat_to_dense(hol, d))
+    tolP = 2e-5 if dtype == torch.float32 else 1e-4      # bf16 inputs, fp32 composition
+    assert np.abs(Pd - R.blocks_to_dense(Pr, d)).max() < tolP
+    assert np.abs(Hd - R.blocks_to_dense(Holr, d)).max() < tolP
+    Dp = kernels.padded_head_dim(d)
+    khg = _np(kh)
+    vhg = _np(_unpack_vh(vh_t, T, Dp))
+    assert np.all(khg[:, :, T:] == 0) and np.all(khg[..., d:] == 0)   # padding is zero
+    assert np.all(vhg[..., d:] == 0)
+    scale_k = np.abs(khr).max() + 1e-6
+    if dtype == torch.float32:
+        tol_k, tol_v = 2e-5 * scale_k, 2e-5 * (np.abs(vhr).max() + 1e-6)
+        assert np.abs(khg[:, :, :T, :d] - khr).max() < tol_k
+        assert np.abs(vhg[..., :d] - vhr).max() < tol_v
+    else:   # one bf16 rounding of the transported value: |err| <= 2^-8 |ref| + composition error
+        for got, ref in ((khg[:, :, :T, :d], khr), (vhg[..., :d], vhr)):
+            assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,T,D,H", [(2, 300, 192, 2), (1, 129, 96, 2), (1, 7, 48, 4), (2, 200, 64, 2)])
+def test_attention_stage(dtype, B, T, D, H):
+    es = 0.5
+    x, W = layer(22, B, T, D, H, dtype=dtype)
+    d = D // H
+    q, k, v, gq, gk = _projections(x, W, H, dtype)
+    kh, vh_t, P, _ = kernels.geom_scan(k, v, gq, gk, es)
+    o = kernels.attention(q, kh, vh_t, P, 1.0 / math.sqrt(d))
+    torch.cuda.synchronize()
+    # oracle on the exact kh/vh/P the kernel consumed
+    Pb = _np(kernels.quat_to_dense(P, d))                      # (B,H,T,d,d)
+    khr = _np(kh)[:, :, :T, :d]
+    vhr = _np(_unpack_vh(vh_t, T, d))
+    qq = _np(q).transpose(0, 2, 1, 3)
+    qh = np.einsum("bhtij,bhti->bhtj", Pb, qq)
+    if dtype == torch.bfloat16:
+        qh = round_to(qh, torch.bfloat16)
+    oh = R.causal_attention64(qh, khr, vhr, 1.0 / math.sqrt(d))
+    o_ref = np.einsum("bhtij,bhtj->bhti", Pb, oh).transpose(0, 2, 1, 3)
+    got = _np(o)
+    err = np.abs(got - o_ref)
+    if dtype == torch.float32:
+        assert err.max() < 1e-5 * max(1.0, np.abs(o_ref).max())
+    else:   # softmax weights rounded to bf16 for the PV MFMA and o stored in bf16
+        assert err.max() < 2e-2
+        assert np.sqrt((err ** 2).mean()) < 1e-2 * np.sqrt((o_ref ** 2).mean())
+
+
+GOLDEN_CASES = ["tiny_additive_es005_f64", "tiny_additive_es15_f64", "tiny_interaction_es15_f64",
+                "leftover_d16_es15_f64"]
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+def test_golden_fixture_fp32(golden_dir, name):
+    """fp32 path against the reference's own outputs (fp64 run of
+    core/attention_fast_chunked.py on the same inputs)."""
+    z = np.load(os.path.join(golden_dir, name + ".npz"))
+    seed, B, T, D, H = (int(v) for v in z["meta"])
+    es, lm = float(z["edge_scale"]), str(z["link_mode"])
+    W = {k[2:]: round_to(z[k], torch.float32) for k in z.files if k.startswith("w:")}
+    x = round_to(z["x"], torch.float32)
+    m = make_module(W, D, H, es, lm, torch.float32, DEV)
+    y, g = run_module(m, x, DEV, torch.float32, return_geometry=True)
+    # the fixture was computed from the unrounded fp64 inputs: the fp64 oracle on
+    # the rounded inputs bounds the input-rounding part of the difference
+    y_in = R.forward_blocks(x, W, H, es, lm)
+    assert np.abs(y_in - z["y"]).max() < 2e-5
+    assert np.abs(_np(y) - y_in).max() < 1e-5
+    assert np.abs(_np(y) - z["y"]).max() < 3e-5
+    assert np.abs(_np(g["C"]) - z["P"]).max() < 1e-5
+    assert np.abs(_np(g["H"]) - z["Hol"]).max() < 1e-5
+
+
+def test_cfg1_fp32_against_reference(golden_dir):
+    """BASELINE config 1 (B=8 T=128 D=192 H=4, fp32, edge_scale 0.05): the
+    reference fp32 forward, max-abs <= 1e-5."""
+    z32 = np.load(os.path.join(golden_dir, "cfg1_additive_f32.npz"))
+    z64 = np.load(os.path.join(golden_dir, "cfg1_additive_f64.npz"))
+    seed, B, T, D, H = (int(v) for v in z32["meta"])
+    x, W = layer(seed, B, T, D, H, dtype=torch.float32)
+    xs = z32["x_checksum"]
+    assert abs(round_to(x, torch.float64).sum() - xs[0]) < 1e-6 * abs(xs[1])   # same synthetic inputs
+    m = make_module(W, D, H, 0.05, "additive", torch.float32, DEV)
+    y, _ = run_module(m, x, DEV, torch.float32)
+    yn = _np(y)
+    rows = z32["y_rows"].shape[0]
+    assert np.abs(yn[:rows] - z32["y_rows"]).max() <= 1e-5
+    assert np.abs(yn[:rows] - z64["y_rows"]).max() <= 1e-5
+    assert np.abs(yn.sum(-1) - z32["y_row_sum"]).max() <= 1e-5 * D
+    assert np.abs(np.abs(yn).sum(-1) - z32["y_row_abs"]).max() <= 1e-5 * D
+    y64 = R.forward_blocks(x, W, H, 0.05)
+    assert np.abs(yn - y64).max() <= 1e-5
+
+
+def test_cfg2_bf16_slice_against_oracle():
+    """BASELINE config 2 at full size (B=16 T=2048 H=16 d=96, bf16); batch rows
+    0 and 9 are checked against the fp64 oracle on the same bf16 inputs."""
+    B, T, D, H, es = 16, 2048, 1536, 16, 0.05
+    x, W = layer(2, B, T, D, H, dtype=torch.bfloat16)
+    m = make_module(W, D, H, es, "additive", torch.bfloat16, DEV)
+    y, _ = run_module(m, x, DEV, torch.bfloat16)
+    yn = _np(y)
+    assert np.isfinite(yn).all()
+    for b in (0, 9):
+        y_ref = R.forward_blocks(x[b:b + 1], W, H, es)[0]
+        err = np.abs(yn[b] - y_ref)
+        print(f"cfg2 b={b}: max {err.max():.3e} rms {np.sqrt((err**2).mean()):.3e}")
+        assert err.max() <= 2.5e-2
+        assert np.sqrt((err ** 2).mean()) <= 1e-3
+        assert np.linalg.norm(yn[b] - y_ref) <= 1e-2 * np.linalg.norm(y_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,T,D,H,lm", [(2, 1, 48, 4, "additive"), (1, 2, 48, 4, "additive"),
+                                        (3, 63, 96, 2, "additive"), (1, 64, 96, 1, "additive"),
+                                        (2, 65, 96, 2, "interaction"), (1, 257, 192, 2, "interaction"),
+                                        (2, 40, 64, 4, "additive")])
+def test_end_to_end_shapes(dtype, B, T, D, H, lm):
+    es = 0.7
+    x, W = layer(23, B, T, D, H, lm, dtype=dtype)
+    m = make_module(W, D, H, es, lm, dtype, DEV)
+    y, _ = run_module(m, x, DEV, dtype)
+    y_ref = R.forward_blocks(x, W, H, es, lm)
+    err = np.abs(_np(y) - y_ref)
+    if dtype == torch.float32:
+        assert err.max() < 2e-5
+    else:
+        assert err.max() < 2.5e-2 * max(1.0, np.abs(y_ref).max() / 4)
+
+
+def test_causal_prefix_consistency():
+    """y_t depends on x_0..x_t only: changing x after s leaves y[:, :s] bit-identical."""
+    B, T, D, H, s = 2, 700, 192, 2, 333
+    x, W = layer(24, B, T, D, H, dtype=torch.bfloat16)
+    m = make_module(W, D, H, 0.3, "additive", torch.bfloat16, DEV)
+    y1, _ = run_module(m, x, DEV, torch.bfloat16)
+    x2 = x.copy()
+    x2[:, s:] = round_to(x2[:, s:] * -1.7 + 0.3, torch.bfloat16)
+    y2, _ = run_module(m, x2, DEV, torch.bfloat16)
+    assert torch.equal(y1[:, :s], y2[:, :s])
+    assert not torch.equal(y1[:, s:], y2[:, s:])
+
+
+def test_flat_connection_is_causal_sdpa():
+    """edge_scale = 0 makes every rotation the identity (PDF Theorem 1): the
+    layer reduces to plain causal softmax attention."""
+    B, T, D, H = 2, 190, 96, 2
+    x, W = layer(25, B, T, D, H, dtype=torch.float32)
+    m = make_module(W, D, H, 0.0, "additive", torch.float32, DEV)
+    y, _ = run_module(m, x, DEV, torch.float32)
+    xt = torch.as_tensor(x)
+    d = D // H
+    qkv = (xt @ torch.as_tensor(W["qkv.weight"]).T).view(B, T, H, 3 * d).transpose(1, 2)
+    q, k, v = qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:]
+    o = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
+    y_ref = o.transpose(1, 2).reshape(B, T, D) @ torch.as_tensor(W["out.weight"]).T
+    assert np.abs(_np(y) - y_ref.numpy()).max() < 1e-5
+
+
+def test_deterministic():
+    B, T, D, H = 2, 333, 192, 2
+    x, W = layer(26, B, T, D, H, dtype=torch.bfloat16)
+    m = make_module(W, D, H, 0.3, "additive", torch.bfloat16, DEV)
+    y1, _ = run_module(m, x, DEV, torch.bfloat16)
+    y2, _ = run_module(m, x, DEV, torch.bfloat16)
+    assert torch.equal(y1, y2)
