@@ -42,10 +42,10 @@ CONFIGS = {
 
 def scan_bytes_per_token_head(d: int, io_bytes: int, gen_bytes: int = 4) -> int:
     """Algorithmic HBM bytes of the scan stage per (token, head): read the two
-    generator halves gq, gk (3*nb each, fp32) and k, v (d each); write kh, vh
-    (d each) and P (nb quaternions, fp32)."""
+    generator halves gq, gk (3*nb each, fp32) and q, k, v (d each); write qh,
+    kh, vh (d each) and P (nb quaternions, fp32)."""
     nb = d // 3
-    return 2 * 3 * nb * gen_bytes + 2 * d * io_bytes + 2 * d * io_bytes + nb * 16
+    return 2 * 3 * nb * gen_bytes + 3 * d * io_bytes + 3 * d * io_bytes + nb * 16
 
 
 def attention_core_flops(B, T, H, d) -> float:
@@ -127,10 +127,10 @@ def main():
         q, k, v, gq, gk = m._link_inputs(x)
         if ev is not None:
             ev[1].record()
-        kh, vh_t, P, _ = kernels.geom_scan(k, v, gq, gk, m.edge_scale)
+        qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, m.edge_scale)
         if ev is not None:
             ev[2].record()
-        o = kernels.attention(q, kh, vh_t, P, m.scale)
+        o = kernels.attention(qh, kh, vh_t, P, d, m.scale)
         if ev is not None:
             ev[3].record()
         y = F.linear(o.view(B, T, D), m.out.weight)

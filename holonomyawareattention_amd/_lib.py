@@ -38,9 +38,9 @@ SIGNATURES = [
     ("holo_padded_seq_len", _L, [_L]),
     ("holo_geom_scan_workspace_size", _S, [_I, _L, _I, _I]),
     ("holo_geom_scan_fwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I,
-                                _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L,
-                                _P, _P, _P, _P, _P, _S, _P]),
-    ("holo_attn_fwd", _I, [_I, _L, _I, _I, _I, _F, _P, _L, _L, _P, _P, _P, _P, _L, _L, _P]),
+                                _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L,
+                                _P, _P, _P, _P, _P, _P, _S, _P]),
+    ("holo_attn_fwd", _I, [_I, _L, _I, _I, _I, _F, _P, _P, _P, _P, _P, _L, _L, _P]),
     ("holo_quat_to_dense", _I, [_L, _I, _P, _P, _P]),
 ]
 

@@ -175,9 +175,9 @@ class PathOrderedGeometricMHA(nn.Module):
         track = torch.is_grad_enabled() and (x.requires_grad or bool(params))
         with torch.no_grad():
             q, k, v, gq, gk = self._link_inputs(x)
-            kh, vh_t, P, hol = kernels.geom_scan(k, v, gq, gk, self.edge_scale,
-                                                 want_hol=return_geometry)
-            o = kernels.attention(q, kh, vh_t, P, self.scale)
+            qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
+                                                     want_hol=return_geometry)
+            o = kernels.attention(qh, kh, vh_t, P, self.d, self.scale)
             y = F.linear(o.view(B, L, D), self.out.weight)
         if track:
             y = _ForwardOnly.apply(y, x, *params)

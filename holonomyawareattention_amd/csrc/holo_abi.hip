@@ -43,7 +43,7 @@ int check_common(int B, int64_t T, int H, int d) {
                 B, (long long)T, H, d);
   if (d > kMaxHeadDim)
     return fail(HOLO_ERR_UNSUPPORTED, "head dimension %d above the supported maximum %d", d, kMaxHeadDim);
-  if ((int64_t)B * H > 0x7fffffff || T > ((int64_t)1 << 31))
+  if ((int64_t)B * H * ((T + 127) / 128) > 0x7fffffff || T > ((int64_t)1 << 31))
     return fail(HOLO_ERR_UNSUPPORTED, "B*H or T too large");
   return HOLO_OK;
 }
@@ -54,7 +54,7 @@ extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (1 << 16) | 0; }
+int holo_abi_version(void) { return (2 << 16) | 0; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -70,9 +70,10 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
                        int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
                        const void* gq, int64_t gq_rs, int64_t gq_hs,
                        const void* gk, int64_t gk_rs, int64_t gk_hs,
+                       const void* q, int64_t q_rs, int64_t q_hs,
                        const void* k, int64_t k_rs, int64_t k_hs,
                        const void* v, int64_t v_rs, int64_t v_hs,
-                       void* kh, void* vh_t, float* P, float* hol,
+                       void* qh, void* kh, void* vh_t, float* P, float* hol,
                        void* workspace, size_t workspace_bytes, void* stream) {
   g_last_error.clear();
   int rc = check_common(B, T, H, d);
@@ -86,7 +87,7 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
   if (gen_mode != HOLO_GEN_ADDITIVE && gen_mode != HOLO_GEN_DIRECT)
     return fail(HOLO_ERR_INVALID_ARG, "gen_mode %d unknown", gen_mode);
   const int nb = d / 3;
-  if (!gq || !k || !v || !kh || !vh_t || (nb > 0 && !P))
+  if (!gq || !q || !k || !v || !qh || !kh || !vh_t || (nb > 0 && !P))
     return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
   if (gen_mode == HOLO_GEN_ADDITIVE && !gk)
     return fail(HOLO_ERR_INVALID_ARG, "additive generator needs gk");
@@ -96,10 +97,11 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
     if ((rc = check_layout("gq", gq_rs, gq_hs, H, 3 * nb))) return rc;
     if (gk && (rc = check_layout("gk", gk_rs, gk_hs, H, 3 * nb))) return rc;
   }
+  if ((rc = check_layout("q", q_rs, q_hs, H, d))) return rc;
   if ((rc = check_layout("k", k_rs, k_hs, H, d))) return rc;
   if ((rc = check_layout("v", v_rs, v_hs, H, d))) return rc;
-  if (!aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)) || (hol && !aligned16(hol)))
-    return fail(HOLO_ERR_INVALID_ARG, "kh, vh_t, P and hol must be 16-byte aligned");
+  if (!aligned16(qh) || !aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)) || (hol && !aligned16(hol)))
+    return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t, P and hol must be 16-byte aligned");
   size_t need = holo_geom_scan_workspace_size(B, T, H, d);
   if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
     return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
@@ -112,9 +114,19 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
   a.edge_scale = edge_scale;
   a.gq = gq; a.gq_rs = gq_rs; a.gq_hs = gq_hs;
   a.gk = gk; a.gk_rs = gk_rs; a.gk_hs = gk_hs;
+  a.q = q; a.q_rs = q_rs; a.q_hs = q_hs;
   a.k = k; a.k_rs = k_rs; a.k_hs = k_hs;
   a.v = v; a.v_rs = v_rs; a.v_hs = v_hs;
-  a.kh = kh; a.vh_t = vh_t; a.P = P; a.hol = hol;
+  a.qh = qh; a.kh = kh; a.vh_t = vh_t; a.P = P; a.hol = hol;
+  {
+    // 16-byte vector rows: every row start of gq/gk/k/v must be 16-byte aligned
+    const size_t ge = gen_dtype == HOLO_F32 ? 4 : 2, ie = io_dtype == HOLO_F32 ? 4 : 2;
+    auto al = [](const void* p, int64_t rs, int64_t hs, size_t es) {
+      return p == nullptr || (aligned16(p) && (rs * (int64_t)es) % 16 == 0 && (hs * (int64_t)es) % 16 == 0);
+    };
+    a.wide = (d == 48 || d == 72 || d == 96) && al(gq, gq_rs, gq_hs, ge) && al(gk, gk_rs, gk_hs, ge) &&
+             al(q, q_rs, q_hs, ie) && al(k, k_rs, k_hs, ie) && al(v, v_rs, v_hs, ie);
+  }
   a.totals = static_cast<float*>(workspace);
   a.carry = a.totals ? a.totals + (size_t)B * H * a.nch * nb * 4 : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -126,8 +138,7 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
 }
 
 int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
-                  const void* q, int64_t q_rs, int64_t q_hs,
-                  const void* kh, const void* vh_t, const float* P,
+                  const void* qh, const void* kh, const void* vh_t, const float* P,
                   void* o, int64_t o_rs, int64_t o_hs, void* stream) {
   g_last_error.clear();
   int rc = check_common(B, T, H, d);
@@ -135,12 +146,11 @@ int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
   if (dtype != HOLO_F32 && dtype != HOLO_BF16)
     return fail(HOLO_ERR_INVALID_ARG, "dtype %d is not HOLO_F32 or HOLO_BF16", dtype);
   const int nb = d / 3;
-  if (!q || !kh || !vh_t || !o || (nb > 0 && !P))
+  if (!qh || !kh || !vh_t || !o || (nb > 0 && !P))
     return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
-  if ((rc = check_layout("q", q_rs, q_hs, H, d))) return rc;
   if ((rc = check_layout("o", o_rs, o_hs, H, d))) return rc;
-  if (!aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)))
-    return fail(HOLO_ERR_INVALID_ARG, "kh, vh_t and P must be 16-byte aligned");
+  if (!aligned16(qh) || !aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)))
+    return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t and P must be 16-byte aligned");
   if (!(scale > 0.f) || !(scale < 1e30f))
     return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
 
@@ -148,8 +158,7 @@ int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
   a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d);
   a.T = T; a.Tp = holo::padded_seq(T); a.nch = a.Tp / holo::kChunk;
   a.scale_log2 = scale * 1.4426950408889634f;
-  a.q = q; a.q_rs = q_rs; a.q_hs = q_hs;
-  a.kh = kh; a.vh_t = vh_t; a.P = P;
+  a.qh = qh; a.kh = kh; a.vh_t = vh_t; a.P = P;
   a.o = o; a.o_rs = o_rs; a.o_hs = o_hs;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = dtype == HOLO_F32 ? holo::launch_attn<float>(a, s)

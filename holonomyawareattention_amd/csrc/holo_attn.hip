@@ -19,9 +19,9 @@
 // (l ^ 32) the other 32: the row max and the rescale of the accumulator are
 // per-lane operations plus one cross-lane exchange, and the exponentiated
 // scores are already in the register layout of the P^T operand.
-// The query transport (prologue) and the back-rotation (epilogue) are fused:
-// the workgroup stages its 128 query rows through LDS, rotating each 3-dim
-// block by its stored quaternion.
+// The queries arrive already transported (qh from the scan); the back-rotation
+// o_i = P_i oh_i is fused into the epilogue, which stages the tile's outputs
+// through LDS and rotates each 3-dim block by its stored quaternion.
 #include <type_traits>
 
 #include "holo_kernels.h"
@@ -32,200 +32,294 @@ constexpr int kBM = 128;                  // queries per workgroup
 constexpr int kBN = 64;                   // keys per tile
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+// Running-max threshold (log2 units): the accumulator is rescaled only when a
+// query's max grows by more than this, so exponentiated scores stay <= 2^8.
+// Numerator and denominator use the same stale max, so the result is exact.
+constexpr float kRescaleThreshold = 8.f;
 
 template <typename T, int DP> struct AttnCfg {
   static constexpr int E = 16 / sizeof(T);             // elements per 16 B
-  static constexpr int KS = DP + E;                     // padded LDS row strides
-  static constexpr int VS = kBN + E;
-  static constexpr int QS = DP + E;
+  // LDS row strides chosen so the MFMA operand reads hit distinct banks:
+  // K rows (16 B per lane, 32 rows) at 52 dwords, V^T rows (8 B per lane,
+  // 32 rows) at 34 dwords for bf16.
+  static constexpr int KS = DP + E;
+  static constexpr int VS = kBN + 4;
   static constexpr int OS = DP + 4;                     // fp32 staging
   static constexpr int NBX = (DP + 2) / 3;              // 3-dim groups covering DP
-  static constexpr size_t kv_bytes = (size_t)(kBN * KS + DP * VS) * sizeof(T);
-  static constexpr size_t q_bytes = (size_t)kBM * QS * sizeof(T);
+  static constexpr int KCH = kBN * DP / E / kThreads;   // 16 B chunks per thread per tile
+  static constexpr int VCH = DP * kBN / E / kThreads;
+  static constexpr int kStage = kBN * KS + DP * VS;     // elements of one K + V^T stage
+  static constexpr int kStages = 3;
+  static constexpr size_t kv_bytes = (size_t)kStages * kStage * sizeof(T);
   static constexpr size_t o_bytes = (size_t)kBM * OS * sizeof(float);
-  static constexpr size_t lds = kv_bytes > q_bytes ? (kv_bytes > o_bytes ? kv_bytes : o_bytes)
-                                                   : (q_bytes > o_bytes ? q_bytes : o_bytes);
+  static constexpr size_t lds = kv_bytes > o_bytes ? kv_bytes : o_bytes;
+  static constexpr int NG8 = (NBX + 7) / 8;             // epilogue items per row (8 groups each)
+  static constexpr int EPI = (kBM * NG8 + kThreads - 1) / kThreads;   // items per thread
+  static_assert(KCH * E * kThreads == kBN * DP, "K tile must split evenly over the threads");
+  static_assert(VCH * E * kThreads == kBN * DP, "V tile must split evenly over the threads");
+  static_assert((kStage * sizeof(T)) % 16 == 0, "stages must stay 16-byte aligned");
 };
 
+// Pipeline over key tiles j = 0, 1, ...: three LDS stages hold tiles j, j+1
+// and j+2; registers hold tile j+3 in flight. Iteration j issues the QK MFMAs
+// of tile j+1, then runs the softmax and PV MFMAs of tile j (so the VALU work
+// overlaps the matrix core), stores tile j+2 into the free stage, issues the
+// loads of tile j+3 and ends with the tile's only barrier.
 template <typename T, int DP>
-__global__ void __launch_bounds__(kThreads) attn_fwd(AttnArgs a) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+attn_fwd(AttnArgs a) {
   using C = AttnCfg<T, DP>;
   extern __shared__ __align__(16) unsigned char smem[];
-  T* Ks = reinterpret_cast<T*>(smem);
-  T* Vs = Ks + kBN * C::KS;
-  T* Qs = reinterpret_cast<T*>(smem);
-  float* Os = reinterpret_cast<float*>(smem);
+  T* const kv = reinterpret_cast<T*>(smem);
+  float* const Os = reinterpret_cast<float*>(smem);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
   const int lr = lane & 31;               // query column of this lane (MFMA col)
   const int g = lane >> 5;                // lane half
-  const int bh = blockIdx.x;
-  const int b = bh / a.H, h = bh % a.H;
-  const int64_t ntile = (a.T + kBM - 1) / kBM;
-  const int64_t q0 = (ntile - 1 - blockIdx.y) * kBM;   // longest tiles first
-  const int64_t qw = q0 + 32 * w;                       // first query of this wave
-  const int64_t qi = qw + lr;                           // this lane's query
-
-  // ---- prologue: qh = P^T q for the tile's rows, staged in LDS ----
-  for (int idx = tid; idx < kBM * C::NBX; idx += kThreads) {
-    int r = idx / C::NBX, blk = idx % C::NBX, c0 = 3 * blk;
-    int64_t t = q0 + r;
-    float u[3] = {0.f, 0.f, 0.f};
-    if (t < a.T) {
-      const T* qr = reinterpret_cast<const T*>(a.q) + (b * a.T + t) * a.q_rs + h * a.q_hs + c0;
-      for (int j = 0; j < 3; ++j)
-        if (c0 + j < a.d) u[j] = to_f32(qr[j]);
-      if (blk < a.nb) {
-        rot3 R = qmat(load_quat(a.P + ((bh * a.T + t) * a.nb + blk) * 4));
-        float y0, y1, y2;
-        rot_t_apply(R, u[0], u[1], u[2], y0, y1, y2);
-        u[0] = y0; u[1] = y1; u[2] = y2;
-      }
-    }
-    for (int j = 0; j < 3; ++j)
-      if (c0 + j < DP) Qs[r * C::QS + c0 + j] = from_f32<T>(u[j]);
+  // Workgroup L runs on XCD L % 8. When B*H is a multiple of 8, XCD x takes the
+  // (b, h) pairs congruent to x and runs the query tiles of one pair back to
+  // back (longest first), so a pair's keys/values stay in that XCD's L2.
+  const int ntile = (int)((a.T + kBM - 1) / kBM);
+  const int L = blockIdx.x;
+  int bh, qt;
+  if ((a.B * a.H) % 8 == 0) {
+    const int j = L >> 3;
+    bh = 8 * (j / ntile) + (L & 7);
+    qt = ntile - 1 - j % ntile;
+  } else {
+    bh = L % (a.B * a.H);
+    qt = ntile - 1 - L / (a.B * a.H);
   }
-  __syncthreads();
+  const int b = bh / a.H, h = bh % a.H;
+  const int64_t q0 = (int64_t)qt * kBM;
+  const int64_t qw = q0 + 32 * w;                       // first query of this wave
 
+  // ---- Q^T operand straight from qh (the scan's transported queries) ----
   constexpr bool kBF = sizeof(T) == 2;
   constexpr int QF = kBF ? DP / 16 : DP / 2;            // Q^T operand steps
   typedef typename std::conditional<kBF, bf16x8, float>::type qfrag_t;
   qfrag_t qf[QF];
-  for (int s = 0; s < QF; ++s) {
-    if constexpr (kBF) qf[s] = *reinterpret_cast<const bf16x8*>(&Qs[(32 * w + lr) * C::QS + 16 * s + 8 * g]);
-    else qf[s] = Qs[(32 * w + lr) * C::QS + 2 * s + g];
+  {
+    const int64_t qrow_t = qw + lr;                     // rows past Tp read as zero
+    const T* qrow = reinterpret_cast<const T*>(a.qh) + ((int64_t)bh * a.Tp + qrow_t) * DP;
+    const bool in = qrow_t < a.Tp;
+    static_for<QF>([&](auto s) {
+      if constexpr (kBF) qf[s] = in ? *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * g) : bf16x8{};
+      else qf[s] = in ? qrow[2 * s + g] : 0.f;
+    });
   }
-  __syncthreads();
 
   f32x16 O[DP / 32];
-  for (int i = 0; i < DP / 32; ++i) O[i] = f32x16{};
+  static_for<DP / 32>([&](auto i) { O[i] = f32x16{}; });
   float m_run = -1e30f, l_run = 0.f;
+  const float c = a.scale_log2;
 
   int64_t kend = q0 + kBM; if (kend > a.T) kend = a.T;
   const int nkv = (int)((kend + kBN - 1) / kBN);
-  const T* kbase = reinterpret_cast<const T*>(a.kh) + (int64_t)bh * a.Tp * DP;
-  const T* vbase = reinterpret_cast<const T*>(a.vh_t) + (int64_t)bh * a.nch * DP * kBN;
+  // tiles this wave attends to: keys up to its last query (0 when past T)
+  const int nact = qw >= a.T ? 0 : (int)((qw + 31) / kBN) + 1 < nkv ? (int)((qw + 31) / kBN) + 1 : nkv;
+  const u32x4* kbase = reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.kh) + (int64_t)bh * a.Tp * DP);
+  const u32x4* vbase = reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.vh_t) + (int64_t)bh * a.nch * DP * kBN);
+  constexpr int TCH = kBN * DP / C::E;                  // 16 B chunks per tile
+  constexpr int RC = DP / C::E, VC = kBN / C::E;        // chunks per K row / V^T row
 
-  for (int kt = 0; kt < nkv; ++kt) {
+  u32x4 kreg[C::KCH], vreg[C::VCH];
+  auto load_tile = [&](int kt) {
+    const u32x4* kn = kbase + (int64_t)kt * TCH;
+    const u32x4* vn = vbase + (int64_t)kt * TCH;
+    static_for<C::KCH>([&](auto j) { kreg[j] = kn[tid + j * kThreads]; });
+    static_for<C::VCH>([&](auto j) { vreg[j] = vn[tid + j * kThreads]; });
+  };
+  auto store_tile = [&](int st) {
+    T* Ks = kv + st * C::kStage;
+    T* Vs = Ks + kBN * C::KS;
+    static_for<C::KCH>([&](auto j) {
+      int i = tid + j * kThreads, r = i / RC, cc = i % RC;
+      *reinterpret_cast<u32x4*>(&Ks[r * C::KS + cc * C::E]) = kreg[j];
+    });
+    static_for<C::VCH>([&](auto j) {
+      int i = tid + j * kThreads, r = i / VC, cc = i % VC;
+      u32x2* dst = reinterpret_cast<u32x2*>(&Vs[r * C::VS + cc * C::E]);
+      dst[0] = vreg[j].xy;
+      dst[1] = vreg[j].zw;
+    });
+  };
+  // S^T (64 keys x 32 queries) of the tile in stage st
+  auto qk = [&](int st, f32x16 (&S)[2]) {
+    const T* Ks = kv + st * C::kStage;
+    S[0] = f32x16{}; S[1] = f32x16{};
+    static_for<QF>([&](auto s) {
+      static_for<2>([&](auto kb) {
+        if constexpr (kBF) {
+          bf16x8 av = *reinterpret_cast<const bf16x8*>(&Ks[(32 * kb + lr) * C::KS + 16 * s + 8 * g]);
+          S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qf[s], S[kb], 0, 0, 0);
+        } else {
+          float av = Ks[(32 * kb + lr) * C::KS + 2 * s + g];
+          S[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, qf[s], S[kb], 0, 0, 0);
+        }
+      });
+    });
+  };
+  // online softmax (log2 units, one lane pair per query) and O^T += V^T P^T
+  // of tile kt (stage st); the QK MFMAs of the next tile (stage stn, into Sn)
+  // are issued in the same basic block as the exponentials so the two overlap.
+  auto softmax_pv = [&](int kt, int st, f32x16 (&S)[2], int stn, f32x16 (&Sn)[2]) {
+    const T* Vs = kv + st * C::kStage + kBN * C::KS;
     const int64_t k0 = (int64_t)kt * kBN;
-    // ---- stage the key tile (row-major) and the value tile (transposed) ----
-    {
-      constexpr int RC = DP / C::E;                    // 16 B chunks per key row
-      const uint4* ksrc = reinterpret_cast<const uint4*>(kbase + k0 * DP);
-      for (int i = tid; i < kBN * RC; i += kThreads) {
-        int r = i / RC, cc = i % RC;
-        *reinterpret_cast<uint4*>(&Ks[r * C::KS + cc * C::E]) = ksrc[i];
-      }
-      constexpr int VC = kBN / C::E;                   // 16 B chunks per value row
-      const uint4* vsrc = reinterpret_cast<const uint4*>(vbase + (int64_t)kt * DP * kBN);
-      for (int i = tid; i < DP * VC; i += kThreads) {
-        int r = i / VC, cc = i % VC;
-        *reinterpret_cast<uint4*>(&Vs[r * C::VS + cc * C::E]) = vsrc[i];
-      }
+    if (k0 + kBN - 1 > qw) {             // tile reaches past this wave's first query
+      const int rel = (int)(qw - k0) + lr - 4 * g;     // key offset limit for this lane
+      static_for<2>([&](auto kb) {
+        static_for<16>([&](auto r) {
+          if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) S[kb][(int)r] = -INFINITY;
+        });
+      });
     }
-    __syncthreads();
-
-    if (qw + 31 >= k0 && qw < a.T) {
-      // ---- S^T = K Q^T ----
-      f32x16 S[2] = {f32x16{}, f32x16{}};
-      for (int kb = 0; kb < 2; ++kb) {
-        for (int s = 0; s < QF; ++s) {
-          if constexpr (kBF) {
-            bf16x8 av = *reinterpret_cast<const bf16x8*>(&Ks[(32 * kb + lr) * C::KS + 16 * s + 8 * g]);
-            S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qf[s], S[kb], 0, 0, 0);
-          } else {
-            float av = Ks[(32 * kb + lr) * C::KS + 2 * s + g];
-            S[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, qf[s], S[kb], 0, 0, 0);
-          }
-        }
-      }
-      // ---- online softmax (log2 domain), per lane = per query ----
-      const bool need_mask = (k0 + kBN - 1 > qw);
-      float mx = -INFINITY;
-      for (int kb = 0; kb < 2; ++kb)
-        for (int r = 0; r < 16; ++r) {
-          float s = S[kb][r] * a.scale_log2;
-          if (need_mask) {
-            int64_t key = k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key > qi) s = -INFINITY;
-          }
-          S[kb][r] = s;
-          mx = fmaxf(mx, s);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+    float mx = S[0][0];
+    static_for<2>([&](auto kb) { static_for<16>([&](auto r) { mx = fmaxf(mx, S[kb][(int)r]); }); });
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+    if (__any(mx > m_run + kRescaleThreshold)) {       // wave-uniform, rare after warm-up
       const float m_new = fmaxf(m_run, mx);
       const float corr = exp2f(m_run - m_new);
       m_run = m_new;
-      float ls = 0.f;
-      for (int kb = 0; kb < 2; ++kb)
-        for (int r = 0; r < 16; ++r) {
-          float p = exp2f(S[kb][r] - m_new);
-          S[kb][r] = p;
-          ls += p;
-        }
-      l_run = l_run * corr + ls;
-      for (int i = 0; i < DP / 32; ++i)
-        for (int r = 0; r < 16; ++r) O[i][r] *= corr;
-
-      // ---- O^T += V^T P^T ----
-      if constexpr (kBF) {
-        bf16x8 pb[2][2];
-        for (int kb = 0; kb < 2; ++kb)
-          for (int hh = 0; hh < 2; ++hh)
-            for (int e = 0; e < 8; ++e) pb[kb][hh][e] = (bf16)S[kb][8 * hh + e];
-        for (int db = 0; db < DP / 32; ++db)
-          for (int kb = 0; kb < 2; ++kb)
-            for (int hh = 0; hh < 2; ++hh) {
-              const T* vr = &Vs[(32 * db + lr) * C::VS + 32 * kb + 16 * hh + 4 * g];
-              bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
-              bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 8);
-              bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-              O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[kb][hh], O[db], 0, 0, 0);
-            }
-      } else {
-        for (int db = 0; db < DP / 32; ++db)
-          for (int kb = 0; kb < 2; ++kb)
-            for (int r = 0; r < 16; ++r) {
-              float av = Vs[(32 * db + lr) * C::VS + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3)];
-              O[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, S[kb][r], O[db], 0, 0, 0);
-            }
-      }
+      l_run *= corr;
+      static_for<DP / 32>([&](auto i) { O[i] *= corr; });
     }
+    const float nm = -m_run;
+    qk(stn, Sn);
+    static_for<2>([&](auto kb) {
+      static_for<16>([&](auto r) { S[kb][(int)r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][(int)r], c, nm)); });
+    });
+    if constexpr (kBF) {
+      // P^T operand in bf16; the row sum is taken over the same rounded
+      // values (two per v_dot2), so numerator and denominator agree.
+      bf16x8 pb[2][2];
+      static_for<2>([&](auto kb) {
+        static_for<2>([&](auto hh) {
+          static_for<8>([&](auto e) { pb[kb][hh][(int)e] = (bf16)S[kb][8 * hh + e]; });
+        });
+      });
+      float ls = 0.f;
+      const bf16x2 one2 = {(bf16)1.f, (bf16)1.f};
+      static_for<2>([&](auto kb) {
+        static_for<2>([&](auto hh) {
+          static_for<4>([&](auto e) {
+            bf16x2 pr = {pb[kb][hh][2 * e], pb[kb][hh][2 * e + 1]};
+            ls = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, ls, false);
+          });
+        });
+      });
+      l_run += ls;
+      static_for<2>([&](auto kb) {
+        static_for<2>([&](auto hh) {
+          static_for<DP / 32>([&](auto db) {          // independent accumulators back to back
+            const T* vr = &Vs[(32 * db + lr) * C::VS + 32 * kb + 16 * hh + 4 * g];
+            bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
+            bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 8);
+            bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[kb][hh], O[db], 0, 0, 0);
+          });
+        });
+      });
+    } else {
+      float ls = 0.f;
+      static_for<2>([&](auto kb) { static_for<16>([&](auto r) { ls += S[kb][(int)r]; }); });
+      l_run += ls;
+      static_for<2>([&](auto kb) {
+        static_for<16>([&](auto r) {
+          static_for<DP / 32>([&](auto db) {
+            float av = Vs[(32 * db + lr) * C::VS + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3)];
+            O[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, S[kb][(int)r], O[db], 0, 0, 0);
+          });
+        });
+      });
+    }
+  };
+  // one pipeline step: tile j in S, tile j+1 into Sn
+  auto step = [&](int j, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
+    // (the next tile's QK runs whenever this tile does; past the wave's last
+    // tile its result is never used)
+    if (j < nact) softmax_pv(j, j % 3, S, (j + 1) % 3, Sn);
+    if (j + 2 < nkv) store_tile((j + 2) % 3);
+    if (j + 3 < nkv) load_tile(j + 3);
     __syncthreads();
+  };
+
+  // ---- fill: tiles 0 and 1 into stages 0 and 1, tile 2 into registers ----
+  load_tile(0);
+  store_tile(0);
+  if (nkv > 1) { load_tile(1); store_tile(1); }
+  if (nkv > 2) load_tile(2);
+  __syncthreads();
+  f32x16 SA[2], SB[2];
+  if (nact > 0) qk(0, SA);
+  for (int j = 0; j < nkv; j += 2) {
+    step(j, SA, SB);
+    if (j + 1 < nkv) step(j + 1, SB, SA);
   }
 
   // ---- epilogue: normalise, stage O^T, back-rotate o = P oh, store ----
   float lt = l_run + __shfl_xor(l_run, 32);
-  const float inv = 1.f / fmaxf(lt, 1e-20f);
-  for (int db = 0; db < DP / 32; ++db)
-    for (int r = 0; r < 16; ++r)
-      Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][r] * inv;
+  const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
+  static_for<DP / 32>([&](auto db) {
+    static_for<16>([&](auto r) {
+      Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][(int)r] * inv;
+    });
+  });
   __syncthreads();
-  for (int idx = tid; idx < kBM * C::NBX; idx += kThreads) {
-    int r = idx / C::NBX, blk = idx % C::NBX, c0 = 3 * blk;
-    int64_t t = q0 + r;
-    if (t >= a.T || c0 >= a.d) continue;
-    float u[3];
-    for (int j = 0; j < 3; ++j) u[j] = (c0 + j < DP) ? Os[r * C::OS + c0 + j] : 0.f;
-    if (blk < a.nb) {
-      rot3 R = qmat(load_quat(a.P + ((bh * a.T + t) * a.nb + blk) * 4));
-      float y0, y1, y2;
-      rot_apply(R, u[0], u[1], u[2], y0, y1, y2);
-      u[0] = y0; u[1] = y1; u[2] = y2;
+  // item = (row, 8 consecutive 3-dim groups = 24 dims); all quaternion loads
+  // of the thread's items are issued before any of them is used
+  f32x4 pq[C::EPI][8];
+  static_for<C::EPI>([&](auto it) {
+    const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
+    const int64_t t = q0 + r;
+    static_for<8>([&](auto jb) {
+      const int blk = 8 * gi + jb;
+      pq[it][jb] = (idx < kBM * C::NG8 && t < a.T && blk < a.nb)
+                       ? *reinterpret_cast<const f32x4*>(a.P + ((bh * a.T + t) * a.nb + blk) * 4)
+                       : f32x4{1.f, 0.f, 0.f, 0.f};
+    });
+  });
+  static_for<C::EPI>([&](auto it) {
+    const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
+    const int64_t t = q0 + r;
+    if (idx >= kBM * C::NG8 || t >= a.T || 24 * gi >= a.d) return;
+    float u[24];
+    static_for<24>([&](auto j) { u[j] = (24 * gi + j < DP) ? Os[r * C::OS + 24 * gi + j] : 0.f; });
+    static_for<8>([&](auto jb) {
+      if (8 * gi + jb < a.nb) {
+        rot3 R = qmat(quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]});
+        float y0, y1, y2;
+        rot_apply(R, u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
+        u[3 * jb] = y0; u[3 * jb + 1] = y1; u[3 * jb + 2] = y2;
+      }
+    });
+    T* orow = reinterpret_cast<T*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs + 24 * gi;
+    if (24 * gi + 24 <= a.d && (reinterpret_cast<uintptr_t>(orow) & 15) == 0) {
+      constexpr int E = 16 / sizeof(T);
+      static_for<24 / E>([&](auto cc) {
+        u32x4 raw;
+        T* e = reinterpret_cast<T*>(&raw);
+        static_for<E>([&](auto j) { e[j] = from_f32<T>(u[cc * E + j]); });
+        reinterpret_cast<u32x4*>(orow)[cc] = raw;
+      });
+    } else {
+      static_for<24>([&](auto j) {
+        if (24 * gi + j < a.d) orow[j] = from_f32<T>(u[j]);
+      });
     }
-    T* orow = reinterpret_cast<T*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs + c0;
-    for (int j = 0; j < 3; ++j)
-      if (c0 + j < a.d) orow[j] = from_f32<T>(u[j]);
-  }
+  });
 }
 
 template <typename T, int DP>
 static hipError_t launch_attn_dp(const AttnArgs& a, hipStream_t s) {
   using C = AttnCfg<T, DP>;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&attn_fwd<T, DP>), hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::lds);
+  if (attr != hipSuccess) return attr;
   const int64_t ntile = (a.T + kBM - 1) / kBM;
-  hipLaunchKernelGGL((attn_fwd<T, DP>), dim3(a.B * a.H, (unsigned)ntile), dim3(kThreads),
+  hipLaunchKernelGGL((attn_fwd<T, DP>), dim3((unsigned)(a.B * a.H * ntile)), dim3(kThreads),
                      C::lds, s, a);
   return hipGetLastError();
 }
@@ -255,7 +349,10 @@ __global__ void __launch_bounds__(256) quat_to_dense(int64_t n, int d, int nb, c
   if (br < nb && bc < nb) {
     if (br == bc) {
       rot3 R = qmat(load_quat(q + (i * nb + br) * 4));
-      val = R.m[r - 3 * br][c - 3 * bc];
+      const int e = 3 * (r - 3 * br) + (c - 3 * bc);
+#pragma unroll
+      for (int k = 0; k < 9; ++k)
+        if (k == e) val = R.m[k / 3][k % 3];
     }
   } else if (r == c) {
     val = 1.f;

@@ -4,15 +4,34 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace holo {
 
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 16-byte and 8-byte raw moves: native vector types (HIP's uint4 is a union
+// struct that is not split into registers when copied as an aggregate).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kChunk = 64;   // scan chunk = key tile = padding granule of T
+
+// Compile-time loop: f(std::integral_constant<int, 0>{}) ... f(<N-1>{}), so that
+// register arrays indexed by the loop variable never become stack arrays.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_impl(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_impl<I + 1, N>(f);
+  }
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) { static_for_impl<0, N>(f); }
 
 __host__ __device__ inline int padded_head_dim(int d) { return (d + 31) / 32 * 32; }
 __host__ __device__ inline int64_t padded_seq(int64_t T) { return (T + kChunk - 1) / kChunk * kChunk; }
@@ -62,7 +81,7 @@ struct rot3 { float m[3][3]; };
 
 __device__ inline rot3 qmat(const quat& q) {
   float ww = q.w * q.w, xx = q.x * q.x, yy = q.y * q.y, zz = q.z * q.z;
-  float inv = 1.f / (ww + xx + yy + zz);
+  float inv = __builtin_amdgcn_rcpf(ww + xx + yy + zz);   // v_rcp_f32, 1 ulp
   float xy = q.x * q.y, xz = q.x * q.z, yz = q.y * q.z;
   float wx = q.w * q.x, wy = q.w * q.y, wz = q.w * q.z;
   rot3 r;

@@ -11,9 +11,11 @@ struct ScanArgs {
   float edge_scale;
   const void* gq; int64_t gq_rs, gq_hs;
   const void* gk; int64_t gk_rs, gk_hs;
+  const void* q; int64_t q_rs, q_hs;
   const void* k; int64_t k_rs, k_hs;
   const void* v; int64_t v_rs, v_hs;
-  void* kh; void* vh_t; float* P; float* hol;
+  void* qh; void* kh; void* vh_t; float* P; float* hol;
+  int wide;        // 16-byte row path of chunk_apply (d in {48, 72, 96}, aligned rows)
   float* totals;   // (B, H, nch, nb, 4) chunk totals
   float* carry;    // (B, H, nch, nb, 4) prefix product at each chunk start
 };
@@ -22,8 +24,7 @@ struct AttnArgs {
   int B, H, d, nb, Dp;
   int64_t T, Tp, nch;
   float scale_log2;                       // scale * log2(e)
-  const void* q; int64_t q_rs, q_hs;
-  const void* kh; const void* vh_t; const float* P;
+  const void* qh; const void* kh; const void* vh_t; const float* P;
   void* o; int64_t o_rs, o_hs;
 };
 

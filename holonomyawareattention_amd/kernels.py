@@ -1,7 +1,7 @@
 """Tensor-level wrappers of the C ABI (device memory and streams come from torch).
 
-``geom_scan``  -> holo_geom_scan_fwd : link rotations, prefix products, kh/vh
-``attention``  -> holo_attn_fwd      : q transport, causal attention, back-rotation
+``geom_scan``  -> holo_geom_scan_fwd : link rotations, prefix products, qh/kh/vh
+``attention``  -> holo_attn_fwd      : causal attention, back-rotation
 ``quat_to_dense`` -> holo_quat_to_dense
 
 Each wrapper checks devices, dtypes and strides on the host before the launch
@@ -53,13 +53,13 @@ def padded_seq_len(T: int) -> int:
     return int(_lib.load().holo_padded_seq_len(T))
 
 
-def geom_scan(k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor, gk: Optional[torch.Tensor],
-              edge_scale: float, want_hol: bool = False
-              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
-    """k, v: (B,T,H,d) views; gq, gk: (B,T,H,3*nb) views (gk None: gq is the
+def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor,
+              gk: Optional[torch.Tensor], edge_scale: float, want_hol: bool = False
+              ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """q, k, v: (B,T,H,d) views; gq, gk: (B,T,H,3*nb) views (gk None: gq is the
     full link parameter g and a_t = edge_scale * g_t). The generator may be
-    fp32 with bf16 k/v (link parameters are composed in fp32 either way).
-    Returns kh (B,H,Tp,Dp), vh_t (B,H,Tp/64,Dp,64), P (B,H,T,nb,4) fp32,
+    fp32 with bf16 q/k/v (link parameters are composed in fp32 either way).
+    Returns qh, kh (B,H,Tp,Dp), vh_t (B,H,Tp/64,Dp,64), P (B,H,T,nb,4) fp32,
     Hol (B,H,nb,4) fp32 or None."""
     lib = _lib.load()
     B, T, H, d = k.shape
@@ -70,19 +70,22 @@ def geom_scan(k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor, gk: Optional[t
     dt = k.dtype
     if dt not in _DT:
         raise ValueError(f"geom_scan: unsupported dtype {dt}")
-    if v.dtype != dt or v.device != dev:
-        raise ValueError(f"geom_scan: v must be {dt} on {dev}")
+    for name, t in (("q", q), ("v", v)):
+        if t.dtype != dt or t.device != dev:
+            raise ValueError(f"geom_scan: {name} must be {dt} on {dev}")
     gdt = gq.dtype
     if gdt not in _DT or (dt == torch.float32 and gdt != torch.float32):
         raise ValueError(f"geom_scan: generator dtype {gdt} with {dt} keys is not supported")
     for name, t in (("gq", gq), ("gk", gk)):
         if t is not None and (t.dtype != gdt or t.device != dev):
             raise ValueError(f"geom_scan: {name} must be {gdt} on {dev}")
+    q_rs, q_hs = _token_view(q, B, T, H, d, "q")
     k_rs, k_hs = _token_view(k, B, T, H, d, "k")
     v_rs, v_hs = _token_view(v, B, T, H, d, "v")
     gq_rs, gq_hs = _token_view(gq, B, T, H, 3 * nb, "gq")
     gk_rs, gk_hs = (0, 0) if gk is None else _token_view(gk, B, T, H, 3 * nb, "gk")
     Dp, Tp = padded_head_dim(d), padded_seq_len(T)
+    qh = torch.empty((B, H, Tp, Dp), dtype=dt, device=dev)
     kh = torch.empty((B, H, Tp, Dp), dtype=dt, device=dev)
     vh_t = torch.empty((B, H, Tp // 64, Dp, 64), dtype=dt, device=dev)
     P = torch.empty((B, H, T, nb, 4), dtype=torch.float32, device=dev)
@@ -93,25 +96,29 @@ def geom_scan(k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor, gk: Optional[t
         B, T, H, d, _lib.HOLO_GEN_DIRECT if gk is None else _lib.HOLO_GEN_ADDITIVE,
         float(edge_scale), _DT[dt], _DT[gdt],
         _ptr(gq), gq_rs, gq_hs, _ptr(gk), gk_rs, gk_hs,
-        _ptr(k), k_rs, k_hs, _ptr(v), v_rs, v_hs,
-        _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(hol),
+        _ptr(q), q_rs, q_hs, _ptr(k), k_rs, k_hs, _ptr(v), v_rs, v_hs,
+        _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(hol),
         _ptr(ws), ws_bytes, _stream(dev))
     _lib.check(rc, "holo_geom_scan_fwd")
-    return kh, vh_t, P, hol
+    return qh, kh, vh_t, P, hol
 
 
-def attention(q: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
-              scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """q: (B,T,H,d) view of raw queries; kh, vh_t, P from geom_scan.
+def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
+              d: int, scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """qh, kh, vh_t, P from geom_scan for head dimension d.
     Returns o as a (B,T,H,d) tensor (contiguous (B,T,H*d) storage unless
-    `out` is given)."""
+    `out`, a (B,T,H,d) view, is given)."""
     lib = _lib.load()
-    B, T, H, d = q.shape
+    if P.dim() != 5:
+        raise ValueError("attention: P must be (B, H, T, nb, 4)")
+    B, H, T = (int(n) for n in P.shape[:3])
     nb = d // 3
-    dev, dt = q.device, q.dtype
+    dev, dt = qh.device, qh.dtype
     if dev.type != "cuda" or dt not in _DT:
-        raise ValueError(f"attention: q must be a float32/bfloat16 GPU tensor (got {dt} on {dev})")
+        raise ValueError(f"attention: qh must be a float32/bfloat16 GPU tensor (got {dt} on {dev})")
     Dp, Tp = padded_head_dim(d), padded_seq_len(T)
+    if tuple(qh.shape) != (B, H, Tp, Dp) or not qh.is_contiguous():
+        raise ValueError("attention: qh does not match the geom_scan layout")
     if tuple(kh.shape) != (B, H, Tp, Dp) or not kh.is_contiguous() or kh.dtype != dt:
         raise ValueError("attention: kh does not match the geom_scan layout")
     if tuple(vh_t.shape) != (B, H, Tp // 64, Dp, 64) or not vh_t.is_contiguous() or vh_t.dtype != dt:
@@ -121,14 +128,13 @@ def attention(q: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Te
     for t in (kh, vh_t, P):
         if t.device != dev:
             raise ValueError("attention: all tensors must be on one device")
-    q_rs, q_hs = _token_view(q, B, T, H, d, "q")
     if out is None:
         out = torch.empty((B, T, H, d), dtype=dt, device=dev)
     elif out.dtype != dt or out.device != dev:
         raise ValueError("attention: out must match q's dtype and device")
     o_rs, o_hs = _token_view(out, B, T, H, d, "out")
     rc = lib.holo_attn_fwd(B, T, H, d, _DT[dt], float(scale),
-                           _ptr(q), q_rs, q_hs, _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
+                           _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
                            _ptr(out), o_rs, o_hs, _stream(dev))
     _lib.check(rc, "holo_attn_fwd")
     return out

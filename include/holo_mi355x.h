@@ -8,12 +8,12 @@
  *   holo_geom_scan_fwd  replaces PathOrderedGeometricMHA._geometry after the
  *                       projections (link rotations, prefix products,
  *                       holonomy: core/attention_fast_chunked.py:73-96) and
- *                       the key/value transports (:109-110);
+ *                       the query/key/value transports (:108-110);
  *   holo_attn_fwd       replaces HoloAttnFn.apply / run_fwd_kernel /
  *                       fwd_kernel (kernel/attention_kernel.py:40-134,166-172):
- *                       query transport, causal online-softmax attention and
- *                       the back-rotation out_i = P_i o_i
- *                       (core/attention_fast_chunked.py:108,119-171);
+ *                       causal online-softmax attention on the transported
+ *                       queries/keys/values and the back-rotation
+ *                       out_i = P_i o_i (core/attention_fast_chunked.py:119-171);
  *   holo_quat_to_dense  expands the stored rotations to the reference's dense
  *                       geometry tensors {"C": P, "H": Hol}
  *                       (core/attention_fast_chunked.py:175-177).
@@ -96,10 +96,12 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  *            at ptr[(b*T + t)*row_stride + h*head_stride + j], j < 3*nb.
  *            In HOLO_GEN_DIRECT mode gk must be NULL. Link parameters are
  *            accumulated and composed in fp32 whatever their storage type.
- *   k, v   : dtype `io_dtype`.
+ *   q, k, v: dtype `io_dtype`.
+ *   q      : like k, v.
  *            element (b, t, h, c) at ptr[(b*T + t)*row_stride + h*head_stride + c], c < d.
  * Outputs:
- *   kh   (B, H, Tp, Dp)        io_dtype, kh[t] = P_t^T k_t   (Tp = padded T, Dp = padded d)
+ *   qh   (B, H, Tp, Dp)        io_dtype, qh[t] = P_t^T q_t   (Tp = padded T, Dp = padded d)
+ *   kh   (B, H, Tp, Dp)        io_dtype, kh[t] = P_t^T k_t
  *   vh_t (B, H, Tp/64, Dp, 64) io_dtype, key tiles of 64 stored transposed:
  *                               vh_t[b][h][t/64][c][t%64] = (P_t^T v_t)[c]
  *        Padding (t >= T or c >= d) is written as zero.
@@ -113,23 +115,22 @@ HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
                        int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
                        const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
                        const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
+                       const void* q, int64_t q_row_stride, int64_t q_head_stride,
                        const void* k, int64_t k_row_stride, int64_t k_head_stride,
                        const void* v, int64_t v_row_stride, int64_t v_head_stride,
-                       void* kh, void* vh_t, float* P, float* hol,
+                       void* qh, void* kh, void* vh_t, float* P, float* hol,
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Causal path-ordered attention on transported keys/values.
- *   q    : raw queries, element (b, t, h, c) at q[(b*T + t)*q_row_stride + h*q_head_stride + c]
- *   kh, vh_t, P : as written by holo_geom_scan_fwd (same B, T, H, d, dtype)
+ * Causal path-ordered attention on transported queries/keys/values.
+ *   qh, kh, vh_t, P : as written by holo_geom_scan_fwd (same B, T, H, d, dtype)
  *   o    : output, element (b, t, h, c) at o[(b*T + t)*o_row_stride + h*o_head_stride + c]
- *          o_i = P_i * sum_{j<=i} softmax_j(scale * (P_i^T q_i).kh_j) * vh_j
+ *          o_i = P_i * sum_{j<=i} softmax_j(scale * qh_i . kh_j) * vh_j
  * dtype is the dtype of q, kh, vh_t and o (HOLO_BF16: bf16 MFMA with fp32
  * accumulation and softmax; HOLO_F32: fp32 MFMA throughout).
  */
 HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
-                  const void* q, int64_t q_row_stride, int64_t q_head_stride,
-                  const void* kh, const void* vh_t, const float* P,
+                  const void* qh, const void* kh, const void* vh_t, const float* P,
                   void* o, int64_t o_row_stride, int64_t o_head_stride,
                   void* stream);
 
