@@ -1,0 +1,102 @@
+"""The C-ABI library loads, exports every symbol include/holo_mi355x.h
+declares, and rejects bad arguments on the host (no kernel is launched)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from holonomyawareattention_amd import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "holo_mi355x.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return re.findall(r"HOLO_API\s+[\w\s\*]+?\b(holo_\w+)\s*\(", text)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert set(names) == {n for n, _, _ in _lib.SIGNATURES}
+    assert "holo_geom_scan_fwd" in names and "holo_attn_fwd" in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_exported_symbols_are_exactly_the_abi():
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l and l.split()[-1].startswith("holo_")}
+    assert exported == set(_declared())
+
+
+def test_version_and_layout_queries(lib):
+    assert lib.holo_abi_version() >> 16 >= 2
+    assert [lib.holo_padded_head_dim(d) for d in (1, 12, 32, 33, 48, 96)] == [32, 32, 32, 64, 64, 96]
+    assert [lib.holo_padded_seq_len(t) for t in (1, 64, 65, 2048)] == [64, 64, 128, 2048]
+    # two fp32 quaternion arrays (totals, carries) of B*H*chunks*nb
+    assert lib.holo_geom_scan_workspace_size(16, 2048, 16, 96) == 2 * 16 * 16 * 32 * 32 * 16
+    assert lib.holo_geom_scan_workspace_size(0, 2048, 16, 96) == 0
+
+
+def _scan(lib, **kw):
+    args = dict(B=1, T=8, H=2, d=12, gen=0, es=0.1, io=_lib.HOLO_F32, gdt=_lib.HOLO_F32,
+                gq=16, gk=16, q=16, k=16, v=16, qh=16, kh=16, vh=16, P=16, hol=None, ws=16, wsb=1 << 20,
+                rs=64, hs=24)
+    args.update(kw)
+    a = args
+    return lib.holo_geom_scan_fwd(a["B"], a["T"], a["H"], a["d"], a["gen"], a["es"], a["io"], a["gdt"],
+                                  a["gq"], a["rs"], a["hs"], a["gk"], a["rs"], a["hs"],
+                                  a["q"], a["rs"], a["hs"], a["k"], a["rs"], a["hs"], a["v"], a["rs"], a["hs"],
+                                  a["qh"], a["kh"], a["vh"], a["P"], a["hol"], a["ws"], a["wsb"], None)
+
+
+def test_scan_argument_validation(lib):
+    assert _scan(lib, B=0) == _lib.HOLO_ERR_BAD_SHAPE
+    assert b"positive" in lib.holo_last_error()
+    assert _scan(lib, d=200) == _lib.HOLO_ERR_UNSUPPORTED
+    assert _scan(lib, io=7) == _lib.HOLO_ERR_INVALID_ARG
+    assert _scan(lib, io=_lib.HOLO_F32, gdt=_lib.HOLO_BF16) == _lib.HOLO_ERR_UNSUPPORTED
+    assert _scan(lib, k=None) == _lib.HOLO_ERR_INVALID_ARG
+    assert _scan(lib, gen=_lib.HOLO_GEN_ADDITIVE, gk=None) == _lib.HOLO_ERR_INVALID_ARG
+    assert _scan(lib, gen=_lib.HOLO_GEN_DIRECT) == _lib.HOLO_ERR_INVALID_ARG      # gk given
+    assert _scan(lib, hs=4) == _lib.HOLO_ERR_INVALID_ARG                          # heads overlap
+    assert _scan(lib, kh=8) == _lib.HOLO_ERR_INVALID_ARG                          # misaligned
+    assert _scan(lib, wsb=16) == _lib.HOLO_ERR_WORKSPACE
+    assert _scan(lib, ws=None) == _lib.HOLO_ERR_WORKSPACE
+
+
+def test_attention_argument_validation(lib):
+    f = lib.holo_attn_fwd
+    assert f(1, 0, 1, 12, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_BAD_SHAPE
+    assert f(1, 8, 1, 120, 0, 0.3, 16, 16, 16, 16, 16, 120, 120, None) == _lib.HOLO_ERR_UNSUPPORTED
+    assert f(1, 8, 1, 12, 0, 0.0, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 0, 0.3, None, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 2, 12, 0, 0.3, 16, 16, 16, 16, 16, 12, 4, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 5, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+
+
+def test_status_codes_map_to_reference_exceptions(lib):
+    _scan(lib, B=0)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.HOLO_ERR_BAD_SHAPE, "scan")
+    _scan(lib, d=200)
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.HOLO_ERR_UNSUPPORTED, "scan")
+    with pytest.raises(_lib.HoloError):
+        _lib.check(_lib.HOLO_ERR_WORKSPACE, "scan")
+    _lib.check(_lib.HOLO_OK, "scan")

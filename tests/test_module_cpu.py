@@ -1,0 +1,60 @@
+"""Host-side behaviour of the drop-in module: constructor, attributes,
+state_dict keys, dispatch predicate and the errors of unsupported calls."""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from holonomyawareattention_amd.attention_kernel import PathOrderedGeometricMHA, _is_exact_tril
+
+REFERENCE_KEYS = {"qkv.weight", "out.weight", "gqproj.weight", "gkproj.weight",
+                  "edge_mlp.0.weight", "edge_mlp.0.bias", "edge_mlp.2.weight", "edge_mlp.2.bias"}
+
+
+def test_constructor_mirrors_reference():
+    m = PathOrderedGeometricMHA(192, n_heads=4, edge_scale=0.05)
+    assert (m.h, m.d, m.n_blocks, m.m_dim) == (4, 48, 16, 48)
+    assert m.scale == pytest.approx(1 / math.sqrt(48))
+    assert m.mode == "causal" and m.link_mode == "interaction" and m.edge_scale == 0.05
+    assert set(m.state_dict()) == REFERENCE_KEYS
+    assert tuple(m.gqproj.weight.shape) == (4 * 48, 192)
+    assert tuple(m.edge_mlp[2].weight.shape) == (4 * 48, 4 * 192)
+    m16 = PathOrderedGeometricMHA(64, n_heads=4)          # d = 16: five blocks, one free dim
+    assert (m16.n_blocks, m16.m_dim) == (5, 15)
+    with pytest.raises(ValueError):
+        PathOrderedGeometricMHA(100, n_heads=3)
+    with pytest.raises(ValueError):
+        PathOrderedGeometricMHA(96, n_heads=2, mode="ring")
+
+
+def test_exact_tril_predicate():
+    T = 7
+    tril = torch.ones(T, T, dtype=torch.bool).tril()
+    assert _is_exact_tril(tril, T)
+    assert not _is_exact_tril(None, T)
+    assert not _is_exact_tril(tril[:-1, :-1], T)
+    ring = tril.clone(); ring[0, T - 1] = True
+    assert not _is_exact_tril(ring, T)
+    assert _is_exact_tril(tril.int(), T)
+
+
+@pytest.mark.parametrize("kind", ["cpu", "inert", "nomask", "ring", "dropout", "dtype"])
+def test_unsupported_calls_raise(kind):
+    """No second code path: everything outside the kernel conditions raises,
+    as the guarded reference does (kernel/attention_fast_chunked.py:106-114)."""
+    T = 6
+    m = PathOrderedGeometricMHA(24, n_heads=2, mode="inert" if kind == "inert" else "causal",
+                                dropout=0.1 if kind == "dropout" else 0.0)
+    x = torch.randn(1, T, 24, dtype=torch.float16 if kind == "dtype" else torch.float32)
+    mask = torch.ones(T, T, dtype=torch.bool).tril()
+    if kind == "nomask":
+        mask = None
+    if kind == "ring":
+        mask = mask.clone(); mask[0, T - 1] = True
+    if kind == "dropout":
+        m.train()
+    with pytest.raises(NotImplementedError):
+        m(x, attn_mask=mask)
+    assert not m._kernel_supported(x, mask)
