@@ -58,26 +58,74 @@ def projection_flops(B, T, D, m_total) -> float:
     return 2.0 * B * T * D * (3 * D + 2 * m_total + D)
 
 
-def cpu_baseline(cfg, x_np, W, T_sample):
+def cpu_baseline(cfg, x_np, W, min_seconds=10.0):
     """Oracle restatement of core/attention_fast_chunked.py (fp32, dense
-    matrix_exp, sequential scan, BLOCK_K=64 streaming with the wrap branch) on
-    batch row 0, first T_sample tokens."""
+    matrix_exp, sequential scan, BLOCK_K=64 streaming with the wrap branch),
+    timed on whole batch rows of the workload (full T) until min_seconds have
+    passed (at least one row)."""
     import torch
     from oracle import holo_ref
-    H = cfg["H"]
-    xt = torch.as_tensor(x_np[:1, :T_sample]).float()
+    B, T, H = x_np.shape[0], x_np.shape[1], cfg["H"]
     Wt = {k: torch.as_tensor(v).float() for k, v in W.items()}
+    rows = 0
     with torch.no_grad():
-        holo_ref.forward_chunked(xt[:, :64], Wt, H, cfg["es"])          # warm-up
+        holo_ref.forward_chunked(torch.as_tensor(x_np[:1, :64]).float(), Wt, H, cfg["es"])  # warm-up
         t0 = time.perf_counter()
-        holo_ref.forward_chunked(xt, Wt, H, cfg["es"])
+        while rows < B and (rows == 0 or time.perf_counter() - t0 < min_seconds):
+            holo_ref.forward_chunked(torch.as_tensor(x_np[rows:rows + 1]).float(), Wt, H, cfg["es"])
+            rows += 1
         dt = time.perf_counter() - t0
-    return {"value": T_sample / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+    return {"value": rows * T / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port", "seconds": round(dt, 3),
-            "sample": f"batch row 0, tokens 0..{T_sample - 1} of the same workload "
-                      f"(B=1, T={T_sample}, H={H}, d_head={cfg['D'] // H}, fp32, dense "
-                      f"SO(d) embedding as the reference computes it); a T-prefix is "
-                      f"cheaper per token than the full T, so this rate is optimistic"}
+            "sample": f"batch rows 0..{rows - 1} of the same workload, full T={T} each "
+                      f"(H={H}, d_head={cfg['D'] // H}, fp32, the reference's dense SO(d) "
+                      f"layout and chunked algorithm step by step, host threads={torch.get_num_threads()})"}
+
+
+PMC_FETCH_SCALE = 2.0      # FETCH_SIZE reads 0.5x the bytes of a plain copy on this pool
+PMC_WRITE_SCALE = 1.0      # WRITE_SIZE reads 1.0x
+
+
+def pmc_summary(dirs):
+    """Per-kernel mean FETCH_SIZE / WRITE_SIZE (KiB per dispatch, from
+    rocprofv3 --pmc counter_collection.csv files under `dirs`), with the
+    calibration factors measured on the --copy-probe copy (1 GiB read, 1 GiB
+    written). Returns a dict keyed by kernel name."""
+    import csv
+    import glob
+    acc = {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                k = (r["Kernel_Name"], r["Counter_Name"])
+                acc.setdefault(k, []).append(float(r["Counter_Value"]))
+    copy = {c: max(v) for (n, c), v in acc.items() if "copyBuffer" in n}
+    fs = (1 << 20) / copy["FETCH_SIZE"] if "FETCH_SIZE" in copy else PMC_FETCH_SCALE
+    ws = (1 << 20) / copy["WRITE_SIZE"] if "WRITE_SIZE" in copy else PMC_WRITE_SCALE
+    out = {"fetch_scale": fs, "write_scale": ws, "kernels": {}}
+    for (name, ctr), v in acc.items():
+        if ctr not in ("FETCH_SIZE", "WRITE_SIZE"):
+            continue
+        e = out["kernels"].setdefault(name, {})
+        scale = fs if ctr == "FETCH_SIZE" else ws
+        e[ctr.lower() + "_bytes"] = sum(v) / len(v) * 1024 * scale
+        e["dispatches"] = len(v)
+    return out
+
+
+def traffic_from_profile(config, kernel_prefix):
+    """HBM bytes per launch of the kernels whose name starts with any of
+    `kernel_prefix` (summed), from the committed profiles/pmc_traffic_<config>.json."""
+    path = os.path.join(REPO, "profiles", f"pmc_traffic_{config}.json")
+    if not os.path.exists(path):
+        return None
+    data = json.load(open(path))
+    tot, found = 0.0, False
+    for name, e in data["kernels"].items():
+        if any(p in name for p in kernel_prefix) and "fetch_size_bytes" in e and "write_size_bytes" in e:
+            tot += e["fetch_size_bytes"] + e["write_size_bytes"]
+            found = True
+    return tot if found else None
 
 
 def main():
@@ -86,9 +134,15 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-sample-tokens", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="end with a plain 1 GiB device copy (PMC counter calibration)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc CSVs under DIR(s) as JSON and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(args.pmc_summary), indent=1))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): "
@@ -165,6 +219,12 @@ def main():
             staged(evs[i])
         torch.cuda.synchronize()
         wall_staged = time.perf_counter() - t1
+        if args.copy_probe:
+            src = torch.ones(1 << 28, dtype=torch.float32, device=dev)     # 1 GiB
+            dst = torch.empty_like(src)
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
     stage = np.zeros(4)
     for e in evs:
         for j in range(4):
@@ -205,19 +265,20 @@ def main():
                       "staged_wall_ms_per_step": wall_staged * 1e3 / args.steps},
         "roofline": {"kernel": "attn_fwd (holo_attn_fwd)", "bound": "mfma",
                      "achieved": core_tflops, "peak": core_peak, "unit": "TFLOP/s",
-                     "frac": core_tflops / core_peak, "traffic": None,
+                     "frac": core_tflops / core_peak,
+                     "traffic": traffic_from_profile(args.config, ["attn_fwd"]),
                      "work_per_launch": f"{fl_core:.4e} FLOP = 2*d*T*(T+1)*B*H"},
         "roofline_scan": {"kernels": "chunk_totals + chunk_carry + chunk_apply (holo_geom_scan_fwd)",
                           "bound": "hbm", "achieved": scan_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                          "frac": scan_gbs / PEAK_HBM_GBS, "traffic": None,
+                          "frac": scan_gbs / PEAK_HBM_GBS,
+                          "traffic": traffic_from_profile(args.config, ["chunk_totals", "chunk_carry", "chunk_apply"]),
                           "bytes_per_launch": scan_bytes,
                           "bytes_per_token_head": scan_bytes_per_token_head(d, io_bytes)},
     }
     if not args.no_cpu_baseline:
         W = {k: v for k, v in inp.items()}
-        Ts = min(args.cpu_sample_tokens, T)
         try:
-            out["cpu_baseline"] = cpu_baseline(cfg, x_np, W, Ts)
+            out["cpu_baseline"] = cpu_baseline(cfg, x_np, W)
         except Exception as e:   # the GPU figure stands on its own
             out["cpu_baseline"] = {"error": repr(e)}
     print(json.dumps(out), flush=True)
