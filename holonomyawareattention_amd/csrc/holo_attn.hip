@@ -236,6 +236,26 @@ attn_fwd(AttnArgs a) {
       });
     }
   };
+  // quaternions of the epilogue items (row, 8 consecutive 3-dim groups); a
+  // row's 8 quaternions are 128 contiguous bytes
+  f32x4 pq[C::EPI][8];
+  auto load_epilogue_quats = [&](auto first, auto count) {
+    static_for<decltype(count)::value>([&](auto k) {
+      constexpr int it = decltype(first)::value + decltype(k)::value;
+      const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
+      const int64_t t = q0 + r;
+      const bool row_ok = idx < kBM * C::NG8 && t < a.T;
+      const float* base = a.P + ((bh * a.T + t) * a.nb + 8 * gi) * 4;
+      if (row_ok && 8 * gi + 8 <= a.nb) {
+        static_for<8>([&](auto jb) { pq[it][jb] = reinterpret_cast<const f32x4*>(base)[jb]; });
+      } else {
+        static_for<8>([&](auto jb) {
+          pq[it][jb] = (row_ok && 8 * gi + jb < a.nb) ? reinterpret_cast<const f32x4*>(base)[jb]
+                                                      : f32x4{1.f, 0.f, 0.f, 0.f};
+        });
+      }
+    });
+  };
   // one pipeline step: tile j in S, tile j+1 into Sn
   auto step = [&](int j, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
     // (the next tile's QK runs whenever this tile does; past the wave's last
@@ -258,6 +278,7 @@ attn_fwd(AttnArgs a) {
     step(j, SA, SB);
     if (j + 1 < nkv) step(j + 1, SB, SA);
   }
+  load_epilogue_quats(std::integral_constant<int, 0>{}, std::integral_constant<int, C::EPI>{});
 
   // ---- epilogue: normalise, stage O^T, back-rotate o = P oh, store ----
   float lt = l_run + __shfl_xor(l_run, 32);
@@ -268,19 +289,7 @@ attn_fwd(AttnArgs a) {
     });
   });
   __syncthreads();
-  // item = (row, 8 consecutive 3-dim groups = 24 dims); all quaternion loads
-  // of the thread's items are issued before any of them is used
-  f32x4 pq[C::EPI][8];
-  static_for<C::EPI>([&](auto it) {
-    const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
-    const int64_t t = q0 + r;
-    static_for<8>([&](auto jb) {
-      const int blk = 8 * gi + jb;
-      pq[it][jb] = (idx < kBM * C::NG8 && t < a.T && blk < a.nb)
-                       ? *reinterpret_cast<const f32x4*>(a.P + ((bh * a.T + t) * a.nb + blk) * 4)
-                       : f32x4{1.f, 0.f, 0.f, 0.f};
-    });
-  });
+  // item = (row, 8 consecutive 3-dim groups = 24 dims), quaternions in pq
   static_for<C::EPI>([&](auto it) {
     const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
     const int64_t t = q0 + r;
@@ -289,9 +298,9 @@ attn_fwd(AttnArgs a) {
     static_for<24>([&](auto j) { u[j] = (24 * gi + j < DP) ? Os[r * C::OS + 24 * gi + j] : 0.f; });
     static_for<8>([&](auto jb) {
       if (8 * gi + jb < a.nb) {
-        rot3 R = qmat(quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]});
         float y0, y1, y2;
-        rot_apply(R, u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
+        quat_rotate(quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]},
+                    u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
         u[3 * jb] = y0; u[3 * jb + 1] = y1; u[3 * jb + 2] = y2;
       }
     });

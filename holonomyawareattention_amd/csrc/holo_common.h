@@ -113,6 +113,20 @@ __device__ inline void rot_apply(const rot3& R, float u0, float u1, float u2,
   y2 = R.m[2][0] * u0 + R.m[2][1] * u1 + R.m[2][2] * u2;
 }
 
+// y = R(q) u with R the homogeneous rotation of q (same map as qmat):
+// R(q) u = ((w^2 - |v|^2) u + 2 (v.u) v + 2 w (v x u)) / |q|^2,  v = (x, y, z)
+__device__ inline void quat_rotate(const quat& q, float u0, float u1, float u2,
+                                   float& y0, float& y1, float& y2) {
+  const float vv = q.x * q.x + q.y * q.y + q.z * q.z;
+  const float inv = __builtin_amdgcn_rcpf(q.w * q.w + vv);
+  const float a = (q.w * q.w - vv) * inv;
+  const float b = 2.f * (q.x * u0 + q.y * u1 + q.z * u2) * inv;
+  const float cw = 2.f * q.w * inv;
+  y0 = a * u0 + b * q.x + cw * (q.y * u2 - q.z * u1);
+  y1 = a * u1 + b * q.y + cw * (q.z * u0 - q.x * u2);
+  y2 = a * u2 + b * q.z + cw * (q.x * u1 - q.y * u0);
+}
+
 __device__ inline quat load_quat(const float* p) {
   f32x4 v = *reinterpret_cast<const f32x4*>(p);
   return quat{v[0], v[1], v[2], v[3]};
