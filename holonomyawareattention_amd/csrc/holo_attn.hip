@@ -37,6 +37,28 @@ constexpr int kThreads = 64 * kWaves;
 // Numerator and denominator use the same stale max, so the result is exact.
 constexpr float kRescaleThreshold = 8.f;
 
+// max / sum of a value over lanes l and l^32 with a VALU lane swap (no LDS
+// round trip): the two results of the swap hold the values of both halves
+__device__ __forceinline__ float pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// maximum of the 32 scores a lane holds, as a balanced tree (a serial chain
+// of dependent max operations leaves the SIMD idle between them)
+__device__ __forceinline__ float tile_max(const f32x16 (&S)[2]) {
+  float m[16];
+  static_for<16>([&](auto r) { m[r] = fmaxf(S[0][(int)r], S[1][(int)r]); });
+  static_for<8>([&](auto r) { m[r] = fmaxf(m[r], m[r + 8]); });
+  static_for<4>([&](auto r) { m[r] = fmaxf(m[r], m[r + 4]); });
+  static_for<2>([&](auto r) { m[r] = fmaxf(m[r], m[r + 2]); });
+  return fmaxf(m[0], m[1]);
+}
+
 template <typename T, int DP> struct AttnCfg {
   static constexpr int E = 16 / sizeof(T);             // elements per 16 B
   // LDS row strides chosen so the MFMA operand reads hit distinct banks:
@@ -176,11 +198,12 @@ attn_fwd(AttnArgs a) {
         });
       });
     }
-    float mx = S[0][0];
-    static_for<2>([&](auto kb) { static_for<16>([&](auto r) { mx = fmaxf(mx, S[kb][(int)r]); }); });
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
-    if (__any(mx > m_run + kRescaleThreshold)) {       // wave-uniform, rare after warm-up
-      const float m_new = fmaxf(m_run, mx);
+    const float mx = pair_max(tile_max(S)) * c;
+    // each row decides for itself (a row's result never depends on its
+    // neighbours'); the wave-uniform branch only skips the work, rare after warm-up
+    const bool need = mx > m_run + kRescaleThreshold;
+    if (__any(need)) {
+      const float m_new = need ? mx : m_run;
       const float corr = exp2f(m_run - m_new);
       m_run = m_new;
       l_run *= corr;
@@ -200,17 +223,19 @@ attn_fwd(AttnArgs a) {
           static_for<8>([&](auto e) { pb[kb][hh][(int)e] = (bf16)S[kb][8 * hh + e]; });
         });
       });
-      float ls = 0.f;
+      // four independent partial sums (one per P^T operand), then a tree
+      float ls[2][2];
       const bf16x2 one2 = {(bf16)1.f, (bf16)1.f};
       static_for<2>([&](auto kb) {
         static_for<2>([&](auto hh) {
+          ls[kb][hh] = 0.f;
           static_for<4>([&](auto e) {
             bf16x2 pr = {pb[kb][hh][2 * e], pb[kb][hh][2 * e + 1]};
-            ls = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, ls, false);
+            ls[kb][hh] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, ls[kb][hh], false);
           });
         });
       });
-      l_run += ls;
+      l_run += (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
       static_for<2>([&](auto kb) {
         static_for<2>([&](auto hh) {
           static_for<DP / 32>([&](auto db) {          // independent accumulators back to back
@@ -223,9 +248,12 @@ attn_fwd(AttnArgs a) {
         });
       });
     } else {
-      float ls = 0.f;
-      static_for<2>([&](auto kb) { static_for<16>([&](auto r) { ls += S[kb][(int)r]; }); });
-      l_run += ls;
+      float t[16];
+      static_for<16>([&](auto r) { t[r] = S[0][(int)r] + S[1][(int)r]; });
+      static_for<8>([&](auto r) { t[r] += t[r + 8]; });
+      static_for<4>([&](auto r) { t[r] += t[r + 4]; });
+      static_for<2>([&](auto r) { t[r] += t[r + 2]; });
+      l_run += t[0] + t[1];
       static_for<2>([&](auto kb) {
         static_for<16>([&](auto r) {
           static_for<DP / 32>([&](auto db) {
@@ -281,7 +309,7 @@ attn_fwd(AttnArgs a) {
   load_epilogue_quats(std::integral_constant<int, 0>{}, std::integral_constant<int, C::EPI>{});
 
   // ---- epilogue: normalise, stage O^T, back-rotate o = P oh, store ----
-  float lt = l_run + __shfl_xor(l_run, 32);
+  float lt = pair_sum(l_run);
   const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
   static_for<DP / 32>([&](auto db) {
     static_for<16>([&](auto r) {
