@@ -153,6 +153,9 @@ int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
     return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t and P must be 16-byte aligned");
   if (!(scale > 0.f) || !(scale < 1e30f))
     return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
+  // key/value tiles of one (b, h) are addressed with 32-bit byte offsets
+  if (holo::padded_seq(T) * holo::padded_head_dim(d) * (dtype == HOLO_F32 ? 4 : 2) > 0x7fffffff)
+    return fail(HOLO_ERR_UNSUPPORTED, "T = %lld too long for one (b, h) key slice", (long long)T);
 
   holo::AttnArgs a;
   a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d);

@@ -36,6 +36,8 @@ constexpr int kThreads = 64 * kWaves;
 // query's max grows by more than this, so exponentiated scores stay <= 2^8.
 // Numerator and denominator use the same stale max, so the result is exact.
 constexpr float kRescaleThreshold = 8.f;
+// dword 3 of a raw buffer resource on gfx9-family targets (32-bit data format)
+constexpr int kBufferWord3 = 0x00020000;
 
 // max / sum of a value over lanes l and l^32 with a VALU lane swap (no LDS
 // round trip): the two results of the swap hold the values of both halves
@@ -48,15 +50,17 @@ __device__ __forceinline__ float pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// maximum of the 32 scores a lane holds, as a balanced tree (a serial chain
-// of dependent max operations leaves the SIMD idle between them)
+__device__ __forceinline__ float max3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
+// maximum of the 32 scores a lane holds: a tree of 3-input maxima (16
+// v_max3, depth 4) instead of a serial chain of dependent operations
 __device__ __forceinline__ float tile_max(const f32x16 (&S)[2]) {
-  float m[16];
-  static_for<16>([&](auto r) { m[r] = fmaxf(S[0][(int)r], S[1][(int)r]); });
-  static_for<8>([&](auto r) { m[r] = fmaxf(m[r], m[r + 8]); });
-  static_for<4>([&](auto r) { m[r] = fmaxf(m[r], m[r + 4]); });
-  static_for<2>([&](auto r) { m[r] = fmaxf(m[r], m[r + 2]); });
-  return fmaxf(m[0], m[1]);
+  float v[32], m[12];
+  static_for<16>([&](auto r) { v[r] = S[0][(int)r]; v[16 + r] = S[1][(int)r]; });
+  static_for<10>([&](auto i) { m[i] = max3(v[3 * i], v[3 * i + 1], v[3 * i + 2]); });
+  m[10] = v[30]; m[11] = v[31];
+  static_for<4>([&](auto i) { m[i] = max3(m[3 * i], m[3 * i + 1], m[3 * i + 2]); });
+  return fmaxf(max3(m[0], m[1], m[2]), m[3]);
 }
 
 template <typename T, int DP> struct AttnCfg {
@@ -148,11 +152,22 @@ attn_fwd(AttnArgs a) {
   constexpr int RC = DP / C::E, VC = kBN / C::E;        // chunks per K row / V^T row
 
   u32x4 kreg[C::KCH], vreg[C::VCH];
+  // buffer loads: the (b, h) slice in a scalar resource descriptor, the tile
+  // offset in a scalar register and a constant byte offset per lane, so a
+  // tile load costs no per-lane address arithmetic
+  const int kv_bytes = (int)((int64_t)a.Tp * DP * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u32x4*>(kbase), 0, kv_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<u32x4*>(vbase), 0, kv_bytes, kBufferWord3);
   auto load_tile = [&](int kt) {
-    const u32x4* kn = kbase + (int64_t)kt * TCH;
-    const u32x4* vn = vbase + (int64_t)kt * TCH;
-    static_for<C::KCH>([&](auto j) { kreg[j] = kn[tid + j * kThreads]; });
-    static_for<C::VCH>([&](auto j) { vreg[j] = vn[tid + j * kThreads]; });
+    const int toff = kt * TCH * 16;
+    static_for<C::KCH>([&](auto j) {
+      kreg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, (tid + j * kThreads) * 16, toff, 0);
+    });
+    static_for<C::VCH>([&](auto j) {
+      vreg[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (tid + j * kThreads) * 16, toff, 0);
+    });
   };
   auto store_tile = [&](int st) {
     T* Ks = kv + st * C::kStage;
