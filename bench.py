@@ -128,6 +128,36 @@ def traffic_from_profile(config, kernel_prefix):
     return tot if found else None
 
 
+def orthogonality_report(m, x, config, kernels, torch):
+    """Geometry at the longest prefix: P_{T-1} (and the holonomy) as the
+    kernels apply them, i.e. the dense block rotations of the stored
+    quaternions under the homogeneous map. Reports max |P^T P - I| entry,
+    the induced infinity norm of P^T P - I (max absolute row sum, at most
+    3x the entry max for 3x3 blocks) and the quaternion norm drift."""
+    B, T, D = x.shape
+    H = m.h
+    d = D // H
+    with torch.no_grad():
+        q, k, v, gq, gk = m._link_inputs(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, m.edge_scale, want_hol=True)
+        torch.cuda.synchronize()
+        scan_ms = (time.perf_counter() - t0) * 1e3
+        out = {"metric": "orthogonality of P at t = T-1", "config": {"workload": config, "B": B, "T": T, "H": H,
+               "d_head": d, "edge_scale": m.edge_scale, "scan_chunk": 64}}
+        for name, quat in (("P_last", P[:, :, T - 1].contiguous()), ("holonomy", hol)):
+            R = kernels.quat_to_dense(quat, d).double()
+            E = R.transpose(-1, -2) @ R - torch.eye(d, dtype=torch.float64, device=R.device)
+            n2 = (quat.double() ** 2).sum(-1)
+            out[name] = {"max_abs_entry": E.abs().max().item(),
+                         "inf_norm": E.abs().sum(-1).max().item(),
+                         "quat_norm2_drift": (n2 - 1).abs().max().item()}
+        out["gate"] = "max_abs_entry <= 1e-4 (the entry maximum; the infinity norm is at most 3x it)"
+        out["scan_ms_wall"] = scan_ms
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,6 +167,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="end with a plain 1 GiB device copy (PMC counter calibration)")
+    ap.add_argument("--ortho", action="store_true",
+                    help="config 3 geometry check: orthogonality of P at t = T-1 (one JSON line) and exit")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSVs under DIR(s) as JSON and exit")
     args = ap.parse_args()
@@ -172,6 +204,9 @@ def main():
                 p.copy_(torch.as_tensor(inp[k]))
     m = m.to(device=dev, dtype=dt).eval()
     x = torch.as_tensor(x_np).to(device=dev, dtype=dt)
+    if args.ortho:
+        print(json.dumps(orthogonality_report(m, x, args.config, kernels, torch)))
+        return
     mask = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
 
     def staged(ev=None):

@@ -259,3 +259,66 @@ def test_scan_wide_path_matches_generic(dtype, D, H):
     torch.cuda.synchronize()
     for a, b in zip(out_w, out_g):
         assert torch.equal(a, b)
+
+
+def _final_product_fp64(a, chunk=4096):
+    """fp64 P_{T-1} = G_{T-2} ... G_0 for link parameters a (B, H, T-1, nb, 3)."""
+    B, H, L, nb, _ = a.shape
+    M = np.broadcast_to(np.eye(3), (B, H, nb, 3, 3)).copy()
+    for t0 in range(0, L, chunk):
+        G = R.rodrigues(a[:, :, t0:t0 + chunk])
+        for i in range(G.shape[2]):
+            M = G[:, :, i] @ M
+    return M
+
+
+def _fp32_matrix_scan(a, chains=64):
+    """The reference's way (sequential fp32 products of rotation matrices, no
+    renormalisation) on the first `chains` (b, h, block) chains."""
+    flat = a.transpose(0, 1, 3, 2, 4).reshape(-1, a.shape[2], 3)[:chains]
+    G = R.rodrigues(flat).astype(np.float32)             # (chains, T-1, 3, 3)
+    M = np.broadcast_to(np.eye(3, dtype=np.float32), (flat.shape[0], 3, 3)).copy()
+    for i in range(G.shape[1]):
+        M = G[:, i] @ M
+    return M
+
+
+def test_cfg3_long_prefix_geometry():
+    """Config 3 (B=2, T=32768, D=1536, H=16, bf16 activations, fp32
+    composition): P_{T-1} as the kernels apply it (the homogeneous rotation of
+    the stored quaternion) is orthogonal, max |P^T P - I| <= 1e-4 entrywise
+    (the induced infinity norm is at most 3x that), and it matches the fp64
+    sequential product of the same links within 1e-3 max-abs."""
+    B, T, D, H, es = 2, 32768, 1536, 16, 0.05
+    d = D // H
+    nb = d // 3
+    g = torch.Generator(device=DEV).manual_seed(33)
+    x = torch.randn(B, T, D, device=DEV, generator=g).to(torch.bfloat16)
+    from holonomyawareattention_amd.attention_kernel import PathOrderedGeometricMHA
+    m = PathOrderedGeometricMHA(D, n_heads=H, edge_scale=es)
+    m.link_mode = "additive"
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, device="cpu", generator=torch.Generator().manual_seed(p.numel())) / math.sqrt(D))
+    m = m.to(device=DEV, dtype=torch.bfloat16).eval()
+    with torch.no_grad():
+        q, k, v, gq, gk = m._link_inputs(x)
+        qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, es, want_hol=True)
+        Pl = kernels.quat_to_dense(P[:, :, T - 1].contiguous(), d).double()
+        eye = torch.eye(d, dtype=torch.float64, device=DEV)
+        E = Pl.transpose(-1, -2) @ Pl - eye
+        ortho_entry, ortho_inf = E.abs().max().item(), E.abs().sum(-1).max().item()
+        Pq = P[:, :, T - 1].double()
+    torch.cuda.synchronize()
+    gq_, gk_ = (_np(t).transpose(0, 2, 1, 3) for t in (gq, gk))       # (B, H, T, nb*3)
+    a = ((gq_[:, :, :-1] + gk_[:, :, 1:]) * es).reshape(B, H, T - 1, nb, 3)
+    ref = _final_product_fp64(a)                                        # (B, H, nb, 3, 3)
+    got = R.blocks_to_dense(ref, d)
+    err = np.abs(_np(Pl) - got).max()
+    drift = _fp32_matrix_scan(a)
+    Ed = np.swapaxes(drift, -1, -2).astype(np.float64) @ drift.astype(np.float64) - np.eye(3)
+    print(f"\ncfg3 P_(T-1): max|PtP-I| {ortho_entry:.3g} (inf-norm {ortho_inf:.3g}), "
+          f"max|P - P_fp64| {err:.3g}, quat |q|^2-1 {(Pq.pow(2).sum(-1) - 1).abs().max().item():.3g}; "
+          f"fp32 matrix scan (reference style, 64 chains): max|PtP-I| {np.abs(Ed).max():.3g}")
+    assert ortho_entry <= 1e-4 and ortho_inf <= 3e-4
+    assert err <= 1e-3
