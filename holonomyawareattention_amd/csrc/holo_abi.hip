@@ -54,7 +54,7 @@ extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (2 << 16) | 0; }
+int holo_abi_version(void) { return (2 << 16) | 1; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -62,8 +62,7 @@ int64_t holo_padded_seq_len(int64_t T) { return holo::padded_seq(T); }
 
 size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d) {
   if (B <= 0 || T <= 0 || H <= 0 || d <= 0) return 0;
-  int64_t nch = holo::padded_seq(T) / holo::kChunk;
-  return (size_t)2 * B * H * nch * (d / 3) * 4 * sizeof(float);
+  return holo::scan_state_bytes(B, T, H, d);
 }
 
 int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
@@ -127,8 +126,13 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
     a.wide = (d == 48 || d == 72 || d == 96) && al(gq, gq_rs, gq_hs, ge) && al(gk, gk_rs, gk_hs, ge) &&
              al(q, q_rs, q_hs, ie) && al(k, k_rs, k_hs, ie) && al(v, v_rs, v_hs, ie);
   }
-  a.totals = static_cast<float*>(workspace);
-  a.carry = a.totals ? a.totals + (size_t)B * H * a.nch * nb * 4 : nullptr;
+  {
+    // chained-scan state: chunk inclusive prefixes, then the ticket counter
+    // and time-out flag (cleared by the scan's own reset launch)
+    const size_t nq = (size_t)B * H * a.nch * nb * 4;
+    a.incl = static_cast<float*>(workspace);
+    a.ticket = reinterpret_cast<unsigned*>(a.incl + nq);
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = io_dtype == HOLO_F32 ? holo::launch_scan<float, float>(a, s)
                  : gen_dtype == HOLO_F32 ? holo::launch_scan<holo::bf16, float>(a, s)

@@ -15,10 +15,11 @@ struct ScanArgs {
   const void* k; int64_t k_rs, k_hs;
   const void* v; int64_t v_rs, v_hs;
   void* qh; void* kh; void* vh_t; float* P; float* hol;
-  int wide;        // 16-byte row path of chunk_apply (d in {48, 72, 96}, aligned rows)
-  float* totals;   // (B, H, nch, nb, 4) chunk totals
-  float* carry;    // (B, H, nch, nb, 4) prefix product at each chunk start
+  int wide;        // 16-byte row path of the scan (d in {48, 72, 96}, aligned rows)
+  float* incl;     // (B, H, nch, nb, 4) prefix product through each chunk (chained-scan state)
+  unsigned* ticket;  // [0]: chunk ticket counter, [1]: carry-wait time-out flag
 };
+size_t scan_state_bytes(int B, int64_t T, int H, int d);
 
 struct AttnArgs {
   int B, H, d, nb, Dp;

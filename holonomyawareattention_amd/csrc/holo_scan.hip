@@ -8,16 +8,21 @@
 //   P_0 = I, P_{t+1} = G_t P_t ; Hol = G_{T-1} P_{T-1}     :89-95
 //   qh_t  = P_t^T q_t, kh_t = P_t^T k_t, vh_t = P_t^T v_t   :108-110
 //
-// Each 3x3 block of every (b, h) is an independent scan over t. The scan runs
-// in three launches over chunks of 64 links:
-//   1. chunk_totals : one thread per (b, chunk, h, block) composes the chunk's
-//                     64 link rotations (quaternions) into the chunk total;
-//   2. chunk_carry  : one thread per (b, h, block) composes the totals in chunk
-//                     order into exclusive carries (the prefix P at each chunk
-//                     start) and the holonomy;
-//   3. chunk_apply  : one workgroup per (b, chunk, h) starts each block from
-//                     its carry, recomposes the chunk link by link, writes P_t
-//                     and the transported kh, vh tiles (zero padding included).
+// Each 3x3 block of every (b, h) is an independent scan over t. The scan is
+// one pass over the inputs in chunks of 64 links, one workgroup per
+// (b, h, chunk):
+//   1. link quaternions of the chunk's links -> LDS;
+//   2. one thread per block composes them from the identity (local prefixes
+//      L_r and the chunk product T_c), waits for the product of all earlier
+//      chunks C = incl[c-1] published by the previous chunk's workgroup, and
+//      publishes incl[c] = T_c C (a chained scan through the workspace);
+//   3. all threads: P_t = L_r C, written to P, and the transported qh, kh, vh.
+// Workgroups take chunks in ticket order (a global counter), chunk-major, so a
+// chunk only ever waits on a chunk that was handed out earlier and is running
+// or done: the wait always ends. Its polls are bounded anyway; a time-out
+// (impossible in a conforming launch) sets a flag in the workspace and the
+// chunk's outputs become NaN. The carry is always incl[c-1], so the
+// composition order, and every bit of the result, does not depend on timing.
 // Threads of a wave cover consecutive blocks of the same token rows, so the
 // token-major input rows are read contiguously.
 #include "holo_kernels.h"
@@ -37,51 +42,111 @@ __device__ inline quat link_quat(const ScanArgs& a, int b, int h, int blk, int64
   return qexp_skew(p0 * a.edge_scale, p1 * a.edge_scale, p2 * a.edge_scale);
 }
 
-template <typename GT>
-__global__ void __launch_bounds__(256) chunk_totals(ScanArgs a) {
-  int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int64_t n = (int64_t)a.B * a.nch * a.H * a.nb;
-  if (gid >= n) return;
-  int blk = gid % a.nb;
-  int h = (gid / a.nb) % a.H;
-  int64_t c = (gid / ((int64_t)a.nb * a.H)) % a.nch;
-  int b = gid / ((int64_t)a.nb * a.H * a.nch);
-  int64_t t0 = c * kChunk;
-  int64_t t1 = t0 + kChunk;
-  if (t1 > a.T - 1) t1 = a.T - 1;      // links 0..T-2 only
-  quat acc = qident();
-  for (int64_t t = t0; t < t1; ++t) acc = qmul(link_quat<GT>(a, b, h, blk, t), acc);
-  store_quat(a.totals + (((int64_t)b * a.H + h) * a.nch + c) * a.nb * 4 + blk * 4, acc);
+size_t scan_state_bytes(int B, int64_t T, int H, int d) {
+  const int64_t nch = padded_seq(T) / kChunk;
+  return (size_t)B * H * nch * (d / 3) * 4 * sizeof(float) + 256;
 }
 
-template <typename GT>
-__global__ void __launch_bounds__(256) chunk_carry(ScanArgs a) {
-  int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int64_t n = (int64_t)a.B * a.H * a.nb;
-  if (gid >= n) return;
-  int blk = gid % a.nb;
-  int h = (gid / a.nb) % a.H;
-  int b = gid / ((int64_t)a.nb * a.H);
-  int64_t base = ((int64_t)b * a.H + h) * a.nch * a.nb * 4 + blk * 4;
-  quat cur = qident();
-  for (int64_t c = 0; c < a.nch; ++c) {
-    int64_t off = base + c * a.nb * 4;
-    store_quat(a.carry + off, cur);
-    cur = qmul(load_quat(a.totals + off), cur);
-  }
-  if (a.hol) {   // cur == P_{T-1}
-    quat g = link_quat<GT>(a, b, h, blk, a.T - 1);
-    store_quat(a.hol + (((int64_t)b * a.H + h) * a.nb + blk) * 4, qmul(g, cur));
+// ---- chained-scan state ----------------------------------------------------
+// incl[b][h][c][blk] (product of chunks 0..c) are fp32 quaternions whose
+// 32-bit words start as kUnset. Each word is written once per scan and read
+// with agent-scope relaxed atomics, so a word is either unset or final and
+// readers need no fence: a quaternion is complete when none of its words is
+// unset. A computed word equal to kUnset (one NaN bit pattern) is stored as
+// the canonical NaN instead.
+constexpr unsigned kUnset = 0xffffffffu;
+constexpr unsigned kCanonNan = 0x7fc00000u;
+constexpr int kMaxPolls = 1 << 18;   // ~0.3 s of polling
+
+__device__ __forceinline__ void put_quat(float* slot, const quat& q) {
+  unsigned* u = reinterpret_cast<unsigned*>(slot);
+  const float v[4] = {q.w, q.x, q.y, q.z};
+  static_for<4>([&](auto k) {
+    unsigned x = __float_as_uint(v[k]);
+    if (x == kUnset) x = kCanonNan;
+    __hip_atomic_store(u + k, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  });
+}
+
+__device__ __forceinline__ bool get_quat(const float* slot, quat& q) {
+  const unsigned* u = reinterpret_cast<const unsigned*>(slot);
+  unsigned x[4];
+  static_for<4>([&](auto k) { x[k] = __hip_atomic_load(u + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); });
+  if (x[0] == kUnset || x[1] == kUnset || x[2] == kUnset || x[3] == kUnset) return false;
+  q = quat{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3])};
+  return true;
+}
+
+// clears the chained-scan state and the ticket counter before every scan
+// (atomic stores, so no cached copy of the old state survives)
+__global__ void __launch_bounds__(256) scan_reset(uint64_t* state, int64_t n_pairs, unsigned* ticket) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n_pairs) __hip_atomic_store(state + i, ~(uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (i == 0) {
+    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ticket + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-// One workgroup per (b, chunk, h) tile of 64 tokens:
+// (b*H + h, chunk) of this workgroup from the ticket counter, chunk-major
+__device__ __forceinline__ void take_ticket(const ScanArgs& a, int64_t& bh, int64_t& c) {
+  __shared__ unsigned s_ticket;
+  if (threadIdx.x == 0)
+    s_ticket = __hip_atomic_fetch_add(a.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int64_t tk = s_ticket, nbh = (int64_t)a.B * a.H;
+  c = tk / nbh;             // >= nch only if the counter was not reset (caller returns)
+  bh = tk % nbh;
+}
+
+// product of chunks 0 .. c-1 for one block (c >= 1): the inclusive prefix
+// that chunk c-1 publishes. Waiting for exactly that value (rather than
+// composing whatever predecessor state happens to be ready) keeps the
+// association, and so every bit of the result, independent of timing.
+__device__ inline quat wait_prefix(const ScanArgs& a, int64_t bh, int64_t c, int blk) {
+  const float* slot = a.incl + ((bh * a.nch + c - 1) * a.nb + blk) * 4;
+  quat x;
+  for (int polls = 0; polls < kMaxPolls; ++polls) {
+    if (get_quat(slot, x)) return x;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __hip_atomic_store(a.ticket + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float nan = __uint_as_float(kCanonNan);
+  return quat{nan, nan, nan, nan};
+}
+
+// Step 2 of the scan for one block (thread blk < nb): gs holds the chunk's
+// link quaternions (slot r = link t0 + r, identity past T-2); on return slot r
+// holds the local prefix L_r and cs[blk] the carry C (product of all earlier
+// chunks). Also writes the holonomy from the last chunk.
+template <typename GT>
+__device__ inline void chain_block(const ScanArgs& a, float* gs, float* cs, int64_t bh, int64_t c, int blk) {
+  const int nb = a.nb;
+  quat p = qident();
+  for (int r = 0; r < kChunk; ++r) {
+    float* slot = &gs[(r * nb + blk) * 4];
+    quat g = load_quat(slot);
+    store_quat(slot, p);
+    p = qmul(g, p);
+  }
+  // C = product of chunks 0..c-1; publish the product of chunks 0..c
+  const quat C = c == 0 ? qident() : wait_prefix(a, bh, c, blk);
+  if (c + 1 < a.nch) put_quat(a.incl + ((bh * a.nch + c) * nb + blk) * 4, qmul(p, C));
+  store_quat(&cs[blk * 4], C);
+  if (a.hol && c == a.nch - 1) {                       // Hol = G_close P_{T-1}
+    const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+    const int64_t n = a.T - c * kChunk;
+    quat pl = qmul(load_quat(&gs[((n - 1) * nb + blk) * 4]), C);
+    store_quat(a.hol + (bh * nb + blk) * 4, qmul(link_quat<GT>(a, b, h, blk, a.T - 1), pl));
+  }
+}
+
+// One workgroup per (b, h, chunk) tile of 64 tokens (any d <= 96):
 //   1. all threads: link quaternions g_t of the tile's links -> LDS;
-//   2. one thread per block: P_t = g_{t-1} ... g_{t0} C (C = carry), written to
-//      global P and over g_t in LDS;
-//   3. all threads, one (token, 3-dim group) each: qh = P^T q, kh = P^T k and
-//      vh = P^T v into row-major qh, kh tiles and a transposed vh tile in LDS
-//      (zero padding);
+//   2. one thread per block: local prefixes and the chained carry (chain_block);
+//   3. all threads: P_t = L_r C -> global P and LDS; qh = P^T q, kh = P^T k
+//      and vh = P^T v into row-major qh, kh tiles and a transposed vh tile in
+//      LDS (zero padding);
 //   4. the tiles leave with 16-byte stores of whole rows (each tile is one
 //      contiguous block in global memory).
 template <typename IO, typename GT, int DP>
@@ -92,17 +157,18 @@ __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
   constexpr int NBM = DP / 3;           // blocks held in LDS (nb <= NBM)
   constexpr int NBX = (DP + 2) / 3;     // 3-dim groups covering DP
   __shared__ __align__(16) float gs[kChunk * NBM * 4];
+  __shared__ __align__(16) float cs[NBM * 4];
   __shared__ __align__(16) IO qhs[kChunk * KS];
   __shared__ __align__(16) IO khs[kChunk * KS];
   __shared__ __align__(16) IO vts[DP * VS];
 
   const int tid = threadIdx.x;
-  const int h = blockIdx.x;
-  const int64_t c = blockIdx.y;
-  const int b = blockIdx.z;
+  int64_t bh, c;
+  take_ticket(a, bh, c);
+  if (c >= a.nch) return;                 // uniform: every thread holds the same ticket
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
   const int nb = a.nb;
   const int64_t t0 = c * kChunk;
-  const int64_t bh = (int64_t)b * a.H + h;
 
   for (int idx = tid; idx < kChunk * nb; idx += 256) {
     int i = idx / nb, blk = idx % nb;
@@ -111,16 +177,13 @@ __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
     *reinterpret_cast<f32x4*>(&gs[idx * 4]) = f32x4{g.w, g.x, g.y, g.z};
   }
   __syncthreads();
-  if (tid < nb) {
-    quat p = load_quat(a.carry + (bh * a.nch + c) * nb * 4 + tid * 4);
-    float* Pout = a.P + (bh * a.T + t0) * nb * 4 + tid * 4;
-    for (int i = 0; i < kChunk; ++i) {
-      float* slot = &gs[(i * nb + tid) * 4];
-      quat g = load_quat(slot);
-      store_quat(slot, p);
-      if (t0 + i < a.T) store_quat(Pout + (int64_t)i * nb * 4, p);
-      p = qmul(g, p);
-    }
+  if (tid < nb) chain_block<GT>(a, gs, cs, bh, c, tid);
+  __syncthreads();
+  for (int idx = tid; idx < kChunk * nb; idx += 256) {
+    const int i = idx / nb, blk = idx % nb;
+    const quat p = qmul(load_quat(&gs[idx * 4]), load_quat(&cs[blk * 4]));
+    store_quat(&gs[idx * 4], p);
+    if (t0 + i < a.T) store_quat(a.P + (bh * a.T + t0 + i) * nb * 4 + blk * 4, p);
   }
   __syncthreads();
   const IO* qin = reinterpret_cast<const IO*>(a.q) + h * a.q_hs;
@@ -203,15 +266,16 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   constexpr int E = 16 / sizeof(IO);
   constexpr int VS = kChunk + E;
   __shared__ __align__(16) float gs[kChunk * NB * 4];
+  __shared__ __align__(16) float cs[NB * 4];
   __shared__ __align__(16) IO vts[DP * VS];
 
   const int tid = threadIdx.x;
   const int i = tid / NG, g = tid % NG;
-  const int h = blockIdx.x;
-  const int64_t c = blockIdx.y;
-  const int b = blockIdx.z;
+  int64_t bh, c;
+  take_ticket(a, bh, c);
+  if (c >= a.nch) return;                 // uniform: every thread holds the same ticket
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
   const int64_t t0 = c * kChunk, t = t0 + i;
-  const int64_t bh = (int64_t)b * a.H + h;
 
   // ---- all global loads first ----
   float gq[24], gk[24], qv[24], kv[24], vv[24];
@@ -247,19 +311,20 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
     *reinterpret_cast<f32x4*>(&gs[(i * NB + 8 * g + j) * 4]) = f32x4{q.w, q.x, q.y, q.z};
   });
   __syncthreads();
-  // ---- chain: one thread per block, P_t from the chunk carry ----
-  if (tid < NB) {
-    quat p = load_quat(a.carry + (bh * a.nch + c) * NB * 4 + tid * 4);
-    float* Pout = a.P + (bh * a.T + t0) * NB * 4 + tid * 4;
-    int n = (int)(a.T - t0 < kChunk ? a.T - t0 : kChunk);
-#pragma unroll 4
-    for (int r = 0; r < n; ++r) {
-      float* slot = &gs[(r * NB + tid) * 4];
-      quat gl = load_quat(slot);
-      store_quat(slot, p);
-      store_quat(Pout + (int64_t)r * NB * 4, p);
-      p = qmul(gl, p);
-    }
+  // ---- local prefixes and the chained carry (one thread per block) ----
+  if (tid < NB) chain_block<GT>(a, gs, cs, bh, c, tid);
+  __syncthreads();
+  // ---- P_t = L_r C for the tile's 64 x NB (token, block) slots: slot
+  // j*NT + tid in step j, so each store instruction writes whole contiguous
+  // rows of P; the results also replace L_r in LDS for the transport ----
+  {
+    float* Pout = a.P + (bh * a.T + t0) * NB * 4;
+    static_for<64 * NB / NT>([&](auto j) {
+      const int slot = j * NT + tid, r = slot / NB, blk = slot % NB;
+      const quat p = qmul(load_quat(&gs[slot * 4]), load_quat(&cs[blk * 4]));
+      store_quat(&gs[slot * 4], p);
+      if (t0 + r < a.T) store_quat(Pout + slot * 4, p);
+    });
   }
   __syncthreads();
   // ---- transport: kh row to global, vh into the transposed tile ----
@@ -296,11 +361,10 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
 template <typename IO, typename GT>
 hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
   const int tpb = 256;
-  int64_t n1 = (int64_t)a.B * a.nch * a.H * a.nb;
-  int64_t n2 = (int64_t)a.B * a.H * a.nb;
-  if (n1 > 0) hipLaunchKernelGGL(chunk_totals<GT>, dim3((n1 + tpb - 1) / tpb), dim3(tpb), 0, s, a);
-  if (n2 > 0) hipLaunchKernelGGL(chunk_carry<GT>, dim3((n2 + tpb - 1) / tpb), dim3(tpb), 0, s, a);
-  dim3 grid(a.H, (unsigned)a.nch, a.B);
+  const int64_t n_pairs = (int64_t)a.B * a.H * a.nch * a.nb * 2;    // 64-bit words of incl
+  hipLaunchKernelGGL(scan_reset, dim3((unsigned)((n_pairs + tpb - 1) / tpb > 0 ? (n_pairs + tpb - 1) / tpb : 1)),
+                     dim3(tpb), 0, s, reinterpret_cast<uint64_t*>(a.incl), n_pairs, a.ticket);
+  const dim3 grid((unsigned)((int64_t)a.B * a.H * a.nch));
   if (a.wide) {
     switch (a.d) {
       case 48: hipLaunchKernelGGL((chunk_apply_wide<IO, GT, 2, 64>), grid, dim3(128), 0, s, a); break;

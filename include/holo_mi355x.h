@@ -109,7 +109,10 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  *                               P_0 = I, P_{t+1} = G_t P_t   (:89-94)
  *   hol  (B, H, nb, 4)         fp32 holonomy G_close P_{T-1} (:95), or NULL.
  * The scan composes within chunks of 64 links and re-anchors each chunk on the
- * product of all earlier chunks.
+ * product of all earlier chunks, which each chunk's workgroup publishes for
+ * the next one in `workspace` (a chained scan): the inputs are read once. The
+ * workspace is cleared by the call itself (a fill kernel on `stream`); two
+ * calls that share one workspace must not run concurrently.
  */
 HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
                        int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
