@@ -12,11 +12,12 @@
 // one pass over the inputs in chunks of 64 links, one workgroup per
 // (b, h, chunk):
 //   1. link quaternions of the chunk's links -> LDS;
-//   2. one thread per block composes them from the identity (local prefixes
-//      L_r and the chunk product T_c), waits for the product of all earlier
+//   2. prefixes within the chunk over all threads (8 segments of 8 links per
+//      block), the chunk product T_c, a wait for the product of all earlier
 //      chunks C = incl[c-1] published by the previous chunk's workgroup, and
-//      publishes incl[c] = T_c C (a chained scan through the workspace);
-//   3. all threads: P_t = L_r C, written to P, and the transported qh, kh, vh.
+//      incl[c] = T_c C published for the next one (a chained scan through the
+//      workspace);
+//   3. all threads: P_t, written to P, and the transported qh, kh, vh.
 // Workgroups take chunks in ticket order (a global counter), chunk-major, so a
 // chunk only ever waits on a chunk that was handed out earlier and is running
 // or done: the wait always ends. Its polls are bounded anyway; a time-out
@@ -115,36 +116,67 @@ __device__ inline quat wait_prefix(const ScanArgs& a, int64_t bh, int64_t c, int
   return quat{nan, nan, nan, nan};
 }
 
-// Step 2 of the scan for one block (thread blk < nb): gs holds the chunk's
-// link quaternions (slot r = link t0 + r, identity past T-2); on return slot r
-// holds the local prefix L_r and cs[blk] the carry C (product of all earlier
-// chunks). Also writes the holonomy from the last chunk.
+// Steps 2-3 of the scan, all threads of the workgroup (thread tid < 8*nb
+// owns segment seg = tid / nb, links 8seg .. 8seg+7, of block blk = tid % nb).
+// On entry gs slot (r, blk) holds the link quaternion of link t0 + r
+// (identity past T-2); on return it holds P_{t0+r}, P is written for
+// t0 + r < T, the chunk's inclusive prefix is published and, from the last
+// chunk, the holonomy is written. Association (fixed, so results do not
+// depend on timing): segment-local prefixes, then the product E of the
+// earlier segments, then P = (segment prefix) (E C) with C the product of all
+// earlier chunks. ss: 8*nb quaternions of LDS, cs: nb.
 template <typename GT>
-__device__ inline void chain_block(const ScanArgs& a, float* gs, float* cs, int64_t bh, int64_t c, int blk) {
+__device__ inline void chunk_prefix(const ScanArgs& a, float* gs, float* ss, float* cs, int64_t bh, int64_t c,
+                                    int tid) {
   const int nb = a.nb;
-  quat p = qident();
-  for (int r = 0; r < kChunk; ++r) {
-    float* slot = &gs[(r * nb + blk) * 4];
-    quat g = load_quat(slot);
-    store_quat(slot, p);
-    p = qmul(g, p);
+  const int seg = tid / (nb > 0 ? nb : 1), blk = tid - seg * nb;
+  const bool act = tid < 8 * nb;
+  if (act) {
+    quat p = qident();
+    for (int r = 8 * seg; r < 8 * seg + 8; ++r) {       // segment-local exclusive prefixes
+      float* slot = &gs[(r * nb + blk) * 4];
+      const quat g = load_quat(slot);
+      store_quat(slot, p);
+      p = qmul(g, p);
+    }
+    store_quat(&ss[(seg * nb + blk) * 4], p);           // segment product
   }
-  // C = product of chunks 0..c-1; publish the product of chunks 0..c
-  const quat C = c == 0 ? qident() : wait_prefix(a, bh, c, blk);
-  if (c + 1 < a.nch) put_quat(a.incl + ((bh * a.nch + c) * nb + blk) * 4, qmul(p, C));
-  store_quat(&cs[blk * 4], C);
-  if (a.hol && c == a.nch - 1) {                       // Hol = G_close P_{T-1}
+  __syncthreads();
+  quat E = qident();                                    // product of the earlier segments
+  if (act) {
+    for (int k = 0; k < seg; ++k) E = qmul(load_quat(&ss[(k * nb + blk) * 4]), E);
+    if (seg == 7) {
+      const quat Tc = qmul(load_quat(&ss[(7 * nb + blk) * 4]), E);       // chunk product
+      const quat C = c == 0 ? qident() : wait_prefix(a, bh, c, blk);
+      if (c + 1 < a.nch) put_quat(a.incl + ((bh * a.nch + c) * nb + blk) * 4, qmul(Tc, C));
+      store_quat(&cs[blk * 4], C);
+    }
+  }
+  __syncthreads();
+  if (act) {
+    const quat X = qmul(E, load_quat(&cs[blk * 4]));
+    const int64_t t0 = c * kChunk;
+    float* Pout = a.P + (bh * a.T + t0) * nb * 4 + blk * 4;
+    for (int r = 8 * seg; r < 8 * seg + 8; ++r) {       // lanes of a wave: whole rows of P
+      float* slot = &gs[(r * nb + blk) * 4];
+      const quat p = qmul(load_quat(slot), X);
+      store_quat(slot, p);
+      if (t0 + r < a.T) store_quat(Pout + (int64_t)r * nb * 4, p);
+    }
+  }
+  __syncthreads();
+  if (a.hol && c == a.nch - 1 && tid < nb) {            // Hol = G_close P_{T-1}
     const int b = (int)(bh / a.H), h = (int)(bh % a.H);
     const int64_t n = a.T - c * kChunk;
-    quat pl = qmul(load_quat(&gs[((n - 1) * nb + blk) * 4]), C);
-    store_quat(a.hol + (bh * nb + blk) * 4, qmul(link_quat<GT>(a, b, h, blk, a.T - 1), pl));
+    const quat pl = load_quat(&gs[((n - 1) * nb + tid) * 4]);
+    store_quat(a.hol + (bh * nb + tid) * 4, qmul(link_quat<GT>(a, b, h, tid, a.T - 1), pl));
   }
 }
 
 // One workgroup per (b, h, chunk) tile of 64 tokens (any d <= 96):
 //   1. all threads: link quaternions g_t of the tile's links -> LDS;
-//   2. one thread per block: local prefixes and the chained carry (chain_block);
-//   3. all threads: P_t = L_r C -> global P and LDS; qh = P^T q, kh = P^T k
+//   2-3. all threads: prefixes, the chained carry and P_t (chunk_prefix) ->
+//      global P and LDS; qh = P^T q, kh = P^T k
 //      and vh = P^T v into row-major qh, kh tiles and a transposed vh tile in
 //      LDS (zero padding);
 //   4. the tiles leave with 16-byte stores of whole rows (each tile is one
@@ -157,6 +189,7 @@ __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
   constexpr int NBM = DP / 3;           // blocks held in LDS (nb <= NBM)
   constexpr int NBX = (DP + 2) / 3;     // 3-dim groups covering DP
   __shared__ __align__(16) float gs[kChunk * NBM * 4];
+  __shared__ __align__(16) float ss[8 * NBM * 4];
   __shared__ __align__(16) float cs[NBM * 4];
   __shared__ __align__(16) IO qhs[kChunk * KS];
   __shared__ __align__(16) IO khs[kChunk * KS];
@@ -177,15 +210,7 @@ __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
     *reinterpret_cast<f32x4*>(&gs[idx * 4]) = f32x4{g.w, g.x, g.y, g.z};
   }
   __syncthreads();
-  if (tid < nb) chain_block<GT>(a, gs, cs, bh, c, tid);
-  __syncthreads();
-  for (int idx = tid; idx < kChunk * nb; idx += 256) {
-    const int i = idx / nb, blk = idx % nb;
-    const quat p = qmul(load_quat(&gs[idx * 4]), load_quat(&cs[blk * 4]));
-    store_quat(&gs[idx * 4], p);
-    if (t0 + i < a.T) store_quat(a.P + (bh * a.T + t0 + i) * nb * 4 + blk * 4, p);
-  }
-  __syncthreads();
+  chunk_prefix<GT>(a, gs, ss, cs, bh, c, tid);
   const IO* qin = reinterpret_cast<const IO*>(a.q) + h * a.q_hs;
   const IO* kin = reinterpret_cast<const IO*>(a.k) + h * a.k_hs;
   const IO* vin = reinterpret_cast<const IO*>(a.v) + h * a.v_hs;
@@ -265,7 +290,11 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   constexpr int D = 24 * NG;            // head dimension
   constexpr int E = 16 / sizeof(IO);
   constexpr int VS = kChunk + E;
-  __shared__ __align__(16) float gs[kChunk * NB * 4];
+  constexpr int KS = DP + E;             // row stride of the staged qh / kh tiles
+  constexpr int GS_BYTES = kChunk * NB * 16, QK_BYTES = 2 * kChunk * KS * (int)sizeof(IO);
+  // link quaternions / P, later reused for the transported qh and kh tiles
+  __shared__ __align__(16) float gs[(GS_BYTES > QK_BYTES ? GS_BYTES : QK_BYTES) / 4];
+  __shared__ __align__(16) float ss[8 * NB * 4];
   __shared__ __align__(16) float cs[NB * 4];
   __shared__ __align__(16) IO vts[DP * VS];
 
@@ -311,22 +340,8 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
     *reinterpret_cast<f32x4*>(&gs[(i * NB + 8 * g + j) * 4]) = f32x4{q.w, q.x, q.y, q.z};
   });
   __syncthreads();
-  // ---- local prefixes and the chained carry (one thread per block) ----
-  if (tid < NB) chain_block<GT>(a, gs, cs, bh, c, tid);
-  __syncthreads();
-  // ---- P_t = L_r C for the tile's 64 x NB (token, block) slots: slot
-  // j*NT + tid in step j, so each store instruction writes whole contiguous
-  // rows of P; the results also replace L_r in LDS for the transport ----
-  {
-    float* Pout = a.P + (bh * a.T + t0) * NB * 4;
-    static_for<64 * NB / NT>([&](auto j) {
-      const int slot = j * NT + tid, r = slot / NB, blk = slot % NB;
-      const quat p = qmul(load_quat(&gs[slot * 4]), load_quat(&cs[blk * 4]));
-      store_quat(&gs[slot * 4], p);
-      if (t0 + r < a.T) store_quat(Pout + slot * 4, p);
-    });
-  }
-  __syncthreads();
+  // ---- prefixes: gs slots become P_t, P written, carry chained ----
+  chunk_prefix<GT>(a, gs, ss, cs, bh, c, tid);
   // ---- transport: kh row to global, vh into the transposed tile ----
   static_for<8>([&](auto j) {
     rot3 R = qmat(load_quat(&gs[(i * NB + 8 * g + j) * 4]));
@@ -338,20 +353,31 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
     rot_t_apply(R, vv[3 * j], vv[3 * j + 1], vv[3 * j + 2], y0, y1, y2);
     vv[3 * j] = y0; vv[3 * j + 1] = y1; vv[3 * j + 2] = y2;
   });
-  IO* qrow = reinterpret_cast<IO*>(a.qh) + (bh * a.Tp + t) * DP;
-  IO* krow = reinterpret_cast<IO*>(a.kh) + (bh * a.Tp + t) * DP;
-  store_row<IO, 24>(qrow + 24 * g, qv);
-  store_row<IO, 24>(krow + 24 * g, kv);
+  // ---- stage the three transported tiles in LDS (the P slots are free once
+  // every thread has read its own), then write each with whole 16-byte rows
+  // per lane: the qh and kh tiles of a chunk are contiguous 64 x DP blocks ----
+  __syncthreads();
+  IO* qts = reinterpret_cast<IO*>(gs);
+  IO* kts = qts + kChunk * KS;
+  store_row<IO, 24>(qts + i * KS + 24 * g, qv);
+  store_row<IO, 24>(kts + i * KS + 24 * g, kv);
   if (DP > D && g == NG - 1) {
     float z[DP > D ? DP - D : E];
     static_for<(DP > D ? DP - D : E)>([&](auto j) { z[j] = 0.f; });
     if constexpr (DP > D) {
-      store_row<IO, DP - D>(qrow + D, z);
-      store_row<IO, DP - D>(krow + D, z);
+      store_row<IO, DP - D>(qts + i * KS + D, z);
+      store_row<IO, DP - D>(kts + i * KS + D, z);
     }
   }
   static_for<24>([&](auto j) { vts[(24 * g + j) * VS + i] = from_f32<IO>(vv[j]); });
   __syncthreads();
+  u32x4* qdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.qh) + (bh * a.Tp + t0) * DP);
+  u32x4* kdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.kh) + (bh * a.Tp + t0) * DP);
+  constexpr int KR = DP / E;
+  for (int idx = tid; idx < kChunk * KR; idx += NT) {
+    qdst[idx] = *reinterpret_cast<const u32x4*>(&qts[(idx / KR) * KS + (idx % KR) * E]);
+    kdst[idx] = *reinterpret_cast<const u32x4*>(&kts[(idx / KR) * KS + (idx % KR) * E]);
+  }
   u32x4* vdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.vh_t) + (bh * a.nch + c) * DP * kChunk);
   constexpr int VR = kChunk / E;
   for (int idx = tid; idx < DP * VR; idx += NT)
