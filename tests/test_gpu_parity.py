@@ -160,6 +160,9 @@ def test_cfg1_fp32_against_reference(golden_dir):
     assert np.abs(yn.sum(-1) - z32["y_row_sum"]).max() <= 1e-5 * D
     assert np.abs(np.abs(yn).sum(-1) - z32["y_row_abs"]).max() <= 1e-5 * D
     y64 = R.forward_blocks(x, W, H, 0.05)
+    print(f"cfg1: max-abs vs reference fp32 rows {np.abs(yn[:rows] - z32['y_rows']).max():.3e}, "
+          f"vs reference fp64 rows {np.abs(yn[:rows] - z64['y_rows']).max():.3e}, "
+          f"vs fp64 oracle (all rows) {np.abs(yn - y64).max():.3e}")
     assert np.abs(yn - y64).max() <= 1e-5
 
 
