@@ -40,12 +40,12 @@ CONFIGS = {
 }
 
 
-def scan_bytes_per_token_head(d: int, io_bytes: int, gen_bytes: int = 4) -> int:
+def scan_bytes_per_token_head(d: int, io_bytes: int, gen_bytes: int = 4, quat_bytes: int = 16) -> int:
     """Algorithmic HBM bytes of the scan stage per (token, head): read the two
     generator halves gq, gk (3*nb each, fp32) and q, k, v (d each); write qh,
-    kh, vh (d each) and P (nb quaternions, fp32)."""
+    kh, vh (d each) and P (nb quaternions: 16 B in fp32, 8 B as int16)."""
     nb = d // 3
-    return 2 * 3 * nb * gen_bytes + 3 * d * io_bytes + 3 * d * io_bytes + nb * 16
+    return 2 * 3 * nb * gen_bytes + 3 * d * io_bytes + 3 * d * io_bytes + nb * quat_bytes
 
 
 def attention_core_flops(B, T, H, d) -> float:
@@ -215,6 +215,9 @@ def main():
         return
     mask = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
 
+    pfmt = m._p_format(x, False)
+    qbytes = 8 if pfmt == "snorm16" else 16
+
     def staged(ev=None):
         """The module's forward, stage by stage (same kernels and order)."""
         if ev is not None:
@@ -222,7 +225,7 @@ def main():
         q, k, v, gq, gk = m._link_inputs(x)
         if ev is not None:
             ev[1].record()
-        qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, m.edge_scale)
+        qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, m.edge_scale, p_format=pfmt)
         if ev is not None:
             ev[2].record()
         o = kernels.attention(qh, kh, vh_t, P, d, m.scale)
@@ -277,7 +280,7 @@ def main():
     fl_core = attention_core_flops(B, T, H, d)
     fl_proj = projection_flops(B, T, D, m_total)
     io_bytes = 2 if dt == torch.bfloat16 else 4
-    scan_bytes = scan_bytes_per_token_head(d, io_bytes) * B * T * H
+    scan_bytes = scan_bytes_per_token_head(d, io_bytes, quat_bytes=qbytes) * B * T * H
     core_peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
     core_tflops = fl_core / (stage_ms[2] * 1e-3) / 1e12
     scan_gbs = scan_bytes / (stage_ms[1] * 1e-3) / 1e9
@@ -314,7 +317,8 @@ def main():
                           "frac": scan_gbs / PEAK_HBM_GBS,
                           "traffic": traffic_from_profile(args.config, ["scan_reset", "chunk_apply"]),
                           "bytes_per_launch": scan_bytes,
-                          "bytes_per_token_head": scan_bytes_per_token_head(d, io_bytes)},
+                          "bytes_per_token_head": scan_bytes_per_token_head(d, io_bytes, quat_bytes=qbytes),
+                          "p_format": pfmt},
     }
     if not args.no_cpu_baseline:
         W = {k: v for k, v in inp.items()}

@@ -163,6 +163,14 @@ class PathOrderedGeometricMHA(nn.Module):
             gk = None
         return qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], gq, gk
 
+    @staticmethod
+    def _p_format(x: torch.Tensor, return_geometry: bool) -> str:
+        """Storage of the prefix rotations between the scan and the attention
+        epilogue: int16 quaternions (half the bytes, quantisation ~6e-5 of a
+        rotated vector, well below bf16 rounding) on the bf16 path, fp32 for
+        fp32 runs and whenever the geometry is returned."""
+        return "snorm16" if x.dtype == torch.bfloat16 and not return_geometry else "f32"
+
     def forward(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor] = None,
                 return_geometry: bool = False
                 ) -> Tuple[torch.Tensor, Optional[Dict[str, torch.Tensor]]]:
@@ -176,7 +184,8 @@ class PathOrderedGeometricMHA(nn.Module):
         with torch.no_grad():
             q, k, v, gq, gk = self._link_inputs(x)
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
-                                                     want_hol=return_geometry)
+                                                     want_hol=return_geometry,
+                                                     p_format=self._p_format(x, return_geometry))
             o = kernels.attention(qh, kh, vh_t, P, self.d, self.scale)
             y = F.linear(o.view(B, L, D), self.out.weight)
         if track:

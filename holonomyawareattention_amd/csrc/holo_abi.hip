@@ -54,7 +54,7 @@ extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (2 << 16) | 1; }
+int holo_abi_version(void) { return (3 << 16) | 0; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -66,7 +66,7 @@ size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d) {
 }
 
 int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
-                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype, int p_format,
                        const void* gq, int64_t gq_rs, int64_t gq_hs,
                        const void* gk, int64_t gk_rs, int64_t gk_hs,
                        const void* q, int64_t q_rs, int64_t q_hs,
@@ -85,6 +85,8 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
     return fail(HOLO_ERR_UNSUPPORTED, "fp32 keys/values need an fp32 generator");
   if (gen_mode != HOLO_GEN_ADDITIVE && gen_mode != HOLO_GEN_DIRECT)
     return fail(HOLO_ERR_INVALID_ARG, "gen_mode %d unknown", gen_mode);
+  if (p_format != HOLO_QUAT_F32 && p_format != HOLO_QUAT_SNORM16)
+    return fail(HOLO_ERR_INVALID_ARG, "p_format %d is not HOLO_QUAT_F32 or HOLO_QUAT_SNORM16", p_format);
   const int nb = d / 3;
   if (!gq || !q || !k || !v || !qh || !kh || !vh_t || (nb > 0 && !P))
     return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
@@ -117,6 +119,7 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
   a.k = k; a.k_rs = k_rs; a.k_hs = k_hs;
   a.v = v; a.v_rs = v_rs; a.v_hs = v_hs;
   a.qh = qh; a.kh = kh; a.vh_t = vh_t; a.P = P; a.hol = hol;
+  a.p_format = p_format;
   {
     // 16-byte vector rows: every row start of gq/gk/k/v must be 16-byte aligned
     const size_t ge = gen_dtype == HOLO_F32 ? 4 : 2, ie = io_dtype == HOLO_F32 ? 4 : 2;
@@ -141,14 +144,16 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
   return HOLO_OK;
 }
 
-int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
-                  const void* qh, const void* kh, const void* vh_t, const float* P,
+int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float scale,
+                  const void* qh, const void* kh, const void* vh_t, const void* P,
                   void* o, int64_t o_rs, int64_t o_hs, void* stream) {
   g_last_error.clear();
   int rc = check_common(B, T, H, d);
   if (rc) return rc;
   if (dtype != HOLO_F32 && dtype != HOLO_BF16)
     return fail(HOLO_ERR_INVALID_ARG, "dtype %d is not HOLO_F32 or HOLO_BF16", dtype);
+  if (p_format != HOLO_QUAT_F32 && p_format != HOLO_QUAT_SNORM16)
+    return fail(HOLO_ERR_INVALID_ARG, "p_format %d is not HOLO_QUAT_F32 or HOLO_QUAT_SNORM16", p_format);
   const int nb = d / 3;
   if (!qh || !kh || !vh_t || !o || (nb > 0 && !P))
     return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
@@ -167,6 +172,7 @@ int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
   a.scale_log2 = scale * 1.4426950408889634f;
   a.qh = qh; a.kh = kh; a.vh_t = vh_t; a.P = P;
   a.o = o; a.o_rs = o_rs; a.o_hs = o_hs;
+  a.p_format = p_format;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = dtype == HOLO_F32 ? holo::launch_attn<float>(a, s)
                                    : holo::launch_attn<holo::bf16>(a, s);

@@ -91,7 +91,7 @@ template <typename T, int DP> struct AttnCfg {
 // of tile j+1, then runs the softmax and PV MFMAs of tile j (so the VALU work
 // overlaps the matrix core), stores tile j+2 into the free stage, issues the
 // loads of tile j+3 and ends with the tile's only barrier.
-template <typename T, int DP>
+template <typename T, int DP, bool PQ16>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 attn_fwd(AttnArgs a) {
   using C = AttnCfg<T, DP>;
@@ -280,22 +280,25 @@ attn_fwd(AttnArgs a) {
     }
   };
   // quaternions of the epilogue items (row, 8 consecutive 3-dim groups); a
-  // row's 8 quaternions are 128 contiguous bytes
-  f32x4 pq[C::EPI][8];
+  // row's 8 quaternions are 128 contiguous bytes in fp32, 64 in int16
+  typedef typename std::conditional<PQ16, u32x2, f32x4>::type pq_t;
+  const pq_t pq_ident = [] {
+    if constexpr (PQ16) return u32x2{1u, 0u};            // (1, 0, 0, 0)
+    else return f32x4{1.f, 0.f, 0.f, 0.f};
+  }();
+  pq_t pq[C::EPI][8];
   auto load_epilogue_quats = [&](auto first, auto count) {
     static_for<decltype(count)::value>([&](auto k) {
       constexpr int it = decltype(first)::value + decltype(k)::value;
       const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
       const int64_t t = q0 + r;
       const bool row_ok = idx < kBM * C::NG8 && t < a.T;
-      const float* base = a.P + ((bh * a.T + t) * a.nb + 8 * gi) * 4;
+      const pq_t* base = reinterpret_cast<const pq_t*>(
+          reinterpret_cast<const char*>(a.P) + ((bh * a.T + t) * a.nb + 8 * gi) * (int64_t)sizeof(pq_t));
       if (row_ok && 8 * gi + 8 <= a.nb) {
-        static_for<8>([&](auto jb) { pq[it][jb] = reinterpret_cast<const f32x4*>(base)[jb]; });
+        static_for<8>([&](auto jb) { pq[it][jb] = base[jb]; });
       } else {
-        static_for<8>([&](auto jb) {
-          pq[it][jb] = (row_ok && 8 * gi + jb < a.nb) ? reinterpret_cast<const f32x4*>(base)[jb]
-                                                      : f32x4{1.f, 0.f, 0.f, 0.f};
-        });
+        static_for<8>([&](auto jb) { pq[it][jb] = (row_ok && 8 * gi + jb < a.nb) ? base[jb] : pq_ident; });
       }
     });
   };
@@ -342,8 +345,10 @@ attn_fwd(AttnArgs a) {
     static_for<8>([&](auto jb) {
       if (8 * gi + jb < a.nb) {
         float y0, y1, y2;
-        quat_rotate(quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]},
-                    u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
+        quat qr;
+        if constexpr (PQ16) qr = unpack_quat_snorm16(pq[it][jb]);
+        else qr = quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]};
+        quat_rotate(qr, u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
         u[3 * jb] = y0; u[3 * jb + 1] = y1; u[3 * jb + 2] = y2;
       }
     });
@@ -364,26 +369,31 @@ attn_fwd(AttnArgs a) {
   });
 }
 
-template <typename T, int DP>
+template <typename T, int DP, bool PQ16>
 static hipError_t launch_attn_dp(const AttnArgs& a, hipStream_t s) {
   using C = AttnCfg<T, DP>;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&attn_fwd<T, DP>), hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::lds);
+      reinterpret_cast<const void*>(&attn_fwd<T, DP, PQ16>), hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::lds);
   if (attr != hipSuccess) return attr;
   const int64_t ntile = (a.T + kBM - 1) / kBM;
-  hipLaunchKernelGGL((attn_fwd<T, DP>), dim3((unsigned)(a.B * a.H * ntile)), dim3(kThreads),
+  hipLaunchKernelGGL((attn_fwd<T, DP, PQ16>), dim3((unsigned)(a.B * a.H * ntile)), dim3(kThreads),
                      C::lds, s, a);
   return hipGetLastError();
 }
 
-template <typename T>
-hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
+template <typename T, bool PQ16>
+static hipError_t launch_attn_pf(const AttnArgs& a, hipStream_t s) {
   switch (a.Dp) {
-    case 32: return launch_attn_dp<T, 32>(a, s);
-    case 64: return launch_attn_dp<T, 64>(a, s);
-    case 96: return launch_attn_dp<T, 96>(a, s);
+    case 32: return launch_attn_dp<T, 32, PQ16>(a, s);
+    case 64: return launch_attn_dp<T, 64, PQ16>(a, s);
+    case 96: return launch_attn_dp<T, 96, PQ16>(a, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <typename T>
+hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
+  return a.p_format ? launch_attn_pf<T, true>(a, s) : launch_attn_pf<T, false>(a, s);
 }
 
 template hipError_t launch_attn<float>(const AttnArgs&, hipStream_t);

@@ -137,4 +137,20 @@ __device__ inline void store_quat(float* p, const quat& q) {
   *reinterpret_cast<f32x4*>(p) = v;
 }
 
+// Compact storage of a rotation: round(32767 * q / |q|) per component as
+// int16, 8 bytes. |q / |q|| components are at most 1, so no value leaves
+// [-32767, 32767].
+__device__ inline void store_quat_snorm16(short* p, const quat& q) {
+  const float s = 32767.f * __builtin_amdgcn_rsqf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+  auto cv = [&](float v) { return (unsigned)(int)__builtin_rintf(v * s) & 0xffffu; };
+  *reinterpret_cast<u32x2*>(p) = u32x2{cv(q.w) | (cv(q.x) << 16), cv(q.y) | (cv(q.z) << 16)};
+}
+
+// The stored integers of store_quat_snorm16 as a quaternion (norm ~32767) of
+// the same rotation: the homogeneous rotation map divides by |q|^2.
+__device__ inline quat unpack_quat_snorm16(u32x2 v) {
+  return quat{(float)(short)(v[0] & 0xffffu), (float)((int)v[0] >> 16),
+              (float)(short)(v[1] & 0xffffu), (float)((int)v[1] >> 16)};
+}
+
 }  // namespace holo

@@ -15,6 +15,7 @@ struct ScanArgs {
   const void* k; int64_t k_rs, k_hs;
   const void* v; int64_t v_rs, v_hs;
   void* qh; void* kh; void* vh_t; float* P; float* hol;
+  int p_format;    // 0: fp32 quaternions, 1: int16 (round(32767 q/|q|))
   int wide;        // 16-byte row path of the scan (d in {48, 72, 96}, aligned rows)
   float* incl;     // (B, H, nch, nb, 4) prefix product through each chunk (chained-scan state)
   unsigned* ticket;  // [0]: chunk ticket counter, [1]: carry-wait time-out flag
@@ -25,8 +26,9 @@ struct AttnArgs {
   int B, H, d, nb, Dp;
   int64_t T, Tp, nch;
   float scale_log2;                       // scale * log2(e)
-  const void* qh; const void* kh; const void* vh_t; const float* P;
+  const void* qh; const void* kh; const void* vh_t; const void* P;
   void* o; int64_t o_rs, o_hs;
+  int p_format;    // 0: fp32 quaternions, 1: int16 (round(32767 q/|q|))
 };
 
 template <typename IO, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);

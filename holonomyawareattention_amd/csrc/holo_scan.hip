@@ -156,12 +156,15 @@ __device__ inline void chunk_prefix(const ScanArgs& a, float* gs, float* ss, flo
   if (act) {
     const quat X = qmul(E, load_quat(&cs[blk * 4]));
     const int64_t t0 = c * kChunk;
-    float* Pout = a.P + (bh * a.T + t0) * nb * 4 + blk * 4;
+    const int64_t q0 = (bh * a.T + t0) * nb + blk;      // quaternion index of (t0, blk)
     for (int r = 8 * seg; r < 8 * seg + 8; ++r) {       // lanes of a wave: whole rows of P
       float* slot = &gs[(r * nb + blk) * 4];
       const quat p = qmul(load_quat(slot), X);
       store_quat(slot, p);
-      if (t0 + r < a.T) store_quat(Pout + (int64_t)r * nb * 4, p);
+      if (t0 + r < a.T) {
+        if (a.p_format) store_quat_snorm16(reinterpret_cast<short*>(a.P) + (q0 + (int64_t)r * nb) * 4, p);
+        else store_quat(a.P + (q0 + (int64_t)r * nb) * 4, p);
+      }
     }
   }
   __syncthreads();

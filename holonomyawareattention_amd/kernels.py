@@ -17,6 +17,8 @@ import torch
 from . import _lib
 
 _DT = {torch.float32: _lib.HOLO_F32, torch.bfloat16: _lib.HOLO_BF16}
+# storage of P: name -> (holo_quat_format, torch dtype of the (B, H, T, nb, 4) tensor)
+_PFMT = {"f32": (_lib.HOLO_QUAT_F32, torch.float32), "snorm16": (_lib.HOLO_QUAT_SNORM16, torch.int16)}
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -54,13 +56,16 @@ def padded_seq_len(T: int) -> int:
 
 
 def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor,
-              gk: Optional[torch.Tensor], edge_scale: float, want_hol: bool = False
+              gk: Optional[torch.Tensor], edge_scale: float, want_hol: bool = False,
+              p_format: str = "f32"
               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """q, k, v: (B,T,H,d) views; gq, gk: (B,T,H,3*nb) views (gk None: gq is the
     full link parameter g and a_t = edge_scale * g_t). The generator may be
     fp32 with bf16 q/k/v (link parameters are composed in fp32 either way).
-    Returns qh, kh (B,H,Tp,Dp), vh_t (B,H,Tp/64,Dp,64), P (B,H,T,nb,4) fp32,
-    Hol (B,H,nb,4) fp32 or None."""
+    Returns qh, kh (B,H,Tp,Dp), vh_t (B,H,Tp/64,Dp,64), P (B,H,T,nb,4) and
+    Hol (B,H,nb,4) fp32 or None. P is fp32 quaternions (p_format "f32") or
+    round(32767 q/|q|) as int16 ("snorm16", half the bytes; the attention
+    epilogue uses either, quat_to_dense takes fp32)."""
     lib = _lib.load()
     B, T, H, d = k.shape
     nb = d // 3
@@ -88,13 +93,15 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     qh = torch.empty((B, H, Tp, Dp), dtype=dt, device=dev)
     kh = torch.empty((B, H, Tp, Dp), dtype=dt, device=dev)
     vh_t = torch.empty((B, H, Tp // 64, Dp, 64), dtype=dt, device=dev)
-    P = torch.empty((B, H, T, nb, 4), dtype=torch.float32, device=dev)
+    if p_format not in _PFMT:
+        raise ValueError(f"geom_scan: p_format must be one of {sorted(_PFMT)}")
+    P = torch.empty((B, H, T, nb, 4), dtype=_PFMT[p_format][1], device=dev)
     hol = torch.empty((B, H, nb, 4), dtype=torch.float32, device=dev) if want_hol else None
     ws_bytes = int(lib.holo_geom_scan_workspace_size(B, T, H, d))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     rc = lib.holo_geom_scan_fwd(
         B, T, H, d, _lib.HOLO_GEN_DIRECT if gk is None else _lib.HOLO_GEN_ADDITIVE,
-        float(edge_scale), _DT[dt], _DT[gdt],
+        float(edge_scale), _DT[dt], _DT[gdt], _PFMT[p_format][0],
         _ptr(gq), gq_rs, gq_hs, _ptr(gk), gk_rs, gk_hs,
         _ptr(q), q_rs, q_hs, _ptr(k), k_rs, k_hs, _ptr(v), v_rs, v_hs,
         _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(hol),
@@ -123,7 +130,8 @@ def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.T
         raise ValueError("attention: kh does not match the geom_scan layout")
     if tuple(vh_t.shape) != (B, H, Tp // 64, Dp, 64) or not vh_t.is_contiguous() or vh_t.dtype != dt:
         raise ValueError("attention: vh_t does not match the geom_scan layout")
-    if tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous() or P.dtype != torch.float32:
+    pf = {torch.float32: _lib.HOLO_QUAT_F32, torch.int16: _lib.HOLO_QUAT_SNORM16}.get(P.dtype)
+    if tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous() or pf is None:
         raise ValueError("attention: P does not match the geom_scan layout")
     for t in (kh, vh_t, P):
         if t.device != dev:
@@ -133,7 +141,7 @@ def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.T
     elif out.dtype != dt or out.device != dev:
         raise ValueError("attention: out must match q's dtype and device")
     o_rs, o_hs = _token_view(out, B, T, H, d, "out")
-    rc = lib.holo_attn_fwd(B, T, H, d, _DT[dt], float(scale),
+    rc = lib.holo_attn_fwd(B, T, H, d, _DT[dt], pf, float(scale),
                            _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
                            _ptr(out), o_rs, o_hs, _stream(dev))
     _lib.check(rc, "holo_attn_fwd")

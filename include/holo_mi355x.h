@@ -65,6 +65,16 @@ typedef enum holo_dtype {
   HOLO_BF16 = 1
 } holo_dtype;
 
+/* Storage of the prefix rotations P (one quaternion per block and token). */
+typedef enum holo_quat_format {
+  /* (w, x, y, z) fp32, 16 bytes                                             */
+  HOLO_QUAT_F32 = 0,
+  /* round(32767 * q / |q|) as int16, 8 bytes: the rotation of a quaternion
+     does not depend on its norm, so the stored integers are used as they are;
+     quantisation moves a rotated vector by about 6e-5 of its length        */
+  HOLO_QUAT_SNORM16 = 1
+} holo_quat_format;
+
 typedef enum holo_gen_mode {
   /* a_t = edge_scale * (gq_t + gk_{(t+1) mod T})  (core/attention_fast_chunked.py:80-84) */
   HOLO_GEN_ADDITIVE = 0,
@@ -105,7 +115,8 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  *   vh_t (B, H, Tp/64, Dp, 64) io_dtype, key tiles of 64 stored transposed:
  *                               vh_t[b][h][t/64][c][t%64] = (P_t^T v_t)[c]
  *        Padding (t >= T or c >= d) is written as zero.
- *   P    (B, H, T, nb, 4)      fp32 quaternions of the prefix products
+ *   P    (B, H, T, nb, 4)      quaternions of the prefix products in `p_format`
+ *                               (fp32 or int16, holo_quat_format)
  *                               P_0 = I, P_{t+1} = G_t P_t   (:89-94)
  *   hol  (B, H, nb, 4)         fp32 holonomy G_close P_{T-1} (:95), or NULL.
  * The scan composes within chunks of 64 links and re-anchors each chunk on the
@@ -115,7 +126,7 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  * calls that share one workspace must not run concurrently.
  */
 HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
-                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype, int p_format,
                        const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
                        const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
                        const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -126,19 +137,20 @@ HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
 
 /*
  * Causal path-ordered attention on transported queries/keys/values.
- *   qh, kh, vh_t, P : as written by holo_geom_scan_fwd (same B, T, H, d, dtype)
+ *   qh, kh, vh_t, P : as written by holo_geom_scan_fwd (same B, T, H, d, dtype,
+ *                     p_format)
  *   o    : output, element (b, t, h, c) at o[(b*T + t)*o_row_stride + h*o_head_stride + c]
  *          o_i = P_i * sum_{j<=i} softmax_j(scale * qh_i . kh_j) * vh_j
  * dtype is the dtype of q, kh, vh_t and o (HOLO_BF16: bf16 MFMA with fp32
  * accumulation and softmax; HOLO_F32: fp32 MFMA throughout).
  */
-HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, float scale,
-                  const void* qh, const void* kh, const void* vh_t, const float* P,
+HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float scale,
+                  const void* qh, const void* kh, const void* vh_t, const void* P,
                   void* o, int64_t o_row_stride, int64_t o_head_stride,
                   void* stream);
 
 /*
- * Expand quaternions (n, nb, 4) to dense fp32 rotation matrices (n, d, d):
+ * Expand fp32 quaternions (n, nb, 4) to dense fp32 rotation matrices (n, d, d):
  * block b on dims 3b..3b+2, identity on the leftover dims.
  */
 HOLO_API int holo_quat_to_dense(int64_t n, int d, const float* quat, float* dense, void* stream);

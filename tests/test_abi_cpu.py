@@ -56,12 +56,12 @@ def test_version_and_layout_queries(lib):
 
 
 def _scan(lib, **kw):
-    args = dict(B=1, T=8, H=2, d=12, gen=0, es=0.1, io=_lib.HOLO_F32, gdt=_lib.HOLO_F32,
+    args = dict(B=1, T=8, H=2, d=12, gen=0, es=0.1, io=_lib.HOLO_F32, gdt=_lib.HOLO_F32, pf=_lib.HOLO_QUAT_F32,
                 gq=16, gk=16, q=16, k=16, v=16, qh=16, kh=16, vh=16, P=16, hol=None, ws=16, wsb=1 << 20,
                 rs=64, hs=24)
     args.update(kw)
     a = args
-    return lib.holo_geom_scan_fwd(a["B"], a["T"], a["H"], a["d"], a["gen"], a["es"], a["io"], a["gdt"],
+    return lib.holo_geom_scan_fwd(a["B"], a["T"], a["H"], a["d"], a["gen"], a["es"], a["io"], a["gdt"], a["pf"],
                                   a["gq"], a["rs"], a["hs"], a["gk"], a["rs"], a["hs"],
                                   a["q"], a["rs"], a["hs"], a["k"], a["rs"], a["hs"], a["v"], a["rs"], a["hs"],
                                   a["qh"], a["kh"], a["vh"], a["P"], a["hol"], a["ws"], a["wsb"], None)
@@ -72,6 +72,7 @@ def test_scan_argument_validation(lib):
     assert b"positive" in lib.holo_last_error()
     assert _scan(lib, d=200) == _lib.HOLO_ERR_UNSUPPORTED
     assert _scan(lib, io=7) == _lib.HOLO_ERR_INVALID_ARG
+    assert _scan(lib, pf=2) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, io=_lib.HOLO_F32, gdt=_lib.HOLO_BF16) == _lib.HOLO_ERR_UNSUPPORTED
     assert _scan(lib, k=None) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, gen=_lib.HOLO_GEN_ADDITIVE, gk=None) == _lib.HOLO_ERR_INVALID_ARG
@@ -84,12 +85,13 @@ def test_scan_argument_validation(lib):
 
 def test_attention_argument_validation(lib):
     f = lib.holo_attn_fwd
-    assert f(1, 0, 1, 12, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_BAD_SHAPE
-    assert f(1, 8, 1, 120, 0, 0.3, 16, 16, 16, 16, 16, 120, 120, None) == _lib.HOLO_ERR_UNSUPPORTED
-    assert f(1, 8, 1, 12, 0, 0.0, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 1, 12, 0, 0.3, None, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 2, 12, 0, 0.3, 16, 16, 16, 16, 16, 12, 4, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 1, 12, 5, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 0, 1, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_BAD_SHAPE
+    assert f(1, 8, 1, 120, 0, 0, 0.3, 16, 16, 16, 16, 16, 120, 120, None) == _lib.HOLO_ERR_UNSUPPORTED
+    assert f(1, 8, 1, 12, 0, 0, 0.0, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 0, 0, 0.3, None, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 2, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 4, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 5, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 0, 3, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
 
 
 def test_status_codes_map_to_reference_exceptions(lib):

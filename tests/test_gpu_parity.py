@@ -325,3 +325,32 @@ def test_cfg3_long_prefix_geometry():
           f"fp32 matrix scan (reference style, 64 chains): max|PtP-I| {np.abs(Ed).max():.3g}")
     assert ortho_entry <= 1e-4 and ortho_inf <= 3e-4
     assert err <= 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_compact_quaternion_format(dtype):
+    """P stored as round(32767 q/|q|) int16 (p_format "snorm16"): the same
+    rotations as the fp32 quaternions to the quantisation step, and the
+    attention output it gives stays within bf16-level error of the fp32-P one
+    (the rotation error is ~6e-5 of |o|, bf16 rounds at 4e-3)."""
+    B, T, D, H, es = 2, 300, 192, 2, 0.8
+    x, W = layer(28, B, T, D, H, dtype=dtype)
+    d = D // H
+    q, k, v, gq, gk = _projections(x, W, H, dtype)
+    out32 = kernels.geom_scan(q, k, v, gq, gk, es)
+    out16 = kernels.geom_scan(q, k, v, gq, gk, es, p_format="snorm16")
+    for a, b in zip(out32[:3], out16[:3]):
+        assert torch.equal(a, b)                         # transports do not depend on the storage
+    P32, P16 = out32[3], out16[3]
+    assert P16.dtype == torch.int16
+    Pn = P32 / P32.norm(dim=-1, keepdim=True)
+    assert (torch.round(Pn * 32767).to(torch.int16) - P16).abs().max().item() <= 1
+    R32 = _np(kernels.quat_to_dense(P32, d))
+    R16 = _np(kernels.quat_to_dense(P16.float().contiguous(), d))
+    assert np.abs(R32 - R16).max() < 2e-4
+    o32 = kernels.attention(*out32[:4], d, 1.0 / math.sqrt(d))
+    o16 = kernels.attention(*out16[:4], d, 1.0 / math.sqrt(d))
+    torch.cuda.synchronize()
+    diff = (o32.float() - o16.float()).abs().max().item()
+    scale = o32.float().abs().max().item()
+    assert diff <= (2e-4 if dtype == torch.float32 else 1.6e-2) * max(scale, 1.0)
