@@ -93,7 +93,7 @@ class PathOrderedGeometricMHA(nn.Module):
         self._mask_ok = None
 
     # ---- dispatch predicate (kernel/attention_kernel.py:203-208) ----
-    def _unsupported_reason(self, x, attn_mask) -> Optional[str]:
+    def _unsupported_reason(self, x, attn_mask, causal_implied: bool = False) -> Optional[str]:
         if self.mode != "causal":
             return f"mode={self.mode!r} (only 'causal' runs on the kernel path)"
         if not x.is_cuda:
@@ -104,6 +104,8 @@ class PathOrderedGeometricMHA(nn.Module):
             return f"dtype {x.dtype} (float32 and bfloat16 are supported)"
         if self.link_mode not in ("additive", "interaction"):
             return f"link_mode={self.link_mode!r}"
+        if causal_implied:                    # prefill / decode: the causal mask is the definition
+            return None
         L = x.shape[1]
         key = None if attn_mask is None else (attn_mask.data_ptr(), attn_mask._version,
                                               tuple(attn_mask.shape), attn_mask.device)
@@ -151,17 +153,22 @@ class PathOrderedGeometricMHA(nn.Module):
         else:
             qkv = F.linear(x, self.qkv.weight).view(B, L, H, 3 * d)
             pair = torch.cat([x, torch.roll(x, shifts=-1, dims=1)], dim=-1)
-            hid = self.edge_mlp[1](self.edge_mlp[0](pair)).reshape(B * L, -1)
-            lin2 = self.edge_mlp[2]
-            if x.dtype == torch.float32:
-                g = F.linear(hid, lin2.weight, lin2.bias)
-            else:
-                g = torch.mm(hid, lin2.weight.t(), out_dtype=torch.float32)
-                if lin2.bias is not None:
-                    g = g + lin2.bias.float()
-            gq = g.view(B, L, H, m)                              # a_t = es * g_t
+            gq = self._edge_params(pair).view(B, L, H, m)        # a_t = es * g_t
             gk = None
         return qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], gq, gk
+
+    def _edge_params(self, pair: torch.Tensor) -> torch.Tensor:
+        """Interaction generator on (..., 2D) pairs [x_t ; x_{t+1}]
+        (core/attention_fast_chunked.py:73-77): (N, H*m) with the last layer
+        written in fp32."""
+        hid = self.edge_mlp[1](self.edge_mlp[0](pair)).reshape(-1, 4 * self.h * self.d)
+        lin2 = self.edge_mlp[2]
+        if pair.dtype == torch.float32:
+            return F.linear(hid, lin2.weight, lin2.bias)
+        g = torch.mm(hid, lin2.weight.t(), out_dtype=torch.float32)
+        if lin2.bias is not None:
+            g = g + lin2.bias.float()
+        return g
 
     @staticmethod
     def _p_format(x: torch.Tensor, return_geometry: bool) -> str:
@@ -196,3 +203,77 @@ class PathOrderedGeometricMHA(nn.Module):
         C = kernels.quat_to_dense(P, d).to(x.dtype)
         Hm = kernels.quat_to_dense(hol, d).to(x.dtype)
         return y, {"C": C, "H": Hm}
+
+    # ---- incremental decode (no counterpart in the reference) ----
+    def prefill(self, x: torch.Tensor, capacity: Optional[int] = None) -> Tuple[torch.Tensor, "DecodeState"]:
+        """Causal forward of the prefix x (B, T, D) -- the same kernels as
+        `forward` -- plus the state that `decode_step` continues from: the
+        prefix's transported keys and values (global frame) in caches of
+        `capacity` positions (default T + 256, rounded up to 64), P_{T-1} and
+        the link inputs of token T-1."""
+        reason = self._unsupported_reason(x, None, causal_implied=True)
+        if reason is not None:
+            raise NotImplementedError(f"holonomyawareattention_amd prefill: {reason}")
+        B, T, D = x.shape
+        H, d = self.h, self.d
+        cap = T + 256 if capacity is None else int(capacity)
+        cap = (max(cap, T + 1) + 63) // 64 * 64
+        with torch.no_grad():
+            q, k, v, gq, gk = self._link_inputs(x)
+            qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale, p_format="f32")
+            o = kernels.attention(qh, kh, vh_t, P, d, self.scale)
+            y = F.linear(o.view(B, T, D), self.out.weight)
+            Dp, Tp = kh.shape[-1], kh.shape[2]
+            kc = torch.zeros((B, H, cap, Dp), dtype=x.dtype, device=x.device)
+            vc = torch.zeros((B, H, cap // 64, Dp, 64), dtype=x.dtype, device=x.device)
+            kc[:, :, :Tp] = kh
+            vc[:, :, :Tp // 64] = vh_t
+            st = DecodeState(kc, vc, P[:, :, T - 1].contiguous(), T,
+                             gq[:, T - 1].contiguous() if self.link_mode == "additive" else x[:, T - 1].clone())
+        return y, st
+
+    def decode_step(self, x_t: torch.Tensor, state: "DecodeState") -> torch.Tensor:
+        """Output (B, 1, D) for the next token x_t (B, 1, D) after the tokens in
+        `state` (from `prefill` or earlier steps); equals row t of `forward`
+        over the whole sequence. Updates `state`."""
+        B, L, D = x_t.shape
+        if L != 1:
+            raise ValueError("decode_step takes one token per sequence (B, 1, D)")
+        t = state.t
+        if t >= state.capacity:
+            raise ValueError(f"decode cache full ({state.capacity} positions)")
+        H, d = self.h, self.d
+        with torch.no_grad():
+            if self.link_mode == "additive":
+                q, k, v, gq, gk = self._link_inputs(x_t)
+                kernels.decode_geom(q[:, 0], k[:, 0], v[:, 0], state.g_prev, gk[:, 0], self.edge_scale, t,
+                                    state.P, state.qh, state.kh, state.vh)
+                state.g_prev = gq[:, 0].contiguous()
+            else:
+                qkv = F.linear(x_t, self.qkv.weight).view(B, H, 3 * d)
+                g = self._edge_params(torch.cat([state.g_prev, x_t[:, 0]], dim=-1)).view(B, H, self.m_dim)
+                kernels.decode_geom(qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], g, None,
+                                    self.edge_scale, t, state.P, state.qh, state.kh, state.vh)
+                state.g_prev = x_t[:, 0].clone()
+            if state.workspace is None:        # sized once for the last position of the cache
+                n = kernels.decode_workspace_bytes(B, H, d, state.capacity - 1)
+                state.workspace = torch.empty(max(n, 16), dtype=torch.uint8, device=x_t.device)
+            o = kernels.decode_attention(state.qh, state.kh, state.vh, state.P, t, d, self.scale,
+                                         workspace=state.workspace)
+            y = F.linear(o.view(B, 1, D), self.out.weight)
+        state.t = t + 1
+        return y
+
+
+class DecodeState:
+    """Caches and running geometry of `PathOrderedGeometricMHA.decode_step`:
+    kh (B, H, capacity, Dp) and vh (B, H, capacity/64, Dp, 64) transported keys
+    and values in the frame of token 0, P (B, H, nb, 4) fp32 = P_{t-1}, t = the
+    next token's position, g_prev = the link inputs of token t-1 (gq in
+    additive mode, x_{t-1} in interaction mode)."""
+
+    def __init__(self, kh, vh, P, t, g_prev):
+        self.kh, self.vh, self.P, self.t, self.g_prev = kh, vh, P, t, g_prev
+        self.capacity = int(kh.shape[2])
+        self.qh = torch.empty((kh.shape[0], kh.shape[1], kh.shape[3]), dtype=kh.dtype, device=kh.device)
+        self.workspace = None

@@ -190,4 +190,98 @@ int holo_quat_to_dense(int64_t n, int d, const float* quat, float* dense, void* 
   return HOLO_OK;
 }
 
+int holo_decode_geom_fwd(int B, int H, int d, int64_t t, int64_t capacity,
+                         int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                         const void* gq, int64_t gq_bs, int64_t gq_hs,
+                         const void* gk, int64_t gk_bs, int64_t gk_hs,
+                         const void* q, int64_t q_bs, int64_t q_hs,
+                         const void* k, int64_t k_bs, int64_t k_hs,
+                         const void* v, int64_t v_bs, int64_t v_hs,
+                         float* P, void* qh, void* kh_cache, void* vh_cache, void* stream) {
+  g_last_error.clear();
+  int rc = check_common(B, capacity, H, d);
+  if (rc) return rc;
+  if (t < 0 || capacity % holo::kChunk != 0 || t >= capacity)
+    return fail(HOLO_ERR_BAD_SHAPE, "need 0 <= t < capacity and capacity a multiple of 64 (t=%lld, capacity=%lld)",
+                (long long)t, (long long)capacity);
+  if (io_dtype != HOLO_F32 && io_dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "io_dtype %d is not HOLO_F32 or HOLO_BF16", io_dtype);
+  if (gen_dtype != HOLO_F32 && gen_dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "gen_dtype %d is not HOLO_F32 or HOLO_BF16", gen_dtype);
+  if (io_dtype == HOLO_F32 && gen_dtype != HOLO_F32)
+    return fail(HOLO_ERR_UNSUPPORTED, "fp32 keys/values need an fp32 generator");
+  if (gen_mode != HOLO_GEN_ADDITIVE && gen_mode != HOLO_GEN_DIRECT)
+    return fail(HOLO_ERR_INVALID_ARG, "gen_mode %d unknown", gen_mode);
+  const int nb = d / 3;
+  if (!q || !k || !v || !qh || !kh_cache || !vh_cache || (nb > 0 && !P))
+    return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if (t > 0 && nb > 0 && (!gq || (gen_mode == HOLO_GEN_ADDITIVE) != (gk != nullptr)))
+    return fail(HOLO_ERR_INVALID_ARG, "link parameters: gq (and gk in additive mode only) are required for t > 0");
+  if (!aligned16(qh) || !aligned16(kh_cache) || !aligned16(vh_cache) || (P && !aligned16(P)))
+    return fail(HOLO_ERR_INVALID_ARG, "qh, the caches and P must be 16-byte aligned");
+
+  holo::DecodeGeomArgs a;
+  a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d); a.gen_mode = gen_mode;
+  a.t = t; a.cap = capacity; a.edge_scale = edge_scale;
+  a.gq = gq; a.gq_bs = gq_bs; a.gq_hs = gq_hs;
+  a.gk = gk; a.gk_bs = gk_bs; a.gk_hs = gk_hs;
+  a.q = q; a.q_bs = q_bs; a.q_hs = q_hs;
+  a.k = k; a.k_bs = k_bs; a.k_hs = k_hs;
+  a.v = v; a.v_bs = v_bs; a.v_hs = v_hs;
+  a.P = P; a.qh = qh; a.kc = kh_cache; a.vc = vh_cache;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = io_dtype == HOLO_F32 ? holo::launch_decode_geom<float, float>(a, s)
+                 : gen_dtype == HOLO_F32 ? holo::launch_decode_geom<holo::bf16, float>(a, s)
+                                         : holo::launch_decode_geom<holo::bf16, holo::bf16>(a, s);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "decode geometry launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+size_t holo_decode_attn_workspace_size(int B, int H, int d, int64_t t) {
+  if (B <= 0 || H <= 0 || d <= 0 || t < 0) return 0;
+  return (size_t)B * H * holo::decode_splits(t) * (holo::padded_head_dim(d) + 2) * sizeof(float);
+}
+
+int holo_decode_attn_fwd(int B, int H, int d, int64_t t, int64_t capacity, int dtype, float scale,
+                         const void* qh, const void* kh_cache, const void* vh_cache, const float* P,
+                         void* o, int64_t o_bs, int64_t o_hs,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  int rc = check_common(B, capacity, H, d);
+  if (rc) return rc;
+  if (t < 0 || capacity % holo::kChunk != 0 || t >= capacity)
+    return fail(HOLO_ERR_BAD_SHAPE, "need 0 <= t < capacity and capacity a multiple of 64 (t=%lld, capacity=%lld)",
+                (long long)t, (long long)capacity);
+  if (dtype != HOLO_F32 && dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "dtype %d is not HOLO_F32 or HOLO_BF16", dtype);
+  if (!(scale > 0.f) || !(scale < 1e30f))
+    return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
+  const int nb = d / 3;
+  if (!qh || !kh_cache || !vh_cache || !o || (nb > 0 && !P))
+    return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if (o_hs < d || o_bs < (int64_t)H * o_hs)
+    return fail(HOLO_ERR_INVALID_ARG, "o strides (batch %lld, head %lld) overlap", (long long)o_bs, (long long)o_hs);
+  if (!aligned16(qh) || !aligned16(kh_cache) || !aligned16(vh_cache) || (P && !aligned16(P)))
+    return fail(HOLO_ERR_INVALID_ARG, "qh, the caches and P must be 16-byte aligned");
+  if (capacity * holo::padded_head_dim(d) * (dtype == HOLO_F32 ? 4 : 2) > 0x7fffffff)
+    return fail(HOLO_ERR_UNSUPPORTED, "capacity %lld too long for one (b, h) key slice", (long long)capacity);
+  const size_t need = holo_decode_attn_workspace_size(B, H, d, t);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
+                need, workspace ? workspace_bytes : (size_t)0);
+
+  holo::DecodeAttnArgs a;
+  a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d);
+  a.t = t; a.cap = capacity; a.nsplit = holo::decode_splits(t);
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.qh = qh; a.kc = kh_cache; a.vc = vh_cache; a.P = P;
+  a.o = o; a.o_bs = o_bs; a.o_hs = o_hs;
+  a.ws = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = dtype == HOLO_F32 ? holo::launch_decode_attn<float>(a, s)
+                                   : holo::launch_decode_attn<holo::bf16>(a, s);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "decode attention launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
 }  // extern "C"

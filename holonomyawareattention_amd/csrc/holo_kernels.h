@@ -31,7 +31,33 @@ struct AttnArgs {
   int p_format;    // 0: fp32 quaternions, 1: int16 (round(32767 q/|q|))
 };
 
+struct DecodeGeomArgs {
+  int B, H, d, nb, Dp, gen_mode;
+  int64_t t, cap;                  // new token's position, cache capacity (multiple of 64)
+  float edge_scale;
+  const void* gq; int64_t gq_bs, gq_hs;   // link parameters of token t-1 (unused when t == 0)
+  const void* gk; int64_t gk_bs, gk_hs;   // gk of token t (additive mode)
+  const void* q; int64_t q_bs, q_hs;
+  const void* k; int64_t k_bs, k_hs;
+  const void* v; int64_t v_bs, v_hs;
+  float* P;                        // (B, H, nb, 4) fp32: P_{t-1} in, P_t out
+  void* qh;                        // (B, H, Dp)
+  void* kc; void* vc;              // caches (B, H, cap, Dp) and (B, H, cap/64, Dp, 64)
+};
+
+struct DecodeAttnArgs {
+  int B, H, d, nb, Dp;
+  int64_t t, cap, nsplit;          // keys 0..t are attended
+  float scale_log2;
+  const void* qh; const void* kc; const void* vc; const float* P;
+  void* o; int64_t o_bs, o_hs;
+  float* ws;                       // (B, H, nsplit, Dp + 2) partials
+};
+
 template <typename IO, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
+template <typename IO, typename GT> hipError_t launch_decode_geom(const DecodeGeomArgs& a, hipStream_t s);
+template <typename T> hipError_t launch_decode_attn(const DecodeAttnArgs& a, hipStream_t s);
+int64_t decode_splits(int64_t t);
 template <typename T> hipError_t launch_attn(const AttnArgs& a, hipStream_t s);
 hipError_t launch_quat_to_dense(int64_t n, int d, const float* q, float* out, hipStream_t s);
 

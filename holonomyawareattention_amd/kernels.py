@@ -162,3 +162,78 @@ def quat_to_dense(quat: torch.Tensor, d: int) -> torch.Tensor:
     rc = lib.holo_quat_to_dense(n, d, _ptr(quat) if nb else None, _ptr(out), _stream(quat.device))
     _lib.check(rc, "holo_quat_to_dense")
     return out
+
+
+def _bh_view(t: torch.Tensor, B: int, H: int, width: int, name: str) -> Tuple[int, int]:
+    """(batch stride, head stride) of a (B, H, >= width) view with a unit last stride."""
+    if t.dim() != 3 or t.shape[0] != B or t.shape[1] != H or t.shape[2] < width or t.stride(2) != 1:
+        raise ValueError(f"{name}: expected a (B={B}, H={H}, {width}) view with a unit last stride")
+    return t.stride(0), t.stride(1)
+
+
+def decode_geom(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g_prev: Optional[torch.Tensor],
+                gk: Optional[torch.Tensor], edge_scale: float, t: int, P: torch.Tensor,
+                qh: torch.Tensor, kh_cache: torch.Tensor, vh_cache: torch.Tensor) -> None:
+    """One decode step's geometry for token t (see holo_decode_geom_fwd).
+    q, k, v: (B,H,d) views of the new token; g_prev: link parameters of token
+    t-1 (B,H,3nb): gq in additive mode (with gk of token t), the edge-MLP
+    output g in direct mode (gk None); not read when t = 0. P (B,H,nb,4) fp32
+    is updated in place from P_{t-1} to P_t; qh (B,H,Dp) receives P_t^T q_t
+    and row t of the caches the transported key and value."""
+    lib = _lib.load()
+    B, H, d = k.shape
+    nb = d // 3
+    dev, dt = k.device, k.dtype
+    if dev.type != "cuda" or dt not in _DT:
+        raise ValueError("decode_geom: k must be a float32/bfloat16 GPU tensor")
+    Dp = padded_head_dim(d)
+    cap = int(kh_cache.shape[2])
+    if tuple(kh_cache.shape) != (B, H, cap, Dp) or not kh_cache.is_contiguous() or kh_cache.dtype != dt:
+        raise ValueError("decode_geom: kh_cache must be a contiguous (B, H, capacity, Dp) tensor")
+    if tuple(vh_cache.shape) != (B, H, cap // 64, Dp, 64) or not vh_cache.is_contiguous() or vh_cache.dtype != dt:
+        raise ValueError("decode_geom: vh_cache must be a contiguous (B, H, capacity/64, Dp, 64) tensor")
+    if tuple(qh.shape) != (B, H, Dp) or not qh.is_contiguous() or qh.dtype != dt:
+        raise ValueError("decode_geom: qh must be a contiguous (B, H, Dp) tensor")
+    if tuple(P.shape) != (B, H, nb, 4) or P.dtype != torch.float32 or not P.is_contiguous():
+        raise ValueError("decode_geom: P must be a contiguous fp32 (B, H, nb, 4) tensor")
+    q_s, k_s, v_s = (_bh_view(x, B, H, d, n) for x, n in ((q, "q"), (k, "k"), (v, "v")))
+    gdt = torch.float32 if g_prev is None else g_prev.dtype
+    if g_prev is not None and gdt not in _DT:
+        raise ValueError("decode_geom: link parameters must be float32 or bfloat16")
+    g_s = (0, 0) if g_prev is None else _bh_view(g_prev, B, H, 3 * nb, "g_prev")
+    gk_s = (0, 0) if gk is None else _bh_view(gk, B, H, 3 * nb, "gk")
+    mode = _lib.HOLO_GEN_ADDITIVE if gk is not None or (g_prev is None and t == 0) else _lib.HOLO_GEN_DIRECT
+    rc = lib.holo_decode_geom_fwd(
+        B, H, d, int(t), cap, mode, float(edge_scale), _DT[dt], _DT[gdt],
+        _ptr(g_prev), g_s[0], g_s[1], _ptr(gk), gk_s[0], gk_s[1],
+        _ptr(q), q_s[0], q_s[1], _ptr(k), k_s[0], k_s[1], _ptr(v), v_s[0], v_s[1],
+        _ptr(P) if nb else None, _ptr(qh), _ptr(kh_cache), _ptr(vh_cache), _stream(dev))
+    _lib.check(rc, "holo_decode_geom_fwd")
+
+
+def decode_workspace_bytes(B: int, H: int, d: int, t: int) -> int:
+    """Workspace bytes of decode_attention at position t."""
+    return int(_lib.load().holo_decode_attn_workspace_size(B, H, d, int(t)))
+
+
+def decode_attention(qh: torch.Tensor, kh_cache: torch.Tensor, vh_cache: torch.Tensor, P: torch.Tensor,
+                     t: int, d: int, scale: float, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """o_t (B,H,d) = P_t sum_{j<=t} softmax_j(scale qh . kh_j) vh_j over cache rows 0..t."""
+    lib = _lib.load()
+    B, H, Dp = (int(n) for n in qh.shape)
+    dev, dt = qh.device, qh.dtype
+    nb = d // 3
+    cap = int(kh_cache.shape[2])
+    if out is None:
+        out = torch.empty((B, H, d), dtype=dt, device=dev)
+    o_s = _bh_view(out, B, H, d, "out")
+    need = int(lib.holo_decode_attn_workspace_size(B, H, d, int(t)))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    rc = lib.holo_decode_attn_fwd(B, H, d, int(t), cap, _DT[dt], float(scale),
+                                  _ptr(qh), _ptr(kh_cache), _ptr(vh_cache), _ptr(P) if nb else None,
+                                  _ptr(out), o_s[0], o_s[1], _ptr(workspace),
+                                  workspace.numel() * workspace.element_size(), _stream(dev))
+    _lib.check(rc, "holo_decode_attn_fwd")
+    return out

@@ -150,6 +150,47 @@ HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_form
                   void* stream);
 
 /*
+ * Incremental decode (no counterpart in the reference, which only runs whole
+ * sequences; row t of its forward, core/attention_fast_chunked.py:63-173, is
+ * what these two calls produce for a new token t after tokens 0..t-1).
+ *
+ * Cache layouts (io dtype): kh_cache (B, H, capacity, Dp) and vh_cache
+ * (B, H, capacity/64, Dp, 64), i.e. the scan's kh / vh_t layouts with
+ * `capacity` (a multiple of 64) in place of Tp; rows 0..t-1 hold the
+ * transported keys and values of the earlier tokens (e.g. copied from a scan
+ * of the prefix). P (B, H, nb, 4) fp32 holds P_{t-1} on entry (identity for
+ * t = 0) and P_t on return.
+ *
+ * holo_decode_geom_fwd: composes the link of edge t-1 -> t into P
+ *   (additive: gq of token t-1 plus gk of token t; direct: g of edge t-1;
+ *   neither is read when t = 0), writes qh = P_t^T q_t (B, H, Dp) and appends
+ *   kh_t = P_t^T k_t, vh_t = P_t^T v_t as row t of the caches. Inputs are one
+ *   token per (b, h): element (b, h, c) at ptr[b*batch_stride + h*head_stride + c].
+ */
+HOLO_API int holo_decode_geom_fwd(int B, int H, int d, int64_t t, int64_t capacity,
+                         int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                         const void* gq, int64_t gq_batch_stride, int64_t gq_head_stride,
+                         const void* gk, int64_t gk_batch_stride, int64_t gk_head_stride,
+                         const void* q, int64_t q_batch_stride, int64_t q_head_stride,
+                         const void* k, int64_t k_batch_stride, int64_t k_head_stride,
+                         const void* v, int64_t v_batch_stride, int64_t v_head_stride,
+                         float* P, void* qh, void* kh_cache, void* vh_cache, void* stream);
+
+/* Workspace bytes for holo_decode_attn_fwd at position t. */
+HOLO_API size_t holo_decode_attn_workspace_size(int B, int H, int d, int64_t t);
+
+/*
+ * holo_decode_attn_fwd: o_t = P_t sum_{j<=t} softmax_j(scale * qh . kh_j) vh_j
+ *   over cache rows 0..t, written at o[b*o_batch_stride + h*o_head_stride + c].
+ *   Split over 256-key segments with a merge; every cached key and value is
+ *   read once.
+ */
+HOLO_API int holo_decode_attn_fwd(int B, int H, int d, int64_t t, int64_t capacity, int dtype, float scale,
+                         const void* qh, const void* kh_cache, const void* vh_cache, const float* P,
+                         void* o, int64_t o_batch_stride, int64_t o_head_stride,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Expand fp32 quaternions (n, nb, 4) to dense fp32 rotation matrices (n, d, d):
  * block b on dims 3b..3b+2, identity on the leftover dims.
  */

@@ -104,3 +104,28 @@ def test_status_codes_map_to_reference_exceptions(lib):
     with pytest.raises(_lib.HoloError):
         _lib.check(_lib.HOLO_ERR_WORKSPACE, "scan")
     _lib.check(_lib.HOLO_OK, "scan")
+
+
+def _dgeom(lib, **kw):
+    a = dict(B=1, H=2, d=12, t=3, cap=64, gen=0, es=0.1, io=_lib.HOLO_F32, gdt=_lib.HOLO_F32,
+             gq=16, gk=16, q=16, k=16, v=16, P=16, qh=16, kc=16, vc=16, bs=48, hs=24)
+    a.update(kw)
+    return lib.holo_decode_geom_fwd(a["B"], a["H"], a["d"], a["t"], a["cap"], a["gen"], a["es"], a["io"], a["gdt"],
+                                    a["gq"], a["bs"], a["hs"], a["gk"], a["bs"], a["hs"],
+                                    a["q"], a["bs"], a["hs"], a["k"], a["bs"], a["hs"], a["v"], a["bs"], a["hs"],
+                                    a["P"], a["qh"], a["kc"], a["vc"], None)
+
+
+def test_decode_argument_validation(lib):
+    assert _dgeom(lib, t=64) == _lib.HOLO_ERR_BAD_SHAPE                 # t >= capacity
+    assert _dgeom(lib, cap=100) == _lib.HOLO_ERR_BAD_SHAPE              # capacity not a multiple of 64
+    assert _dgeom(lib, gk=None) == _lib.HOLO_ERR_INVALID_ARG            # additive needs gk when t > 0
+    assert _dgeom(lib, gen=_lib.HOLO_GEN_DIRECT) == _lib.HOLO_ERR_INVALID_ARG   # direct takes no gk
+    assert _dgeom(lib, kc=8) == _lib.HOLO_ERR_INVALID_ARG               # misaligned cache
+    assert _dgeom(lib, d=200) == _lib.HOLO_ERR_UNSUPPORTED
+    f = lib.holo_decode_attn_fwd
+    need = lib.holo_decode_attn_workspace_size(1, 2, 12, 300)
+    assert need == 1 * 2 * 2 * (32 + 2) * 4                             # two 256-key segments at t = 300
+    assert f(1, 2, 12, 300, 320, 0, 0.3, 16, 16, 16, 16, 16, 24, 12, 16, 16, None) == _lib.HOLO_ERR_WORKSPACE
+    assert f(1, 2, 12, 400, 320, 0, 0.3, 16, 16, 16, 16, 16, 24, 12, 16, need, None) == _lib.HOLO_ERR_BAD_SHAPE
+    assert f(1, 2, 12, 3, 64, 0, 0.3, 16, 16, 16, 16, 16, 24, 4, 16, need, None) == _lib.HOLO_ERR_INVALID_ARG
