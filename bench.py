@@ -164,6 +164,77 @@ def orthogonality_report(m, x, config, kernels, torch):
     return out
 
 
+DECODE_CFG = dict(B=64, T0=8192, D=1536, H=16, es=0.05)     # config 5
+
+
+def decode_bench(args, torch, F, synth, kernels, Module):
+    """Config 5: prefill 8192 tokens for 64 sequences, then time single-token
+    decode steps (the module's decode_step, stage by stage with HIP events).
+    The decode attention reads every cached key and value once per step:
+    2 * B * H * (t + 1) * d * 2 bytes at position t, its roofline."""
+    c = DECODE_CFG
+    B, T0, D, H, es = c["B"], c["T0"], c["D"], c["H"], c["es"]
+    d = D // H
+    steps, warm = args.decode_steps, max(args.warmup, 1)
+    dev, dt = torch.device("cuda:0"), torch.bfloat16
+    inp = synth.layer_inputs(5, 1, 1, D, H, "additive")          # weights only (x is drawn below)
+    m = Module(D, n_heads=H, edge_scale=es)
+    m.link_mode = "additive"
+    with torch.no_grad():
+        for k, p in m.state_dict().items():
+            if k in inp:
+                p.copy_(torch.as_tensor(inp[k]))
+    m = m.to(device=dev, dtype=dt).eval()
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(B, T0 + warm + steps, D, device=dev, generator=g).to(dt)
+    t0 = time.perf_counter()
+    _, st = m.prefill(x[:, :T0], capacity=T0 + warm + steps)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    for i in range(warm):
+        m.decode_step(x[:, T0 + i:T0 + i + 1], st)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    kv_bytes = 0
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    with torch.no_grad():
+        for i in range(steps):
+            pos = T0 + warm + i
+            xt = x[:, pos:pos + 1]
+            e = ev[i]
+            e[0].record()
+            q, k, v, gq, gk = m._link_inputs(xt)
+            kernels.decode_geom(q[:, 0], k[:, 0], v[:, 0], st.g_prev, gk[:, 0], es, st.t, st.P, st.qh, st.kh, st.vh)
+            st.g_prev = gq[:, 0].contiguous()
+            e[1].record()
+            o = kernels.decode_attention(st.qh, st.kh, st.vh, st.P, st.t, d, m.scale, workspace=st.workspace)
+            e[2].record()
+            F.linear(o.view(B, 1, D), m.out.weight)
+            e[3].record()
+            kv_bytes += 2 * B * H * (st.t + 1) * d * 2
+            st.t += 1
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    stage = [sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(steps)) for j in range(3)]
+    attn_s = stage[1] * 1e-3
+    ms = wall * 1e3 / steps
+    return {"metric": "decode tokens/s (cfg5: B=64, prefix 8192, bf16), KV-read GB/s of the decode attention",
+            "value": B * steps / wall, "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic (x ~ N(0,1) from torch.randn seeded 5; weights from the "
+                                     "SplitMix64 generator, N(0,1/d_model))",
+            "config": {"workload": "cfg5: incremental decode after a prefill", "global_batch": B, "prefix": T0,
+                       "positions": [T0 + warm, T0 + warm + steps - 1], "n_heads": H, "d_head": d, "d_model": D,
+                       "link_mode": "additive", "edge_scale": es, "parallelism": "single GPU"},
+            "stages_ms_per_step": {"projections_and_geometry": stage[0] / steps, "decode_attention": stage[1] / steps,
+                                   "out_projection": stage[2] / steps},
+            "roofline": {"kernel": "decode_attn_split + decode_attn_combine (holo_decode_attn_fwd)", "bound": "hbm",
+                         "achieved": kv_bytes / attn_s / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": kv_bytes / attn_s / 1e9 / PEAK_HBM_GBS, "traffic": None,
+                         "bytes_per_step": kv_bytes / steps},
+            "prefill_s": round(prefill_s, 3), "cpu_baseline": None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,6 +246,9 @@ def main():
                     help="end with a plain 1 GiB device copy (PMC counter calibration)")
     ap.add_argument("--ortho", action="store_true",
                     help="config 3 geometry check: orthogonality of P at t = T-1 (one JSON line) and exit")
+    ap.add_argument("--decode", action="store_true",
+                    help="config 5: incremental decode after a prefill (one JSON line) and exit")
+    ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSVs under DIR(s) as JSON and exit")
     args = ap.parse_args()
@@ -194,6 +268,9 @@ def main():
     from holonomyawareattention_amd import kernels, synth
     from holonomyawareattention_amd.attention_kernel import PathOrderedGeometricMHA
 
+    if args.decode:
+        print(json.dumps(decode_bench(args, torch, F, synth, kernels, PathOrderedGeometricMHA)))
+        return
     cfg = CONFIGS[args.config]
     B, T, D, H, es = cfg["B"], cfg["T"], cfg["D"], cfg["H"], cfg["es"]
     d = D // H
