@@ -105,6 +105,16 @@ __global__ void __launch_bounds__(256) decode_attn_split(DecodeAttnArgs a) {
   const int64_t n0 = (int64_t)s * kDecodeSplit;
   const int nk = (int)((a.t + 1 - n0) < kDecodeSplit ? (a.t + 1 - n0) : kDecodeSplit);   // >= 1
 
+  // ---- value tiles of the segment (used after the softmax) ----
+  constexpr int kTiles = kDecodeSplit / kChunk;
+  u32x4 vraw[kTiles][NJ];
+  static_for<kTiles>([&](auto tl) {
+    if (tl * kChunk < nk) {
+      const u32x4* vt = reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.vc) +
+                                                       (bh * (a.cap / kChunk) + n0 / kChunk + tl) * DP * kChunk);
+      static_for<NJ>([&](auto j) { vraw[tl][j] = vt[tid + 256 * j]; });
+    }
+  });
   // ---- scores of key n0 + tid (log2 units) ----
   float sc = -INFINITY;
   if (tid < nk) {
@@ -139,25 +149,24 @@ __global__ void __launch_bounds__(256) decode_attn_split(DecodeAttnArgs a) {
   l = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
 
   // ---- P V over the segment's value tiles: chunk c = tid + 256 j of a tile
-  // holds dim c / CPR, keys E (c % CPR) .. + E ----
+  // holds dim c / CPR, keys E (c % CPR) .. + E. The chunks do not depend on
+  // the scores, so they are loaded with the keys at the start (below, vraw),
+  // one memory round trip per workgroup ----
   const int sub = tid % CPR;
   float acc[NJ];
   static_for<NJ>([&](auto j) { acc[j] = 0.f; });
-  const int ntl = (nk + kChunk - 1) / kChunk;
-  for (int tl = 0; tl < ntl; ++tl) {
-    const int64_t gt = n0 / kChunk + tl;
-    const u32x4* vt = reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.vc) +
-                                                     (bh * (a.cap / kChunk) + gt) * DP * kChunk);
-    const int kb = tl * kChunk + E * sub;      // first key of this thread's chunks (segment-local)
-    static_for<NJ>([&](auto j) {
-      const u32x4 raw = vt[tid + 256 * j];
-      const T* e = reinterpret_cast<const T*>(&raw);
-      static_for<E>([&](auto i) {
-        // keys past t hold no data yet: skip them (their weight is zero)
-        if (kb + i < nk) acc[j] = __builtin_fmaf(ps[kb + i], to_f32(e[i]), acc[j]);
+  static_for<kTiles>([&](auto tl) {
+    if (tl * kChunk < nk) {
+      const int kb = tl * kChunk + E * sub;    // first key of this thread's chunks (segment-local)
+      static_for<NJ>([&](auto j) {
+        const T* e = reinterpret_cast<const T*>(&vraw[tl][j]);
+        static_for<E>([&](auto i) {
+          // keys past t hold no data yet: skip them (their weight is zero)
+          if (kb + i < nk) acc[j] = __builtin_fmaf(ps[kb + i], to_f32(e[i]), acc[j]);
+        });
       });
-    });
-  }
+    }
+  });
   static_for<NJ>([&](auto j) {
     for (int o = 1; o < CPR; o <<= 1) acc[j] += __shfl_xor(acc[j], o);
   });
