@@ -179,19 +179,52 @@ __global__ void __launch_bounds__(256) decode_attn_split(DecodeAttnArgs a) {
 
 template <typename T, int DP>
 __global__ void __launch_bounds__(128) decode_attn_combine(DecodeAttnArgs a) {
+  // Merge of the segment partials {m, l, o[DP]}: every load of a 128-segment
+  // group is issued before it is used (the weights go through LDS), so the
+  // merge costs a few memory round trips, not one per segment.
+  constexpr int kTh = 128;
   __shared__ float os[DP];
-  const int tid = threadIdx.x;
+  __shared__ float wts[kTh];
+  __shared__ float red[2];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t bh = blockIdx.x;
   const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const int ns = (int)a.nsplit;
   const float* part = a.ws + bh * a.nsplit * (DP + 2);
   float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, part[s * (DP + 2)]);
+  for (int s = tid; s < ns; s += kTh) M = fmaxf(M, part[(int64_t)s * (DP + 2)]);
+  M = wave_max(M);
+  if (lane == 0) red[w] = M;
+  __syncthreads();
+  M = fmaxf(red[0], red[1]);
   float L = 0.f, acc = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const float wgt = exp2f(part[s * (DP + 2)] - M);
-    L += part[s * (DP + 2) + 1] * wgt;
-    if (tid < DP) acc += part[s * (DP + 2) + 2 + tid] * wgt;
+  for (int base = 0; base < ns; base += kTh) {
+    const int n = ns - base < kTh ? ns - base : kTh;
+    __syncthreads();                           // the previous group's weights are consumed
+    float wgt = 0.f;
+    if (tid < n) {
+      const float* ps = part + (int64_t)(base + tid) * (DP + 2);
+      wgt = exp2f(ps[0] - M);
+      L += ps[1] * wgt;
+    }
+    wts[tid] = wgt;
+    __syncthreads();
+    if (tid < DP) {
+      const float* pc = part + (int64_t)base * (DP + 2) + 2 + tid;
+      int s = 0;
+      for (; s + 8 <= n; s += 8) {
+        float v[8];
+        static_for<8>([&](auto i) { v[i] = pc[(int64_t)(s + i) * (DP + 2)]; });
+        static_for<8>([&](auto i) { acc = __builtin_fmaf(v[i], wts[s + i], acc); });
+      }
+      for (; s < n; ++s) acc = __builtin_fmaf(pc[(int64_t)s * (DP + 2)], wts[s], acc);
+    }
   }
+  L = wave_sum(L);
+  __syncthreads();
+  if (lane == 0) red[w] = L;
+  __syncthreads();
+  L = red[0] + red[1];
   if (tid < DP) os[tid] = acc * __builtin_amdgcn_rcpf(L);
   __syncthreads();
   T* orow = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_bs + (int64_t)h * a.o_hs;
