@@ -91,6 +91,10 @@ class PathOrderedGeometricMHA(nn.Module):
         self._wcat_key = None
         self._wcat = None
         self._mask_ok = None
+        # profiling hook: when set to a sequence of 5 torch.cuda.Event, forward
+        # records them on the launch stream around its four stages (link
+        # inputs, geometry scan, attention, out-projection); no host sync
+        self._stage_events = None
 
     # ---- dispatch predicate (kernel/attention_kernel.py:203-208) ----
     def _unsupported_reason(self, x, attn_mask, causal_implied: bool = False) -> Optional[str]:
@@ -188,13 +192,24 @@ class PathOrderedGeometricMHA(nn.Module):
         B, L, D = x.shape
         params = [p for p in self.parameters() if p.requires_grad]
         track = torch.is_grad_enabled() and (x.requires_grad or bool(params))
+        ev = self._stage_events
         with torch.no_grad():
+            if ev is not None:
+                ev[0].record()
             q, k, v, gq, gk = self._link_inputs(x)
+            if ev is not None:
+                ev[1].record()
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
                                                      want_hol=return_geometry,
                                                      p_format=self._p_format(x, return_geometry))
+            if ev is not None:
+                ev[2].record()
             o = kernels.attention(qh, kh, vh_t, P, self.d, self.scale)
+            if ev is not None:
+                ev[3].record()
             y = F.linear(o.view(B, L, D), self.out.weight)
+            if ev is not None:
+                ev[4].record()
         if track:
             y = _ForwardOnly.apply(y, x, *params)
         if not return_geometry:

@@ -8,7 +8,8 @@
 // The wrap branch (i < j) of the reference is always masked under tril and is
 // not computed.
 //
-// Work decomposition: one workgroup (4 waves) per (b, h, 128-query tile); each
+// Work decomposition: one workgroup (4 waves) per (b, h) and folded pair of
+// 128-query tiles (a long and a short tile, run one after the other); each
 // wave owns 32 queries. Key/value tiles of 64 keys are staged in LDS
 // (kh row-major, vh already stored transposed by the scan), and each wave
 // computes
@@ -104,269 +105,281 @@ attn_fwd(AttnArgs a) {
   const int w = tid >> 6;
   const int lr = lane & 31;               // query column of this lane (MFMA col)
   const int g = lane >> 5;                // lane half
-  // Workgroup L runs on XCD L % 8. When B*H is a multiple of 8, XCD x takes the
-  // (b, h) pairs congruent to x and runs the query tiles of one pair back to
-  // back (longest first), so a pair's keys/values stay in that XCD's L2.
+  // Causal query tiles differ in length, so each workgroup runs a folded pair
+  // of one (b, h): query tile ntile-1-f, then tile f (alone when they
+  // coincide). Every pair of tiles covers ntile+1 key tiles of 128 keys, so
+  // all workgroups carry the same work and the grid ends without a tail.
+  // Workgroup L runs on XCD L % 8; when B*H is a multiple of 8, XCD x takes the
+  // (b, h) pairs congruent to x and runs the folds of one pair back to back, so
+  // a pair's keys/values stay in that XCD's L2.
   const int ntile = (int)((a.T + kBM - 1) / kBM);
+  const int nfold = (ntile + 1) / 2;
   const int L = blockIdx.x;
-  int bh, qt;
+  int bh, f;
   if ((a.B * a.H) % 8 == 0) {
     const int j = L >> 3;
-    bh = 8 * (j / ntile) + (L & 7);
-    qt = ntile - 1 - j % ntile;
+    bh = 8 * (j / nfold) + (L & 7);
+    f = j % nfold;
   } else {
     bh = L % (a.B * a.H);
-    qt = ntile - 1 - L / (a.B * a.H);
+    f = L / (a.B * a.H);
   }
   const int b = bh / a.H, h = bh % a.H;
-  const int64_t q0 = (int64_t)qt * kBM;
-  const int64_t qw = q0 + 32 * w;                       // first query of this wave
+  auto run_tile = [&](const int qt) {
+    const int64_t q0 = (int64_t)qt * kBM;
+    const int64_t qw = q0 + 32 * w;                       // first query of this wave
 
-  // ---- Q^T operand straight from qh (the scan's transported queries) ----
-  constexpr bool kBF = sizeof(T) == 2;
-  constexpr int QF = kBF ? DP / 16 : DP / 2;            // Q^T operand steps
-  typedef typename std::conditional<kBF, bf16x8, float>::type qfrag_t;
-  qfrag_t qf[QF];
-  {
-    const int64_t qrow_t = qw + lr;                     // rows past Tp read as zero
-    const T* qrow = reinterpret_cast<const T*>(a.qh) + ((int64_t)bh * a.Tp + qrow_t) * DP;
-    const bool in = qrow_t < a.Tp;
-    static_for<QF>([&](auto s) {
-      if constexpr (kBF) qf[s] = in ? *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * g) : bf16x8{};
-      else qf[s] = in ? qrow[2 * s + g] : 0.f;
-    });
-  }
+    // ---- Q^T operand straight from qh (the scan's transported queries) ----
+    constexpr bool kBF = sizeof(T) == 2;
+    constexpr int QF = kBF ? DP / 16 : DP / 2;            // Q^T operand steps
+    typedef typename std::conditional<kBF, bf16x8, float>::type qfrag_t;
+    qfrag_t qf[QF];
+    {
+      const int64_t qrow_t = qw + lr;                     // rows past Tp read as zero
+      const T* qrow = reinterpret_cast<const T*>(a.qh) + ((int64_t)bh * a.Tp + qrow_t) * DP;
+      const bool in = qrow_t < a.Tp;
+      static_for<QF>([&](auto s) {
+        if constexpr (kBF) qf[s] = in ? *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * g) : bf16x8{};
+        else qf[s] = in ? qrow[2 * s + g] : 0.f;
+      });
+    }
 
-  f32x16 O[DP / 32];
-  static_for<DP / 32>([&](auto i) { O[i] = f32x16{}; });
-  float m_run = -1e30f, l_run = 0.f;
-  const float c = a.scale_log2;
+    f32x16 O[DP / 32];
+    static_for<DP / 32>([&](auto i) { O[i] = f32x16{}; });
+    float m_run = -1e30f, l_run = 0.f;
+    const float c = a.scale_log2;
 
-  int64_t kend = q0 + kBM; if (kend > a.T) kend = a.T;
-  const int nkv = (int)((kend + kBN - 1) / kBN);
-  // tiles this wave attends to: keys up to its last query (0 when past T)
-  const int nact = qw >= a.T ? 0 : (int)((qw + 31) / kBN) + 1 < nkv ? (int)((qw + 31) / kBN) + 1 : nkv;
-  const u32x4* kbase = reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.kh) + (int64_t)bh * a.Tp * DP);
-  const u32x4* vbase = reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.vh_t) + (int64_t)bh * a.nch * DP * kBN);
-  constexpr int TCH = kBN * DP / C::E;                  // 16 B chunks per tile
-  constexpr int RC = DP / C::E, VC = kBN / C::E;        // chunks per K row / V^T row
+    int64_t kend = q0 + kBM; if (kend > a.T) kend = a.T;
+    const int nkv = (int)((kend + kBN - 1) / kBN);
+    // tiles this wave attends to: keys up to its last query (0 when past T)
+    const int nact = qw >= a.T ? 0 : (int)((qw + 31) / kBN) + 1 < nkv ? (int)((qw + 31) / kBN) + 1 : nkv;
+    const u32x4* kbase = reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.kh) + (int64_t)bh * a.Tp * DP);
+    const u32x4* vbase = reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.vh_t) + (int64_t)bh * a.nch * DP * kBN);
+    constexpr int TCH = kBN * DP / C::E;                  // 16 B chunks per tile
+    constexpr int RC = DP / C::E, VC = kBN / C::E;        // chunks per K row / V^T row
 
-  u32x4 kreg[C::KCH], vreg[C::VCH];
-  // buffer loads: the (b, h) slice in a scalar resource descriptor, the tile
-  // offset in a scalar register and a constant byte offset per lane, so a
-  // tile load costs no per-lane address arithmetic
-  const int kv_bytes = (int)((int64_t)a.Tp * DP * (int64_t)sizeof(T));
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<u32x4*>(kbase), 0, kv_bytes, kBufferWord3);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<u32x4*>(vbase), 0, kv_bytes, kBufferWord3);
-  auto load_tile = [&](int kt) {
-    const int toff = kt * TCH * 16;
-    static_for<C::KCH>([&](auto j) {
-      kreg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, (tid + j * kThreads) * 16, toff, 0);
-    });
-    static_for<C::VCH>([&](auto j) {
-      vreg[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (tid + j * kThreads) * 16, toff, 0);
-    });
-  };
-  auto store_tile = [&](int st) {
-    T* Ks = kv + st * C::kStage;
-    T* Vs = Ks + kBN * C::KS;
-    static_for<C::KCH>([&](auto j) {
-      int i = tid + j * kThreads, r = i / RC, cc = i % RC;
-      *reinterpret_cast<u32x4*>(&Ks[r * C::KS + cc * C::E]) = kreg[j];
-    });
-    static_for<C::VCH>([&](auto j) {
-      int i = tid + j * kThreads, r = i / VC, cc = i % VC;
-      u32x2* dst = reinterpret_cast<u32x2*>(&Vs[r * C::VS + cc * C::E]);
-      dst[0] = vreg[j].xy;
-      dst[1] = vreg[j].zw;
-    });
-  };
-  // S^T (64 keys x 32 queries) of the tile in stage st
-  auto qk = [&](int st, f32x16 (&S)[2]) {
-    const T* Ks = kv + st * C::kStage;
-    S[0] = f32x16{}; S[1] = f32x16{};
-    static_for<QF>([&](auto s) {
+    u32x4 kreg[C::KCH], vreg[C::VCH];
+    // buffer loads: the (b, h) slice in a scalar resource descriptor, the tile
+    // offset in a scalar register and a constant byte offset per lane, so a
+    // tile load costs no per-lane address arithmetic
+    const int kv_bytes = (int)((int64_t)a.Tp * DP * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<u32x4*>(kbase), 0, kv_bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<u32x4*>(vbase), 0, kv_bytes, kBufferWord3);
+    auto load_tile = [&](int kt) {
+      const int toff = kt * TCH * 16;
+      static_for<C::KCH>([&](auto j) {
+        kreg[j] = __builtin_amdgcn_raw_buffer_load_b128(krs, (tid + j * kThreads) * 16, toff, 0);
+      });
+      static_for<C::VCH>([&](auto j) {
+        vreg[j] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (tid + j * kThreads) * 16, toff, 0);
+      });
+    };
+    auto store_tile = [&](int st) {
+      T* Ks = kv + st * C::kStage;
+      T* Vs = Ks + kBN * C::KS;
+      static_for<C::KCH>([&](auto j) {
+        int i = tid + j * kThreads, r = i / RC, cc = i % RC;
+        *reinterpret_cast<u32x4*>(&Ks[r * C::KS + cc * C::E]) = kreg[j];
+      });
+      static_for<C::VCH>([&](auto j) {
+        int i = tid + j * kThreads, r = i / VC, cc = i % VC;
+        u32x2* dst = reinterpret_cast<u32x2*>(&Vs[r * C::VS + cc * C::E]);
+        dst[0] = vreg[j].xy;
+        dst[1] = vreg[j].zw;
+      });
+    };
+    // S^T (64 keys x 32 queries) of the tile in stage st
+    auto qk = [&](int st, f32x16 (&S)[2]) {
+      const T* Ks = kv + st * C::kStage;
+      S[0] = f32x16{}; S[1] = f32x16{};
+      static_for<QF>([&](auto s) {
+        static_for<2>([&](auto kb) {
+          if constexpr (kBF) {
+            bf16x8 av = *reinterpret_cast<const bf16x8*>(&Ks[(32 * kb + lr) * C::KS + 16 * s + 8 * g]);
+            S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qf[s], S[kb], 0, 0, 0);
+          } else {
+            float av = Ks[(32 * kb + lr) * C::KS + 2 * s + g];
+            S[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, qf[s], S[kb], 0, 0, 0);
+          }
+        });
+      });
+    };
+    // online softmax (log2 units, one lane pair per query) and O^T += V^T P^T
+    // of tile kt (stage st); the QK MFMAs of the next tile (stage stn, into Sn)
+    // are issued in the same basic block as the exponentials so the two overlap.
+    auto softmax_pv = [&](int kt, int st, f32x16 (&S)[2], int stn, f32x16 (&Sn)[2]) {
+      const T* Vs = kv + st * C::kStage + kBN * C::KS;
+      const int64_t k0 = (int64_t)kt * kBN;
+      if (k0 + kBN - 1 > qw) {             // tile reaches past this wave's first query
+        const int rel = (int)(qw - k0) + lr - 4 * g;     // key offset limit for this lane
+        static_for<2>([&](auto kb) {
+          static_for<16>([&](auto r) {
+            if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) S[kb][(int)r] = -INFINITY;
+          });
+        });
+      }
+      const float mx = pair_max(tile_max(S)) * c;
+      // each row decides for itself (a row's result never depends on its
+      // neighbours'); the wave-uniform branch only skips the work, rare after warm-up
+      const bool need = mx > m_run + kRescaleThreshold;
+      if (__any(need)) {
+        const float m_new = need ? mx : m_run;
+        const float corr = exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= corr;
+        static_for<DP / 32>([&](auto i) { O[i] *= corr; });
+      }
+      const float nm = -m_run;
+      qk(stn, Sn);
       static_for<2>([&](auto kb) {
-        if constexpr (kBF) {
-          bf16x8 av = *reinterpret_cast<const bf16x8*>(&Ks[(32 * kb + lr) * C::KS + 16 * s + 8 * g]);
-          S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qf[s], S[kb], 0, 0, 0);
+        static_for<16>([&](auto r) { S[kb][(int)r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][(int)r], c, nm)); });
+      });
+      if constexpr (kBF) {
+        // P^T operand in bf16; the row sum is taken over the same rounded
+        // values (two per v_dot2), so numerator and denominator agree.
+        bf16x8 pb[2][2];
+        static_for<2>([&](auto kb) {
+          static_for<2>([&](auto hh) {
+            static_for<8>([&](auto e) { pb[kb][hh][(int)e] = (bf16)S[kb][8 * hh + e]; });
+          });
+        });
+        // four independent partial sums (one per P^T operand), then a tree
+        float ls[2][2];
+        const bf16x2 one2 = {(bf16)1.f, (bf16)1.f};
+        static_for<2>([&](auto kb) {
+          static_for<2>([&](auto hh) {
+            ls[kb][hh] = 0.f;
+            static_for<4>([&](auto e) {
+              bf16x2 pr = {pb[kb][hh][2 * e], pb[kb][hh][2 * e + 1]};
+              ls[kb][hh] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, ls[kb][hh], false);
+            });
+          });
+        });
+        l_run += (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
+        static_for<2>([&](auto kb) {
+          static_for<2>([&](auto hh) {
+            static_for<DP / 32>([&](auto db) {          // independent accumulators back to back
+              const T* vr = &Vs[(32 * db + lr) * C::VS + 32 * kb + 16 * hh + 4 * g];
+              bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
+              bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 8);
+              bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+              O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[kb][hh], O[db], 0, 0, 0);
+            });
+          });
+        });
+      } else {
+        float t[16];
+        static_for<16>([&](auto r) { t[r] = S[0][(int)r] + S[1][(int)r]; });
+        static_for<8>([&](auto r) { t[r] += t[r + 8]; });
+        static_for<4>([&](auto r) { t[r] += t[r + 4]; });
+        static_for<2>([&](auto r) { t[r] += t[r + 2]; });
+        l_run += t[0] + t[1];
+        static_for<2>([&](auto kb) {
+          static_for<16>([&](auto r) {
+            static_for<DP / 32>([&](auto db) {
+              float av = Vs[(32 * db + lr) * C::VS + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3)];
+              O[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, S[kb][(int)r], O[db], 0, 0, 0);
+            });
+          });
+        });
+      }
+    };
+    // quaternions of the epilogue items (row, 8 consecutive 3-dim groups); a
+    // row's 8 quaternions are 128 contiguous bytes in fp32, 64 in int16
+    typedef typename std::conditional<PQ16, u32x2, f32x4>::type pq_t;
+    const pq_t pq_ident = [] {
+      if constexpr (PQ16) return u32x2{1u, 0u};            // (1, 0, 0, 0)
+      else return f32x4{1.f, 0.f, 0.f, 0.f};
+    }();
+    pq_t pq[C::EPI][8];
+    auto load_epilogue_quats = [&](auto first, auto count) {
+      static_for<decltype(count)::value>([&](auto k) {
+        constexpr int it = decltype(first)::value + decltype(k)::value;
+        const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
+        const int64_t t = q0 + r;
+        const bool row_ok = idx < kBM * C::NG8 && t < a.T;
+        const pq_t* base = reinterpret_cast<const pq_t*>(
+            reinterpret_cast<const char*>(a.P) + ((bh * a.T + t) * a.nb + 8 * gi) * (int64_t)sizeof(pq_t));
+        if (row_ok && 8 * gi + 8 <= a.nb) {
+          static_for<8>([&](auto jb) { pq[it][jb] = base[jb]; });
         } else {
-          float av = Ks[(32 * kb + lr) * C::KS + 2 * s + g];
-          S[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, qf[s], S[kb], 0, 0, 0);
+          static_for<8>([&](auto jb) { pq[it][jb] = (row_ok && 8 * gi + jb < a.nb) ? base[jb] : pq_ident; });
         }
       });
+    };
+    // one pipeline step: tile j in S, tile j+1 into Sn
+    auto step = [&](int j, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
+      // (the next tile's QK runs whenever this tile does; past the wave's last
+      // tile its result is never used)
+      if (j < nact) softmax_pv(j, j % 3, S, (j + 1) % 3, Sn);
+      if (j + 2 < nkv) store_tile((j + 2) % 3);
+      if (j + 3 < nkv) load_tile(j + 3);
+      __syncthreads();
+    };
+
+    // ---- fill: tiles 0 and 1 into stages 0 and 1, tile 2 into registers ----
+    load_tile(0);
+    store_tile(0);
+    if (nkv > 1) { load_tile(1); store_tile(1); }
+    if (nkv > 2) load_tile(2);
+    __syncthreads();
+    f32x16 SA[2], SB[2];
+    if (nact > 0) qk(0, SA);
+    for (int j = 0; j < nkv; j += 2) {
+      step(j, SA, SB);
+      if (j + 1 < nkv) step(j + 1, SB, SA);
+    }
+    load_epilogue_quats(std::integral_constant<int, 0>{}, std::integral_constant<int, C::EPI>{});
+
+    // ---- epilogue: normalise, stage O^T, back-rotate o = P oh, store ----
+    float lt = pair_sum(l_run);
+    const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
+    static_for<DP / 32>([&](auto db) {
+      static_for<16>([&](auto r) {
+        Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][(int)r] * inv;
+      });
     });
-  };
-  // online softmax (log2 units, one lane pair per query) and O^T += V^T P^T
-  // of tile kt (stage st); the QK MFMAs of the next tile (stage stn, into Sn)
-  // are issued in the same basic block as the exponentials so the two overlap.
-  auto softmax_pv = [&](int kt, int st, f32x16 (&S)[2], int stn, f32x16 (&Sn)[2]) {
-    const T* Vs = kv + st * C::kStage + kBN * C::KS;
-    const int64_t k0 = (int64_t)kt * kBN;
-    if (k0 + kBN - 1 > qw) {             // tile reaches past this wave's first query
-      const int rel = (int)(qw - k0) + lr - 4 * g;     // key offset limit for this lane
-      static_for<2>([&](auto kb) {
-        static_for<16>([&](auto r) {
-          if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) S[kb][(int)r] = -INFINITY;
-        });
-      });
-    }
-    const float mx = pair_max(tile_max(S)) * c;
-    // each row decides for itself (a row's result never depends on its
-    // neighbours'); the wave-uniform branch only skips the work, rare after warm-up
-    const bool need = mx > m_run + kRescaleThreshold;
-    if (__any(need)) {
-      const float m_new = need ? mx : m_run;
-      const float corr = exp2f(m_run - m_new);
-      m_run = m_new;
-      l_run *= corr;
-      static_for<DP / 32>([&](auto i) { O[i] *= corr; });
-    }
-    const float nm = -m_run;
-    qk(stn, Sn);
-    static_for<2>([&](auto kb) {
-      static_for<16>([&](auto r) { S[kb][(int)r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][(int)r], c, nm)); });
-    });
-    if constexpr (kBF) {
-      // P^T operand in bf16; the row sum is taken over the same rounded
-      // values (two per v_dot2), so numerator and denominator agree.
-      bf16x8 pb[2][2];
-      static_for<2>([&](auto kb) {
-        static_for<2>([&](auto hh) {
-          static_for<8>([&](auto e) { pb[kb][hh][(int)e] = (bf16)S[kb][8 * hh + e]; });
-        });
-      });
-      // four independent partial sums (one per P^T operand), then a tree
-      float ls[2][2];
-      const bf16x2 one2 = {(bf16)1.f, (bf16)1.f};
-      static_for<2>([&](auto kb) {
-        static_for<2>([&](auto hh) {
-          ls[kb][hh] = 0.f;
-          static_for<4>([&](auto e) {
-            bf16x2 pr = {pb[kb][hh][2 * e], pb[kb][hh][2 * e + 1]};
-            ls[kb][hh] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, ls[kb][hh], false);
-          });
-        });
-      });
-      l_run += (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
-      static_for<2>([&](auto kb) {
-        static_for<2>([&](auto hh) {
-          static_for<DP / 32>([&](auto db) {          // independent accumulators back to back
-            const T* vr = &Vs[(32 * db + lr) * C::VS + 32 * kb + 16 * hh + 4 * g];
-            bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
-            bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 8);
-            bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[kb][hh], O[db], 0, 0, 0);
-          });
-        });
-      });
-    } else {
-      float t[16];
-      static_for<16>([&](auto r) { t[r] = S[0][(int)r] + S[1][(int)r]; });
-      static_for<8>([&](auto r) { t[r] += t[r + 8]; });
-      static_for<4>([&](auto r) { t[r] += t[r + 4]; });
-      static_for<2>([&](auto r) { t[r] += t[r + 2]; });
-      l_run += t[0] + t[1];
-      static_for<2>([&](auto kb) {
-        static_for<16>([&](auto r) {
-          static_for<DP / 32>([&](auto db) {
-            float av = Vs[(32 * db + lr) * C::VS + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3)];
-            O[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, S[kb][(int)r], O[db], 0, 0, 0);
-          });
-        });
-      });
-    }
-  };
-  // quaternions of the epilogue items (row, 8 consecutive 3-dim groups); a
-  // row's 8 quaternions are 128 contiguous bytes in fp32, 64 in int16
-  typedef typename std::conditional<PQ16, u32x2, f32x4>::type pq_t;
-  const pq_t pq_ident = [] {
-    if constexpr (PQ16) return u32x2{1u, 0u};            // (1, 0, 0, 0)
-    else return f32x4{1.f, 0.f, 0.f, 0.f};
-  }();
-  pq_t pq[C::EPI][8];
-  auto load_epilogue_quats = [&](auto first, auto count) {
-    static_for<decltype(count)::value>([&](auto k) {
-      constexpr int it = decltype(first)::value + decltype(k)::value;
+    __syncthreads();
+    // item = (row, 8 consecutive 3-dim groups = 24 dims), quaternions in pq
+    static_for<C::EPI>([&](auto it) {
       const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
       const int64_t t = q0 + r;
-      const bool row_ok = idx < kBM * C::NG8 && t < a.T;
-      const pq_t* base = reinterpret_cast<const pq_t*>(
-          reinterpret_cast<const char*>(a.P) + ((bh * a.T + t) * a.nb + 8 * gi) * (int64_t)sizeof(pq_t));
-      if (row_ok && 8 * gi + 8 <= a.nb) {
-        static_for<8>([&](auto jb) { pq[it][jb] = base[jb]; });
+      if (idx >= kBM * C::NG8 || t >= a.T || 24 * gi >= a.d) return;
+      float u[24];
+      static_for<24>([&](auto j) { u[j] = (24 * gi + j < DP) ? Os[r * C::OS + 24 * gi + j] : 0.f; });
+      static_for<8>([&](auto jb) {
+        if (8 * gi + jb < a.nb) {
+          float y0, y1, y2;
+          quat qr;
+          if constexpr (PQ16) qr = unpack_quat_snorm16(pq[it][jb]);
+          else qr = quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]};
+          quat_rotate(qr, u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
+          u[3 * jb] = y0; u[3 * jb + 1] = y1; u[3 * jb + 2] = y2;
+        }
+      });
+      T* orow = reinterpret_cast<T*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs + 24 * gi;
+      if (24 * gi + 24 <= a.d && (reinterpret_cast<uintptr_t>(orow) & 15) == 0) {
+        constexpr int E = 16 / sizeof(T);
+        static_for<24 / E>([&](auto cc) {
+          u32x4 raw;
+          T* e = reinterpret_cast<T*>(&raw);
+          static_for<E>([&](auto j) { e[j] = from_f32<T>(u[cc * E + j]); });
+          reinterpret_cast<u32x4*>(orow)[cc] = raw;
+        });
       } else {
-        static_for<8>([&](auto jb) { pq[it][jb] = (row_ok && 8 * gi + jb < a.nb) ? base[jb] : pq_ident; });
+        static_for<24>([&](auto j) {
+          if (24 * gi + j < a.d) orow[j] = from_f32<T>(u[j]);
+        });
       }
     });
   };
-  // one pipeline step: tile j in S, tile j+1 into Sn
-  auto step = [&](int j, f32x16 (&S)[2], f32x16 (&Sn)[2]) {
-    // (the next tile's QK runs whenever this tile does; past the wave's last
-    // tile its result is never used)
-    if (j < nact) softmax_pv(j, j % 3, S, (j + 1) % 3, Sn);
-    if (j + 2 < nkv) store_tile((j + 2) % 3);
-    if (j + 3 < nkv) load_tile(j + 3);
-    __syncthreads();
-  };
-
-  // ---- fill: tiles 0 and 1 into stages 0 and 1, tile 2 into registers ----
-  load_tile(0);
-  store_tile(0);
-  if (nkv > 1) { load_tile(1); store_tile(1); }
-  if (nkv > 2) load_tile(2);
-  __syncthreads();
-  f32x16 SA[2], SB[2];
-  if (nact > 0) qk(0, SA);
-  for (int j = 0; j < nkv; j += 2) {
-    step(j, SA, SB);
-    if (j + 1 < nkv) step(j + 1, SB, SA);
+  run_tile(ntile - 1 - f);
+  if (f != ntile - 1 - f) {
+    __syncthreads();                       // the first tile's epilogue is done with the LDS
+    run_tile(f);
   }
-  load_epilogue_quats(std::integral_constant<int, 0>{}, std::integral_constant<int, C::EPI>{});
-
-  // ---- epilogue: normalise, stage O^T, back-rotate o = P oh, store ----
-  float lt = pair_sum(l_run);
-  const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
-  static_for<DP / 32>([&](auto db) {
-    static_for<16>([&](auto r) {
-      Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][(int)r] * inv;
-    });
-  });
-  __syncthreads();
-  // item = (row, 8 consecutive 3-dim groups = 24 dims), quaternions in pq
-  static_for<C::EPI>([&](auto it) {
-    const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
-    const int64_t t = q0 + r;
-    if (idx >= kBM * C::NG8 || t >= a.T || 24 * gi >= a.d) return;
-    float u[24];
-    static_for<24>([&](auto j) { u[j] = (24 * gi + j < DP) ? Os[r * C::OS + 24 * gi + j] : 0.f; });
-    static_for<8>([&](auto jb) {
-      if (8 * gi + jb < a.nb) {
-        float y0, y1, y2;
-        quat qr;
-        if constexpr (PQ16) qr = unpack_quat_snorm16(pq[it][jb]);
-        else qr = quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]};
-        quat_rotate(qr, u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
-        u[3 * jb] = y0; u[3 * jb + 1] = y1; u[3 * jb + 2] = y2;
-      }
-    });
-    T* orow = reinterpret_cast<T*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs + 24 * gi;
-    if (24 * gi + 24 <= a.d && (reinterpret_cast<uintptr_t>(orow) & 15) == 0) {
-      constexpr int E = 16 / sizeof(T);
-      static_for<24 / E>([&](auto cc) {
-        u32x4 raw;
-        T* e = reinterpret_cast<T*>(&raw);
-        static_for<E>([&](auto j) { e[j] = from_f32<T>(u[cc * E + j]); });
-        reinterpret_cast<u32x4*>(orow)[cc] = raw;
-      });
-    } else {
-      static_for<24>([&](auto j) {
-        if (24 * gi + j < a.d) orow[j] = from_f32<T>(u[j]);
-      });
-    }
-  });
 }
 
 template <typename T, int DP, bool PQ16>
@@ -375,8 +388,8 @@ static hipError_t launch_attn_dp(const AttnArgs& a, hipStream_t s) {
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&attn_fwd<T, DP, PQ16>), hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::lds);
   if (attr != hipSuccess) return attr;
-  const int64_t ntile = (a.T + kBM - 1) / kBM;
-  hipLaunchKernelGGL((attn_fwd<T, DP, PQ16>), dim3((unsigned)(a.B * a.H * ntile)), dim3(kThreads),
+  const int64_t nfold = ((a.T + kBM - 1) / kBM + 1) / 2;
+  hipLaunchKernelGGL((attn_fwd<T, DP, PQ16>), dim3((unsigned)(a.B * a.H * nfold)), dim3(kThreads),
                      C::lds, s, a);
   return hipGetLastError();
 }
