@@ -91,3 +91,40 @@ def layer_inputs(seed: int, B: int, T: int, d_model: int, n_heads: int,
         out["edge_mlp.2.weight"] = normal(seed, "edge_mlp.2.weight", (H * m, 4 * D), 1.0 / np.sqrt(4 * D))
         out["edge_mlp.2.bias"] = normal(seed, "edge_mlp.2.bias", (H * m,), 0.1)
     return out
+
+
+def uniform_ints(seed: int, name: str, shape, high: int) -> np.ndarray:
+    """int64 array uniform in [0, high), row-major over `shape`."""
+    shape = tuple(int(s) for s in shape)
+    n = int(np.prod(shape)) if shape else 1
+    u = uniform(seed, name, n)
+    return np.minimum((u * high).astype(np.int64), high - 1).reshape(shape)
+
+
+def decoder_inputs(seed: int, vocab: int, d_model: int, n_heads: int, n_layers: int,
+                   link_mode: str = "additive"):
+    """Seeded weights of a `HoloDecoder` (keys = its state_dict keys).
+
+    Embedding ~ N(0, 1); per block the attention weights of `layer_inputs`
+    (a seed of its own per block), LayerNorm weights 1 + N(0, 0.1^2) and
+    biases N(0, 0.1^2) (so the affine part is exercised), MLP weights
+    N(0, 1/fan_in) with N(0, 0.1^2) biases; LM head N(0, 1/d_model).
+    Returns a dict of float64 numpy arrays.
+    """
+    D = d_model
+    out = {"embed.weight": normal(seed, "embed.weight", (vocab, D))}
+    for i in range(n_layers):
+        p = f"blocks.{i}."
+        core = layer_inputs(seed * 1000003 + i + 1, 1, 1, D, n_heads, link_mode)
+        core.pop("x")
+        for k, v in core.items():
+            out[p + "core." + k] = v
+        for ln in ("ln1", "ln2"):
+            out[p + ln + ".weight"] = 1.0 + normal(seed, p + ln + ".weight", (D,), 0.1)
+            out[p + ln + ".bias"] = normal(seed, p + ln + ".bias", (D,), 0.1)
+        out[p + "ff.0.weight"] = normal(seed, p + "ff.0.weight", (4 * D, D), 1.0 / np.sqrt(D))
+        out[p + "ff.0.bias"] = normal(seed, p + "ff.0.bias", (4 * D,), 0.1)
+        out[p + "ff.2.weight"] = normal(seed, p + "ff.2.weight", (D, 4 * D), 1.0 / np.sqrt(4 * D))
+        out[p + "ff.2.bias"] = normal(seed, p + "ff.2.bias", (D,), 0.1)
+    out["lm_head.weight"] = normal(seed, "lm_head.weight", (vocab, D), 1.0 / np.sqrt(D))
+    return out

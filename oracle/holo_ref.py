@@ -37,6 +37,10 @@ Pinning (every function has at least one independent check in tests/):
   forward_blocks -> forward_chunked (fp64), flat-connection reduction
            (edge_scale = 0 gives torch's causal scaled_dot_product_attention),
            gauge invariance, causal prefix consistency, forward_arc_walk.
+  decoder_forward -> at edge_scale = 0 (P = I) a stack of torch's own pre-LN
+           nn.TransformerEncoderLayer (GELU, causal mask, zero attention
+           biases, the per-head interleaved qkv rows reordered into torch's
+           [q; k; v] layout) in float64; causal prefix consistency.
 """
 from __future__ import annotations
 
@@ -376,3 +380,39 @@ def forward_arc_walk(x: np.ndarray, W: Dict[str, np.ndarray], n_heads: int,
         p /= p.sum(-1, keepdims=True)
         out[:, :, i] = np.einsum("bhj,bhjd->bhd", p, Vt)
     return out.transpose(0, 2, 1, 3).reshape(B, T, D) @ np.asarray(W["out.weight"], np.float64).T
+
+
+# --------------------------------------------------------------------------
+# decoder stack (experiments/session_cherry.py:286-294 block, :315-327 hidden)
+# --------------------------------------------------------------------------
+def _layer_norm64(h: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float = 1e-5) -> np.ndarray:
+    """nn.LayerNorm over the last dim (biased variance), float64."""
+    mu = h.mean(axis=-1, keepdims=True)
+    var = ((h - mu) ** 2).mean(axis=-1, keepdims=True)
+    return (h - mu) / np.sqrt(var + eps) * w + b
+
+
+def _gelu64(x: np.ndarray) -> np.ndarray:
+    """nn.GELU() (exact erf form), float64."""
+    return torch.nn.functional.gelu(torch.as_tensor(x)).numpy()
+
+
+def decoder_forward(tokens: np.ndarray, W: Dict[str, np.ndarray], n_layers: int, n_heads: int,
+                    edge_scale: float, link_mode: str = "additive",
+                    return_hidden: bool = False) -> np.ndarray:
+    """float64 forward of the pre-LN decoder: h = embed[tokens]; per block
+    h += attention(ln1(h)) (forward_blocks) and h += ff(ln2(h)) with
+    ff = Linear -> GELU -> Linear (session_cherry.py:292-294); logits = h W_lm^T."""
+    W = {k: np.asarray(v, dtype=np.float64) for k, v in W.items()}
+    h = W["embed.weight"][np.asarray(tokens)]
+    for i in range(n_layers):
+        p = f"blocks.{i}."
+        core = {k[len(p) + 5:]: v for k, v in W.items() if k.startswith(p + "core.")}
+        a = _layer_norm64(h, W[p + "ln1.weight"], W[p + "ln1.bias"])
+        h = h + forward_blocks(a, core, n_heads, edge_scale, link_mode)
+        a = _layer_norm64(h, W[p + "ln2.weight"], W[p + "ln2.bias"])
+        f = _gelu64(a @ W[p + "ff.0.weight"].T + W[p + "ff.0.bias"])
+        h = h + f @ W[p + "ff.2.weight"].T + W[p + "ff.2.bias"]
+    if return_hidden:
+        return h
+    return h @ W["lm_head.weight"].T
