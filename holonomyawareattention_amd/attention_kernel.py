@@ -24,7 +24,11 @@ dropout is inactive and x is on the GPU (the conditions of
 kernel/attention_kernel.py:203-208; return_geometry is also supported).
 Anything else raises NotImplementedError, as the guarded reference does
 (kernel/attention_fast_chunked.py:106-114): there is no second code path.
-Forward only: the backward of the fused path raises NotImplementedError.
+Under autograd the projections are ordinary differentiable torch GEMMs and the
+scan + attention core is one autograd function whose backward is the gfx950
+backward (holo_attn_bwd; the reference recomputes its forward under autograd,
+kernel/attention_kernel.py:174-187). The geometry output is not differentiable
+(return_geometry under autograd raises NotImplementedError).
 """
 from __future__ import annotations
 
@@ -46,20 +50,64 @@ def _is_exact_tril(mask: Optional[torch.Tensor], L: int) -> bool:
     return torch.equal(mask.bool(), tril)
 
 
-class _ForwardOnly(torch.autograd.Function):
-    """Attaches the kernel output to the autograd graph; its backward is the
-    unfused-recompute counterpart of kernel/attention_kernel.py:174-187, which
-    this build does not provide yet."""
+class _MatmulF32Out(torch.autograd.Function):
+    """x2 (N, D) @ w^T with an fp32 output (the generator projections: link
+    parameters are never rounded to bf16). The backward rounds the incoming
+    fp32 gradient to x's dtype for its two GEMMs."""
 
     @staticmethod
-    def forward(ctx, y, *inputs):
-        return y.view_as(y)
+    def forward(ctx, x2, w):
+        ctx.save_for_backward(x2, w)
+        if x2.dtype == torch.float32:
+            return x2 @ w.t()
+        return torch.mm(x2, w.t(), out_dtype=torch.float32)
 
     @staticmethod
-    def backward(ctx, grad):
-        raise NotImplementedError(
-            "holonomyawareattention_amd: the fused path is forward-only "
-            "(backward is not implemented)")
+    def backward(ctx, dg):
+        x2, w = ctx.saved_tensors
+        dgl = dg.to(x2.dtype)
+        dx = dgl @ w if ctx.needs_input_grad[0] else None
+        dw = dgl.t() @ x2 if ctx.needs_input_grad[1] else None
+        return dx, dw
+
+
+class _PathAttention(torch.autograd.Function):
+    """o (B,L,H,d) = scan + causal attention + back-rotation of q, k, v (views
+    of qkv (B,L,H,3d)) under the links of the fp32 generator output g
+    ((B,L,2*H*m) = [gq | gk] for the additive generator, (B,L,H*m) for the
+    interaction MLP). Backward: holo_attn_bwd, returning dqkv and dg."""
+
+    @staticmethod
+    def forward(ctx, qkv, g, edge_scale, scale, additive, d):
+        B, L, H, _ = qkv.shape
+        m = 3 * (d // 3)
+        gq, gk = _PathAttention._gviews(g, B, L, H, m, additive)
+        qh, kh, vh_t, P, _ = kernels.geom_scan(qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:],
+                                                gq, gk, edge_scale, p_format="f32")
+        lse = torch.empty((B, H, qh.shape[2]), dtype=torch.float32, device=qkv.device)
+        o = kernels.attention(qh, kh, vh_t, P, d, scale, lse=lse)
+        ctx.save_for_backward(g, qh, kh, vh_t, P, lse, o)
+        ctx.cfg = (edge_scale, scale, additive, d, H, m, tuple(qkv.shape))
+        return o
+
+    @staticmethod
+    def _gviews(g, B, L, H, m, additive):
+        if additive:
+            return g[..., :H * m].view(B, L, H, m), g[..., H * m:].view(B, L, H, m)
+        return g.view(B, L, H, m), None
+
+    @staticmethod
+    def backward(ctx, do):
+        g, qh, kh, vh_t, P, lse, o = ctx.saved_tensors
+        es, scale, additive, d, H, m, shp = ctx.cfg
+        B, L = shp[0], shp[1]
+        dqkv = torch.empty(shp, dtype=o.dtype, device=o.device)
+        dg = torch.empty_like(g)
+        gq, gk = _PathAttention._gviews(g, B, L, H, m, additive)
+        dgq, dgk = _PathAttention._gviews(dg, B, L, H, m, additive)
+        kernels.attention_backward(gq, gk, es, qh, kh, vh_t, P, lse, o, do.contiguous(), d, scale,
+                                   dqkv[..., :d], dqkv[..., d:2 * d], dqkv[..., 2 * d:], dgq, dgk)
+        return dqkv, dg, None, None, None, None
 
 
 class PathOrderedGeometricMHA(nn.Module):
@@ -164,15 +212,31 @@ class PathOrderedGeometricMHA(nn.Module):
     def _edge_params(self, pair: torch.Tensor) -> torch.Tensor:
         """Interaction generator on (..., 2D) pairs [x_t ; x_{t+1}]
         (core/attention_fast_chunked.py:73-77): (N, H*m) with the last layer
-        written in fp32."""
+        written in fp32 (differentiable)."""
         hid = self.edge_mlp[1](self.edge_mlp[0](pair)).reshape(-1, 4 * self.h * self.d)
         lin2 = self.edge_mlp[2]
         if pair.dtype == torch.float32:
             return F.linear(hid, lin2.weight, lin2.bias)
-        g = torch.mm(hid, lin2.weight.t(), out_dtype=torch.float32)
+        g = _MatmulF32Out.apply(hid, lin2.weight)
         if lin2.bias is not None:
             g = g + lin2.bias.float()
         return g
+
+    def _forward_autograd(self, x: torch.Tensor) -> torch.Tensor:
+        """Differentiable forward: torch GEMMs for the projections and the
+        generator, _PathAttention for the core."""
+        B, L, D = x.shape
+        H, d, m = self.h, self.d, self.m_dim
+        qkv = F.linear(x, self.qkv.weight).view(B, L, H, 3 * d)
+        additive = self.link_mode == "additive"
+        if additive:
+            wg = torch.cat([self.gqproj.weight, self.gkproj.weight], 0)
+            g = _MatmulF32Out.apply(x.reshape(B * L, D), wg).view(B, L, 2 * H * m)
+        else:
+            pair = torch.cat([x, torch.roll(x, shifts=-1, dims=1)], dim=-1)
+            g = self._edge_params(pair).view(B, L, H * m)
+        o = _PathAttention.apply(qkv, g, self.edge_scale, self.scale, additive, d)
+        return F.linear(o.reshape(B, L, D), self.out.weight)
 
     @staticmethod
     def _p_format(x: torch.Tensor, return_geometry: bool) -> str:
@@ -192,6 +256,12 @@ class PathOrderedGeometricMHA(nn.Module):
         B, L, D = x.shape
         params = [p for p in self.parameters() if p.requires_grad]
         track = torch.is_grad_enabled() and (x.requires_grad or bool(params))
+        if track:
+            if return_geometry:
+                raise NotImplementedError(
+                    "holonomyawareattention_amd kernel path does not support this call: "
+                    "return_geometry under autograd (the geometry output is not differentiable)")
+            return self._forward_autograd(x), None
         ev = self._stage_events
         with torch.no_grad():
             if ev is not None:
@@ -210,8 +280,6 @@ class PathOrderedGeometricMHA(nn.Module):
             y = F.linear(o.view(B, L, D), self.out.weight)
             if ev is not None:
                 ev[4].record()
-        if track:
-            y = _ForwardOnly.apply(y, x, *params)
         if not return_geometry:
             return y, None
         d = self.d

@@ -48,13 +48,40 @@ int check_common(int B, int64_t T, int H, int d) {
   return HOLO_OK;
 }
 
+// Backward workspace, each region 256-byte aligned: doh, doh_t, qh_t, kh_t,
+// vh (io dtype, B*H*Tp*Dp each), delta (fp32, B*H*Tp), dqh, dkh, dvh (fp32,
+// B*H*Tp*Dp each), the chained suffix sums (fp32, B*H*nch*nb*4) and the
+// ticket counter / time-out flag. Returns the total; fills `a` when given.
+size_t bwd_layout(int B, int64_t T, int H, int d, size_t es, void* base, holo::BwdArgs* a) {
+  const int64_t Tp = holo::padded_seq(T), nch = Tp / holo::kChunk;
+  const size_t n = (size_t)B * H * Tp * holo::padded_head_dim(d);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return base ? static_cast<char*>(base) + at : nullptr;
+  };
+  void* r[5];
+  for (auto& p : r) p = take(n * es);
+  float* delta = reinterpret_cast<float*>(take((size_t)B * H * Tp * 4));
+  float* g[3];
+  for (auto& p : g) p = reinterpret_cast<float*>(take(n * 4));
+  float* carry = reinterpret_cast<float*>(take((size_t)B * H * nch * (d / 3) * 16));
+  unsigned* ticket = reinterpret_cast<unsigned*>(take(256));
+  if (a) {
+    a->doh = r[0]; a->doh_t = r[1]; a->qh_t = r[2]; a->kh_t = r[3]; a->vh = r[4];
+    a->delta = delta; a->dqh = g[0]; a->dkh = g[1]; a->dvh = g[2]; a->carry = carry; a->ticket = ticket;
+  }
+  return off;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (3 << 16) | 0; }
+int holo_abi_version(void) { return (4 << 16) | 0; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -146,7 +173,7 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
 
 int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float scale,
                   const void* qh, const void* kh, const void* vh_t, const void* P,
-                  void* o, int64_t o_rs, int64_t o_hs, void* stream) {
+                  void* o, int64_t o_rs, int64_t o_hs, float* lse, void* stream) {
   g_last_error.clear();
   int rc = check_common(B, T, H, d);
   if (rc) return rc;
@@ -158,8 +185,8 @@ int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float
   if (!qh || !kh || !vh_t || !o || (nb > 0 && !P))
     return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
   if ((rc = check_layout("o", o_rs, o_hs, H, d))) return rc;
-  if (!aligned16(qh) || !aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)))
-    return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t and P must be 16-byte aligned");
+  if (!aligned16(qh) || !aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)) || (lse && !aligned16(lse)))
+    return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t, P and lse must be 16-byte aligned");
   if (!(scale > 0.f) || !(scale < 1e30f))
     return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
   // key/value tiles of one (b, h) are addressed with 32-bit byte offsets
@@ -173,10 +200,80 @@ int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float
   a.qh = qh; a.kh = kh; a.vh_t = vh_t; a.P = P;
   a.o = o; a.o_rs = o_rs; a.o_hs = o_hs;
   a.p_format = p_format;
+  a.lse = lse;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = dtype == HOLO_F32 ? holo::launch_attn<float>(a, s)
                                    : holo::launch_attn<holo::bf16>(a, s);
   if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "attention launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+size_t holo_attn_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || (dtype != HOLO_F32 && dtype != HOLO_BF16)) return 0;
+  return bwd_layout(B, T, H, d, dtype == HOLO_F32 ? 4 : 2, nullptr, nullptr);
+}
+
+int holo_attn_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                  float scale,
+                  const void* gq, int64_t gq_rs, int64_t gq_hs, const void* gk, int64_t gk_rs, int64_t gk_hs,
+                  const void* qh, const void* kh, const void* vh_t, const float* P, const float* lse,
+                  const void* o, int64_t o_rs, int64_t o_hs, const void* dout, int64_t do_rs, int64_t do_hs,
+                  void* dq, int64_t dq_rs, int64_t dq_hs, void* dk, int64_t dk_rs, int64_t dk_hs,
+                  void* dv, int64_t dv_rs, int64_t dv_hs,
+                  float* dgq, int64_t dgq_rs, int64_t dgq_hs, float* dgk, int64_t dgk_rs, int64_t dgk_hs,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  int rc = check_common(B, T, H, d);
+  if (rc) return rc;
+  if (io_dtype != HOLO_F32 && io_dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "io_dtype %d is not HOLO_F32 or HOLO_BF16", io_dtype);
+  if (gen_dtype != HOLO_F32)
+    return fail(HOLO_ERR_UNSUPPORTED, "the backward takes an fp32 generator (gen_dtype %d)", gen_dtype);
+  if (gen_mode != HOLO_GEN_ADDITIVE && gen_mode != HOLO_GEN_DIRECT)
+    return fail(HOLO_ERR_INVALID_ARG, "gen_mode %d unknown", gen_mode);
+  const int nb = d / 3;
+  if (!qh || !kh || !vh_t || !lse || !o || !dout || !dq || !dk || !dv || (nb > 0 && (!P || !gq || !dgq)))
+    return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if (nb > 0 && gen_mode == HOLO_GEN_ADDITIVE && (!gk || !dgk))
+    return fail(HOLO_ERR_INVALID_ARG, "additive generator needs gk and dgk");
+  if (nb > 0) {
+    if ((rc = check_layout("gq", gq_rs, gq_hs, H, 3 * nb))) return rc;
+    if ((rc = check_layout("dgq", dgq_rs, dgq_hs, H, 3 * nb))) return rc;
+    if (gen_mode == HOLO_GEN_ADDITIVE) {
+      if ((rc = check_layout("gk", gk_rs, gk_hs, H, 3 * nb))) return rc;
+      if ((rc = check_layout("dgk", dgk_rs, dgk_hs, H, 3 * nb))) return rc;
+    }
+  }
+  if ((rc = check_layout("o", o_rs, o_hs, H, d))) return rc;
+  if ((rc = check_layout("dout", do_rs, do_hs, H, d))) return rc;
+  if ((rc = check_layout("dq", dq_rs, dq_hs, H, d))) return rc;
+  if ((rc = check_layout("dk", dk_rs, dk_hs, H, d))) return rc;
+  if ((rc = check_layout("dv", dv_rs, dv_hs, H, d))) return rc;
+  if (!aligned16(qh) || !aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)) || !aligned16(lse))
+    return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t, P and lse must be 16-byte aligned");
+  if (!(scale > 0.f) || !(scale < 1e30f))
+    return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
+  const size_t es = io_dtype == HOLO_F32 ? 4 : 2;
+  const size_t need = bwd_layout(B, T, H, d, es, nullptr, nullptr);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
+                need, workspace ? workspace_bytes : (size_t)0);
+
+  holo::BwdArgs a;
+  a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d); a.gen_mode = gen_mode;
+  a.T = T; a.Tp = holo::padded_seq(T); a.nch = a.Tp / holo::kChunk;
+  a.scale = scale; a.scale_log2 = scale * 1.4426950408889634f; a.edge_scale = edge_scale;
+  a.gq = gq; a.gq_rs = gq_rs; a.gq_hs = gq_hs; a.gk = gk; a.gk_rs = gk_rs; a.gk_hs = gk_hs;
+  a.qh = qh; a.kh = kh; a.vh_t = vh_t; a.P = P; a.lse = lse;
+  a.o = o; a.o_rs = o_rs; a.o_hs = o_hs; a.dout = dout; a.do_rs = do_rs; a.do_hs = do_hs;
+  a.dq = dq; a.dq_rs = dq_rs; a.dq_hs = dq_hs; a.dk = dk; a.dk_rs = dk_rs; a.dk_hs = dk_hs;
+  a.dv = dv; a.dv_rs = dv_rs; a.dv_hs = dv_hs;
+  a.dgq = dgq; a.dgq_rs = dgq_rs; a.dgq_hs = dgq_hs; a.dgk = dgk; a.dgk_rs = dgk_rs; a.dgk_hs = dgk_hs;
+  bwd_layout(B, T, H, d, es, workspace, &a);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = io_dtype == HOLO_F32 ? holo::launch_bwd<float, float>(a, s)
+                                      : holo::launch_bwd<holo::bf16, float>(a, s);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "backward launch: %s", hipGetErrorString(e));
   return HOLO_OK;
 }
 

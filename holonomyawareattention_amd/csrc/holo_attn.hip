@@ -336,6 +336,7 @@ attn_fwd(AttnArgs a) {
     // ---- epilogue: normalise, stage O^T, back-rotate o = P oh, store ----
     float lt = pair_sum(l_run);
     const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
+    if (a.lse && g == 0 && qw + lr < a.T) a.lse[(int64_t)bh * a.Tp + qw + lr] = m_run + __log2f(lt);
     static_for<DP / 32>([&](auto db) {
       static_for<16>([&](auto r) {
         Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][(int)r] * inv;

@@ -1,0 +1,609 @@
+// Backward of the path-ordered attention forward (scan + attention) on gfx950.
+//
+// Reference behaviour: gradients of core/attention_fast_chunked.py:63-173
+// (its kernel path recomputes the backward through PyTorch autograd,
+// kernel/attention_kernel.py:174-187). With qh = P^T q, kh = P^T k, vh = P^T v,
+// oh = softmax(scale qh kh^T) vh and o = P oh, the gradient splits into
+//   1. doh = P^T do and delta = rowsum(do * o) (= rowsum(doh * oh)),
+//   2. the causal softmax-attention backward in the path frame:
+//        dS = Pm * (doh vh^T - delta),  dqh = scale dS kh,  dkh = scale dS^T qh,
+//        dvh = Pm^T doh                    (Pm recomputed from the saved LSE),
+//   3. dq = P dqh, dk = P dkh, dv = P dvh, and the links: with
+//        c_t = oh x doh + dqh x qh + dkh x kh + dvh x vh   (per 3-dim block),
+//      the reverse recursion of P_{t+1} = G_t P_t reduces to a suffix sum
+//      m_t = sum_{s >= t} c_s (P_t^T dL/dP_t summed along the path), and
+//      vee(G_t^T dL/dG_t - transpose) = P_t m_{t+1}; through the right
+//      Jacobian of exp on SO(3), dL/da_t = map(J_r(phi_t)^T P_t m_{t+1}).
+//      The closing edge only enters the holonomy (zero gradient).
+//
+// Kernels, in launch order:
+//   bwd_prep      one workgroup per (b, h, 64 tokens): doh (row-major and
+//                 tile-transposed), delta, and the other operand layouts the
+//                 MFMA kernels read (qh_t, kh_t, vh row-major)
+//   attn_bwd_dkdv one workgroup per (b, h, 128 keys); each wave keeps its 32
+//                 keys' K and V rows as MFMA operands in registers and sweeps
+//                 the causal query tiles: S, dP, then dV += Pm^T dO and
+//                 dK += dS^T Q with the probabilities already in the operand
+//                 layout of the second product
+//   attn_bwd_dq   one workgroup per (b, h, 128 queries), each wave 32 queries
+//                 in registers, sweeping key tiles: dQ^T += K^T dS^T
+//   link_bwd      chained suffix scan over 64-token chunks (reverse ticket
+//                 order, the same bounded-wait protocol as the forward scan),
+//                 then dq, dk, dv and the generator gradients
+#include <type_traits>
+
+#include "holo_chain.h"
+#include "holo_kernels.h"
+
+namespace holo {
+
+constexpr int kBT = 32;              // queries / keys per backward MFMA tile
+constexpr int kBwdThreads = 256;     // 4 waves
+
+template <typename T, int DP> struct BwdCfg {
+  static constexpr int E = 16 / sizeof(T);        // elements per 16 bytes
+  static constexpr int RS = DP + E;               // LDS stride of a row-major tile row
+  static constexpr int TS = kBT + E;              // LDS stride of a transposed tile row (16 B aligned)
+  static constexpr int QF = sizeof(T) == 2 ? DP / 16 : DP / 2;   // MFMA k-steps over DP
+};
+
+template <typename T> struct frag;
+template <> struct frag<bf16> { typedef bf16x8 type; };
+template <> struct frag<float> { typedef float type; };
+
+// 32 rows r0.. of a (rows, DP) row-major array into LDS (stride RS)
+template <typename T, int DP>
+__device__ __forceinline__ void load_rows(T* dst, const T* src, int tid) {
+  using C = BwdCfg<T, DP>;
+  constexpr int CPR = DP / C::E;
+  for (int i = tid; i < kBT * CPR; i += kBwdThreads) {
+    const int r = i / CPR, cc = i % CPR;
+    *reinterpret_cast<u32x4*>(&dst[r * C::RS + cc * C::E]) =
+        *reinterpret_cast<const u32x4*>(&src[(int64_t)r * DP + cc * C::E]);
+  }
+}
+
+// columns j0 .. j0+31 of a transposed (DP, 64) tile into LDS (stride TS)
+template <typename T, int DP>
+__device__ __forceinline__ void load_cols(T* dst, const T* tile, int j0, int tid) {
+  using C = BwdCfg<T, DP>;
+  constexpr int CPR = kBT / C::E;
+  for (int i = tid; i < DP * CPR; i += kBwdThreads) {
+    const int r = i / CPR, cc = i % CPR;
+    *reinterpret_cast<u32x4*>(&dst[r * C::TS + cc * C::E]) =
+        *reinterpret_cast<const u32x4*>(&tile[(int64_t)r * kChunk + j0 + cc * C::E]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_prep
+// ---------------------------------------------------------------------------
+// Transposes a 64 x DP row-major tile (src) into the (DP, 64) layout (dst),
+// or back when kToRows, through LDS (stride DP + E / 64 + E).
+template <typename T, int DP, bool kToRows>
+__device__ inline void transpose_tile(T* lds, const T* src, T* dst, int tid) {
+  constexpr int E = 16 / sizeof(T);
+  constexpr int SR = kToRows ? kChunk + E : DP + E;          // LDS stride of the source layout
+  constexpr int NR = kToRows ? DP : kChunk;                  // source rows
+  constexpr int NC = kToRows ? kChunk : DP;                  // source columns
+  __syncthreads();
+  for (int i = tid; i < NR * (NC / E); i += kBwdThreads) {
+    const int r = i / (NC / E), cc = i % (NC / E);
+    *reinterpret_cast<u32x4*>(&lds[r * SR + cc * E]) = *reinterpret_cast<const u32x4*>(&src[(int64_t)r * NC + cc * E]);
+  }
+  __syncthreads();
+  // destination: NC rows of NR elements; chunk (row c, part j) gathers column c
+  for (int i = tid; i < NC * (NR / E); i += kBwdThreads) {
+    const int c = i / (NR / E), j = i % (NR / E);
+    u32x4 raw;
+    T* e = reinterpret_cast<T*>(&raw);
+    static_for<E>([&](auto k) { e[k] = lds[(j * E + k) * SR + c]; });
+    *reinterpret_cast<u32x4*>(&dst[(int64_t)c * NR + j * E]) = raw;
+  }
+}
+
+template <typename T, int DP>
+__global__ void __launch_bounds__(kBwdThreads) bwd_prep(BwdArgs a) {
+  constexpr int E = 16 / sizeof(T);
+  constexpr int LDSN = (DP + E) * kChunk > (kChunk + E) * DP ? (DP + E) * kChunk : (kChunk + E) * DP;
+  __shared__ float Ds[kChunk][DP + 1];
+  __shared__ __align__(16) T Ts[LDSN];
+  const int tid = threadIdx.x;
+  const int64_t bh = blockIdx.x / a.nch, c = blockIdx.x % a.nch;
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const int tl = tid >> 2, p = tid & 3;
+  const int64_t t = c * kChunk + tl;
+  const bool in = t < a.T;
+
+  // doh = P^T do and the row dot do . o (4 threads per token)
+  for (int k = p; k < DP; k += 4) Ds[tl][k] = 0.f;
+  __syncthreads();
+  float dot = 0.f;
+  const T* orow = reinterpret_cast<const T*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs;
+  const T* drow = reinterpret_cast<const T*>(a.dout) + (b * a.T + t) * a.do_rs + h * a.do_hs;
+  if (in) {
+    for (int blk = p; blk < a.nb; blk += 4) {
+      const rot3 R = qmat(load_quat(a.P + ((bh * a.T + t) * a.nb + blk) * 4));
+      float u[3], v[3];
+      static_for<3>([&](auto k) { u[k] = to_f32(drow[3 * blk + k]); v[k] = to_f32(orow[3 * blk + k]); });
+      dot += u[0] * v[0] + u[1] * v[1] + u[2] * v[2];
+      float y0, y1, y2;
+      rot_t_apply(R, u[0], u[1], u[2], y0, y1, y2);
+      Ds[tl][3 * blk] = y0; Ds[tl][3 * blk + 1] = y1; Ds[tl][3 * blk + 2] = y2;
+    }
+    if (p == 0) {
+      for (int k = 3 * a.nb; k < a.d; ++k) {
+        const float u = to_f32(drow[k]);
+        dot += u * to_f32(orow[k]);
+        Ds[tl][k] = u;
+      }
+    }
+  }
+  dot += __shfl_xor(dot, 1);
+  dot += __shfl_xor(dot, 2);
+  if (p == 0) a.delta[bh * a.Tp + t] = in ? dot : 0.f;
+  __syncthreads();
+  // doh rows and doh transposed tile
+  T* dohr = reinterpret_cast<T*>(a.doh) + (bh * a.Tp + c * kChunk) * DP;
+  T* doht = reinterpret_cast<T*>(a.doh_t) + (bh * a.nch + c) * DP * kChunk;
+  for (int i = tid; i < kChunk * (DP / E); i += kBwdThreads) {
+    const int r = i / (DP / E), cc = i % (DP / E);
+    u32x4 raw;
+    T* e = reinterpret_cast<T*>(&raw);
+    static_for<E>([&](auto k) { e[k] = from_f32<T>(Ds[r][cc * E + k]); });
+    *reinterpret_cast<u32x4*>(&dohr[(int64_t)r * DP + cc * E]) = raw;
+  }
+  for (int i = tid; i < DP * (kChunk / E); i += kBwdThreads) {
+    const int r = i / (kChunk / E), cc = i % (kChunk / E);
+    u32x4 raw;
+    T* e = reinterpret_cast<T*>(&raw);
+    static_for<E>([&](auto k) { e[k] = from_f32<T>(Ds[cc * E + k][r]); });
+    *reinterpret_cast<u32x4*>(&doht[(int64_t)r * kChunk + cc * E]) = raw;
+  }
+  // the other operand layouts
+  const int64_t row0 = (bh * a.Tp + c * kChunk) * DP, tile0 = (bh * a.nch + c) * DP * kChunk;
+  transpose_tile<T, DP, false>(Ts, reinterpret_cast<const T*>(a.qh) + row0, reinterpret_cast<T*>(a.qh_t) + tile0, tid);
+  transpose_tile<T, DP, false>(Ts, reinterpret_cast<const T*>(a.kh) + row0, reinterpret_cast<T*>(a.kh_t) + tile0, tid);
+  transpose_tile<T, DP, true>(Ts, reinterpret_cast<const T*>(a.vh_t) + tile0, reinterpret_cast<T*>(a.vh) + row0, tid);
+}
+
+// ---------------------------------------------------------------------------
+// attention backward: dK, dV
+// ---------------------------------------------------------------------------
+// MFMA register layouts (32x32 tiles): the A operand lane l holds row l % 32,
+// the B operand column l % 32, each 8 (bf16) or 1 (fp32) values of the k
+// range; the accumulator lane l holds column l % 32 and rows
+// 8 (r / 4) + 4 (l / 32) + (r % 4), r = 0..15. A product whose k index runs
+// over the accumulator rows of an earlier product uses that same order for
+// both operands, so the accumulator is the operand with no data movement.
+template <typename T, int DP>
+__global__ void __launch_bounds__(kBwdThreads) attn_bwd_dkdv(BwdArgs a) {
+  using C = BwdCfg<T, DP>;
+  typedef typename frag<T>::type frag_t;
+  constexpr bool kBF = sizeof(T) == 2;
+  __shared__ __align__(16) T Qs[kBT * C::RS];
+  __shared__ __align__(16) T dOs[kBT * C::RS];
+  __shared__ __align__(16) T QTs[DP * C::TS];
+  __shared__ __align__(16) T dOTs[DP * C::TS];
+  __shared__ float lse_s[kBT], del_s[kBT];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, g = lane >> 5;
+  const int64_t nbh = (int64_t)a.B * a.H;
+  const int64_t kb = blockIdx.x / nbh, bh = blockIdx.x % nbh;      // key block 0 (most queries) first
+  const int64_t k0 = kb * 128, kw0 = k0 + 32 * w;
+  const bool wave_in = kw0 < a.T;
+
+  // this wave's 32 keys: K and V rows as B operands (key = lane % 32)
+  frag_t kf[C::QF], vf[C::QF];
+  {
+    const bool in = kw0 < a.Tp;
+    const T* krow = reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + kw0 + lr) * DP;
+    const T* vrow = reinterpret_cast<const T*>(a.vh) + (bh * a.Tp + kw0 + lr) * DP;
+    static_for<C::QF>([&](auto s) {
+      if constexpr (kBF) {
+        kf[s] = in ? *reinterpret_cast<const bf16x8*>(krow + 16 * s + 8 * g) : bf16x8{};
+        vf[s] = in ? *reinterpret_cast<const bf16x8*>(vrow + 16 * s + 8 * g) : bf16x8{};
+      } else {
+        kf[s] = in ? krow[2 * s + g] : 0.f;
+        vf[s] = in ? vrow[2 * s + g] : 0.f;
+      }
+    });
+  }
+  f32x16 dK[DP / 32], dV[DP / 32];
+  static_for<DP / 32>([&](auto i) { dK[i] = f32x16{}; dV[i] = f32x16{}; });
+  const float cl = a.scale_log2;
+  const int64_t key = kw0 + lr;
+  const int nqt = (int)((a.T + kBT - 1) / kBT);
+  for (int qt = (int)(k0 / kBT); qt < nqt; ++qt) {
+    const int64_t q0 = (int64_t)qt * kBT;
+    __syncthreads();
+    load_rows<T, DP>(Qs, reinterpret_cast<const T*>(a.qh) + (bh * a.Tp + q0) * DP, tid);
+    load_rows<T, DP>(dOs, reinterpret_cast<const T*>(a.doh) + (bh * a.Tp + q0) * DP, tid);
+    const int64_t tile = (bh * a.nch + q0 / kChunk) * DP * kChunk;
+    load_cols<T, DP>(QTs, reinterpret_cast<const T*>(a.qh_t) + tile, (int)(q0 % kChunk), tid);
+    load_cols<T, DP>(dOTs, reinterpret_cast<const T*>(a.doh_t) + tile, (int)(q0 % kChunk), tid);
+    if (tid < kBT) {
+      const bool qin = q0 + tid < a.T;
+      lse_s[tid] = qin ? a.lse[bh * a.Tp + q0 + tid] : INFINITY;
+      del_s[tid] = qin ? a.delta[bh * a.Tp + q0 + tid] : 0.f;
+    }
+    __syncthreads();
+    if (!wave_in || q0 + kBT - 1 < kw0) continue;     // no query of the tile sees these keys
+
+    // S = Q K^T and dP = dO V^T (queries on the rows, this wave's keys on the lanes)
+    f32x16 S = f32x16{}, dP = f32x16{};
+    static_for<C::QF>([&](auto s) {
+      if constexpr (kBF) {
+        const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&Qs[lr * C::RS + 16 * s + 8 * g]);
+        const bf16x8 da = *reinterpret_cast<const bf16x8*>(&dOs[lr * C::RS + 16 * s + 8 * g]);
+        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, kf[s], S, 0, 0, 0);
+        dP = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, vf[s], dP, 0, 0, 0);
+      } else {
+        S = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[lr * C::RS + 2 * s + g], kf[s], S, 0, 0, 0);
+        dP = __builtin_amdgcn_mfma_f32_32x32x2f32(dOs[lr * C::RS + 2 * s + g], vf[s], dP, 0, 0, 0);
+      }
+    });
+    // Pm = exp2(scale_log2 S - lse) (zero above the diagonal and for padding
+    // keys; padding queries carry lse = +inf), dS = Pm (dP - delta)
+    static_for<16>([&](auto r) {
+      const int qr = 8 * (r >> 2) + 4 * g + (r & 3);
+      float pm = exp2f(__builtin_fmaf(S[(int)r], cl, -lse_s[qr]));
+      if (key > q0 + qr || key >= a.T) pm = 0.f;
+      S[(int)r] = pm;
+      dP[(int)r] = pm * (dP[(int)r] - del_s[qr]);
+    });
+    // dV += Pm^T dO, dK += dS^T Q (this wave's keys on the rows, dims on the lanes)
+    if constexpr (kBF) {
+      bf16x8 pb[2], sb[2];
+      static_for<2>([&](auto hh) {
+        static_for<8>([&](auto e) { pb[hh][(int)e] = (bf16)S[8 * hh + e]; sb[hh][(int)e] = (bf16)dP[8 * hh + e]; });
+      });
+      static_for<2>([&](auto hh) {
+        static_for<DP / 32>([&](auto db) {
+          const T* dr = &dOTs[(32 * db + lr) * C::TS + 16 * hh + 4 * g];
+          const T* qr = &QTs[(32 * db + lr) * C::TS + 16 * hh + 4 * g];
+          const bf16x4 dlo = *reinterpret_cast<const bf16x4*>(dr), dhi = *reinterpret_cast<const bf16x4*>(dr + 8);
+          const bf16x4 qlo = *reinterpret_cast<const bf16x4*>(qr), qhi = *reinterpret_cast<const bf16x4*>(qr + 8);
+          const bf16x8 bo = {dlo[0], dlo[1], dlo[2], dlo[3], dhi[0], dhi[1], dhi[2], dhi[3]};
+          const bf16x8 bq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
+          dV[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pb[hh], bo, dV[db], 0, 0, 0);
+          dK[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sb[hh], bq, dK[db], 0, 0, 0);
+        });
+      });
+    } else {
+      static_for<16>([&](auto r) {
+        const int qr = 8 * (r >> 2) + 4 * g + (r & 3);
+        static_for<DP / 32>([&](auto db) {
+          dV[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(S[(int)r], dOTs[(32 * db + lr) * C::TS + qr], dV[db], 0, 0, 0);
+          dK[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(dP[(int)r], QTs[(32 * db + lr) * C::TS + qr], dK[db], 0, 0, 0);
+        });
+      });
+    }
+  }
+  if (kw0 < a.Tp) {
+    static_for<DP / 32>([&](auto db) {
+      static_for<16>([&](auto r) {
+        const int64_t off = (bh * a.Tp + kw0 + 8 * (r >> 2) + 4 * g + (r & 3)) * DP + 32 * db + lr;
+        a.dkh[off] = dK[db][(int)r] * a.scale;
+        a.dvh[off] = dV[db][(int)r];
+      });
+    });
+  }
+}
+
+// ---------------------------------------------------------------------------
+// attention backward: dQ
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ void __launch_bounds__(kBwdThreads) attn_bwd_dq(BwdArgs a) {
+  using C = BwdCfg<T, DP>;
+  typedef typename frag<T>::type frag_t;
+  constexpr bool kBF = sizeof(T) == 2;
+  __shared__ __align__(16) T Ks[kBT * C::RS];
+  __shared__ __align__(16) T Vs[kBT * C::RS];
+  __shared__ __align__(16) T KTs[DP * C::TS];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, g = lane >> 5;
+  const int64_t nbh = (int64_t)a.B * a.H;
+  const int64_t nqb = (a.Tp + 127) / 128;
+  const int64_t qb = nqb - 1 - (int64_t)blockIdx.x / nbh, bh = blockIdx.x % nbh;   // longest first
+  const int64_t q0 = qb * 128, qw0 = q0 + 32 * w, q = qw0 + lr;
+
+  // this wave's 32 queries: Q and dO rows as B operands (query = lane % 32)
+  frag_t qf[C::QF], df[C::QF];
+  {
+    const bool in = qw0 < a.Tp;
+    const T* qrow = reinterpret_cast<const T*>(a.qh) + (bh * a.Tp + q) * DP;
+    const T* drow = reinterpret_cast<const T*>(a.doh) + (bh * a.Tp + q) * DP;
+    static_for<C::QF>([&](auto s) {
+      if constexpr (kBF) {
+        qf[s] = in ? *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * g) : bf16x8{};
+        df[s] = in ? *reinterpret_cast<const bf16x8*>(drow + 16 * s + 8 * g) : bf16x8{};
+      } else {
+        qf[s] = in ? qrow[2 * s + g] : 0.f;
+        df[s] = in ? drow[2 * s + g] : 0.f;
+      }
+    });
+  }
+  const bool qin = q < a.T;
+  const float lse = qin ? a.lse[bh * a.Tp + q] : INFINITY;
+  const float del = qin ? a.delta[bh * a.Tp + q] : 0.f;
+  const float cl = a.scale_log2;
+  f32x16 dQ[DP / 32];
+  static_for<DP / 32>([&](auto i) { dQ[i] = f32x16{}; });
+
+  int64_t qlast = q0 + 127 < a.T - 1 ? q0 + 127 : a.T - 1;    // the workgroup's last query
+  const int nkt = qlast >= q0 ? (int)(qlast / kBT) + 1 : 0;
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int64_t k0 = (int64_t)kt * kBT;
+    __syncthreads();
+    load_rows<T, DP>(Ks, reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + k0) * DP, tid);
+    load_rows<T, DP>(Vs, reinterpret_cast<const T*>(a.vh) + (bh * a.Tp + k0) * DP, tid);
+    load_cols<T, DP>(KTs, reinterpret_cast<const T*>(a.kh_t) + (bh * a.nch + k0 / kChunk) * DP * kChunk,
+                     (int)(k0 % kChunk), tid);
+    __syncthreads();
+    if (qw0 >= a.T || k0 > qw0 + kBT - 1) continue;     // every key of the tile is after every query
+
+    // S^T = K Q^T and dP^T = V dO^T (keys on the rows, this wave's queries on the lanes)
+    f32x16 S = f32x16{}, dP = f32x16{};
+    static_for<C::QF>([&](auto s) {
+      if constexpr (kBF) {
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[lr * C::RS + 16 * s + 8 * g]);
+        const bf16x8 va = *reinterpret_cast<const bf16x8*>(&Vs[lr * C::RS + 16 * s + 8 * g]);
+        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], S, 0, 0, 0);
+        dP = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, df[s], dP, 0, 0, 0);
+      } else {
+        S = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[lr * C::RS + 2 * s + g], qf[s], S, 0, 0, 0);
+        dP = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[lr * C::RS + 2 * s + g], df[s], dP, 0, 0, 0);
+      }
+    });
+    static_for<16>([&](auto r) {
+      const int64_t kr = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
+      float pm = exp2f(__builtin_fmaf(S[(int)r], cl, -lse));
+      if (kr > q || kr >= a.T) pm = 0.f;
+      dP[(int)r] = pm * (dP[(int)r] - del);
+    });
+    // dQ^T += K^T dS^T (dims on the rows, queries on the lanes)
+    if constexpr (kBF) {
+      bf16x8 sb[2];
+      static_for<2>([&](auto hh) { static_for<8>([&](auto e) { sb[hh][(int)e] = (bf16)dP[8 * hh + e]; }); });
+      static_for<2>([&](auto hh) {
+        static_for<DP / 32>([&](auto db) {
+          const T* kr = &KTs[(32 * db + lr) * C::TS + 16 * hh + 4 * g];
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kr), hi = *reinterpret_cast<const bf16x4*>(kr + 8);
+          const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          dQ[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, sb[hh], dQ[db], 0, 0, 0);
+        });
+      });
+    } else {
+      static_for<16>([&](auto r) {
+        const int kr = 8 * (r >> 2) + 4 * g + (r & 3);
+        static_for<DP / 32>([&](auto db) {
+          dQ[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(KTs[(32 * db + lr) * C::TS + kr], dP[(int)r], dQ[db], 0, 0, 0);
+        });
+      });
+    }
+  }
+  if (qw0 < a.Tp) {
+    float* dst = a.dqh + (bh * a.Tp + q) * DP;
+    static_for<DP / 32>([&](auto db) {
+      static_for<4>([&](auto r4) {
+        f32x4 v;
+        static_for<4>([&](auto i) { v[(int)i] = dQ[db][4 * r4 + i] * a.scale; });
+        *reinterpret_cast<f32x4*>(&dst[32 * db + 8 * r4 + 4 * g]) = v;
+      });
+    });
+  }
+}
+
+// ---------------------------------------------------------------------------
+// link_bwd: suffix scan of the per-token cross products, link gradients,
+// and dq, dk, dv in the reference frame
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void cross_acc(float (&c)[3], const float (&u)[3], const float (&v)[3]) {
+  c[0] += u[1] * v[2] - u[2] * v[1];
+  c[1] += u[2] * v[0] - u[0] * v[2];
+  c[2] += u[0] * v[1] - u[1] * v[0];
+}
+
+// dL/da for a = (a01, a02, a12) of one block from g = vee(W - W^T),
+// W = G^T dL/dG: a is phi = (-a12, a02, -a01) in the standard hat map and
+// dL/dphi = J_r(phi)^T g = g + al phi x g + be phi x (phi x g),
+// al = (1 - cos th)/th^2 = 2 sin^2(th/2)/th^2, be = (th - sin th)/th^3
+// (Taylor series of be below th = 1, where the closed form cancels).
+__device__ inline void link_param_grad(float a0, float a1, float a2, const float (&gv)[3], float (&da)[3]) {
+  const float ph[3] = {-a2, a1, -a0};
+  const float th2 = ph[0] * ph[0] + ph[1] * ph[1] + ph[2] * ph[2];
+  float al, be;
+  if (th2 < 1.f) {
+    al = 0.5f + th2 * (-1.f / 24.f + th2 * (1.f / 720.f - th2 * (1.f / 40320.f)));
+    be = 1.f / 6.f + th2 * (-1.f / 120.f + th2 * (1.f / 5040.f - th2 * (1.f / 362880.f)));
+  } else {
+    const float th = sqrtf(th2);
+    float sh, ch;
+    sincosf(0.5f * th, &sh, &ch);
+    al = 2.f * sh * sh / th2;
+    be = (th - 2.f * sh * ch) / (th2 * th);
+  }
+  float pxg[3] = {ph[1] * gv[2] - ph[2] * gv[1], ph[2] * gv[0] - ph[0] * gv[2], ph[0] * gv[1] - ph[1] * gv[0]};
+  float ppg[3] = {ph[1] * pxg[2] - ph[2] * pxg[1], ph[2] * pxg[0] - ph[0] * pxg[2], ph[0] * pxg[1] - ph[1] * pxg[0]};
+  float dph[3];
+  static_for<3>([&](auto k) { dph[k] = gv[k] + al * pxg[k] + be * ppg[k]; });
+  da[0] = -dph[2];
+  da[1] = dph[1];
+  da[2] = -dph[0];
+}
+
+template <typename IO, typename GT, int DP>
+__global__ void __launch_bounds__(kBwdThreads) link_bwd(BwdArgs a) {
+  constexpr int NBJ = (DP / 3 + 3) / 4;          // blocks per thread (thread p owns blocks p, p+4, ...)
+  constexpr int NV = 3 * NBJ;
+  __shared__ float wtot[4][4][NV];               // [wave][p][3 j + k]: the wave's inclusive suffix at its first token
+  __shared__ float carry[DP];                     // suffix sum of all later chunks, per (block, component)
+  __shared__ unsigned s_ticket;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (tid == 0) s_ticket = __hip_atomic_fetch_add(a.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int64_t nbh = (int64_t)a.B * a.H, tk = s_ticket;
+  if (tk / nbh >= a.nch) return;                  // only if the counter was not reset
+  const int64_t c = a.nch - 1 - tk / nbh, bh = tk % nbh;   // last chunk first
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const int tl = tid >> 2, p = tid & 3;
+  const int64_t t = c * kChunk + tl;
+  const bool in = t < a.T;
+
+  // c_t for this thread's blocks
+  float cv[NBJ][3];
+  const IO* orow = reinterpret_cast<const IO*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs;
+  const IO* drow = reinterpret_cast<const IO*>(a.dout) + (b * a.T + t) * a.do_rs + h * a.do_hs;
+  const int64_t prow = (bh * a.Tp + t) * DP;
+  static_for<NBJ>([&](auto j) {
+    const int blk = p + 4 * j;
+    cv[j][0] = cv[j][1] = cv[j][2] = 0.f;
+    if (in && blk < a.nb) {
+      const rot3 R = qmat(load_quat(a.P + ((bh * a.T + t) * a.nb + blk) * 4));
+      float o3[3], d3[3], oh[3], doh[3], qh[3], kh[3], vh[3], dqh[3], dkh[3], dvh[3];
+      static_for<3>([&](auto k) {
+        const int e = 3 * blk + k;
+        o3[k] = to_f32(orow[e]); d3[k] = to_f32(drow[e]);
+        qh[k] = to_f32(reinterpret_cast<const IO*>(a.qh)[prow + e]);
+        kh[k] = to_f32(reinterpret_cast<const IO*>(a.kh)[prow + e]);
+        vh[k] = to_f32(reinterpret_cast<const IO*>(a.vh)[prow + e]);
+        dqh[k] = a.dqh[prow + e]; dkh[k] = a.dkh[prow + e]; dvh[k] = a.dvh[prow + e];
+      });
+      rot_t_apply(R, o3[0], o3[1], o3[2], oh[0], oh[1], oh[2]);
+      rot_t_apply(R, d3[0], d3[1], d3[2], doh[0], doh[1], doh[2]);
+      cross_acc(cv[j], oh, doh);
+      cross_acc(cv[j], dqh, qh);
+      cross_acc(cv[j], dkh, kh);
+      cross_acc(cv[j], dvh, vh);
+    }
+  });
+  // inclusive suffix over the wave's 16 tokens (lane + 4 is the next token)
+  float sv[NBJ][3];
+  static_for<NBJ>([&](auto j) { static_for<3>([&](auto k) { sv[j][k] = cv[j][k]; }); });
+  static_for<4>([&](auto i) {
+    constexpr int off = 4 << i;
+    static_for<NBJ>([&](auto j) {
+      static_for<3>([&](auto k) {
+        const float u = __shfl_down(sv[j][k], off);
+        if (lane + off < 64) sv[j][k] += u;
+      });
+    });
+  });
+  if (lane < 4) {
+    static_for<NBJ>([&](auto j) { static_for<3>([&](auto k) { wtot[w][p][3 * j + k] = sv[j][k]; }); });
+  }
+  __syncthreads();
+  // chained carry: chunk c publishes (its total) + (the suffix of chunks > c)
+  if (tid < a.nb) {
+    const int blk = tid, bp = blk & 3, bj = blk >> 2;
+    float tot[3];
+    static_for<3>([&](auto k) {
+      tot[k] = ((wtot[0][bp][3 * bj + k] + wtot[1][bp][3 * bj + k]) + wtot[2][bp][3 * bj + k]) + wtot[3][bp][3 * bj + k];
+    });
+    quat nxt = quat{0.f, 0.f, 0.f, 0.f};
+    if (c + 1 < a.nch) {
+      const float* slot = a.carry + ((bh * a.nch + c + 1) * a.nb + blk) * 4;
+      bool ok = false;
+      for (int polls = 0; polls < kMaxPolls; ++polls) {
+        if (get_quat(slot, nxt)) { ok = true; break; }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (!ok) {
+        __hip_atomic_store(a.ticket + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float nan = __uint_as_float(kCanonNan);
+        nxt = quat{nan, nan, nan, nan};
+      }
+    }
+    if (c > 0)
+      put_quat(a.carry + ((bh * a.nch + c) * a.nb + blk) * 4, quat{nxt.w + tot[0], nxt.x + tot[1], nxt.y + tot[2], 0.f});
+    carry[3 * blk] = nxt.w; carry[3 * blk + 1] = nxt.x; carry[3 * blk + 2] = nxt.y;
+  }
+  __syncthreads();
+  if (!in) return;
+
+  // m_{t+1} = (suffix within the chunk, tokens > t) + later waves + later chunks
+  const GT* gqr = reinterpret_cast<const GT*>(a.gq) + (b * a.T + t) * a.gq_rs + h * a.gq_hs;
+  const int64_t tn = t + 1 == a.T ? 0 : t + 1;
+  const GT* gkr = a.gen_mode == 0 ? reinterpret_cast<const GT*>(a.gk) + (b * a.T + tn) * a.gk_rs + h * a.gk_hs : gqr;
+  float* dgqr = a.dgq + (b * a.T + t) * a.dgq_rs + h * a.dgq_hs;
+  float* dgkr = a.gen_mode == 0 ? a.dgk + (b * a.T + tn) * a.dgk_rs + h * a.dgk_hs : nullptr;
+  IO* dqr = reinterpret_cast<IO*>(a.dq) + (b * a.T + t) * a.dq_rs + h * a.dq_hs;
+  IO* dkr = reinterpret_cast<IO*>(a.dk) + (b * a.T + t) * a.dk_rs + h * a.dk_hs;
+  IO* dvr = reinterpret_cast<IO*>(a.dv) + (b * a.T + t) * a.dv_rs + h * a.dv_hs;
+  static_for<NBJ>([&](auto j) {
+    const int blk = p + 4 * j;
+    if (blk < a.nb) {
+      float m[3];
+      static_for<3>([&](auto k) {
+        float later = 0.f;
+        for (int w2 = w + 1; w2 < 4; ++w2) later += wtot[w2][p][3 * j + k];
+        m[k] = (sv[j][k] - cv[j][k]) + later + carry[3 * blk + k];
+      });
+      const rot3 R = qmat(load_quat(a.P + ((bh * a.T + t) * a.nb + blk) * 4));
+      float gv[3];
+      rot_apply(R, m[0], m[1], m[2], gv[0], gv[1], gv[2]);
+      float ap[3];
+      static_for<3>([&](auto k) {
+        ap[k] = to_f32(gqr[3 * blk + k]);
+        if (a.gen_mode == 0) ap[k] += to_f32(gkr[3 * blk + k]);
+        ap[k] *= a.edge_scale;
+      });
+      float da[3];
+      link_param_grad(ap[0], ap[1], ap[2], gv, da);
+      static_for<3>([&](auto k) {
+        dgqr[3 * blk + k] = a.edge_scale * da[k];
+        if (a.gen_mode == 0) dgkr[3 * blk + k] = a.edge_scale * da[k];
+      });
+      // dq = P dqh, dk = P dkh, dv = P dvh
+      float u[3], y[3];
+      static_for<3>([&](auto k) { u[k] = a.dqh[prow + 3 * blk + k]; });
+      rot_apply(R, u[0], u[1], u[2], y[0], y[1], y[2]);
+      static_for<3>([&](auto k) { dqr[3 * blk + k] = from_f32<IO>(y[k]); });
+      static_for<3>([&](auto k) { u[k] = a.dkh[prow + 3 * blk + k]; });
+      rot_apply(R, u[0], u[1], u[2], y[0], y[1], y[2]);
+      static_for<3>([&](auto k) { dkr[3 * blk + k] = from_f32<IO>(y[k]); });
+      static_for<3>([&](auto k) { u[k] = a.dvh[prow + 3 * blk + k]; });
+      rot_apply(R, u[0], u[1], u[2], y[0], y[1], y[2]);
+      static_for<3>([&](auto k) { dvr[3 * blk + k] = from_f32<IO>(y[k]); });
+    }
+  });
+  if (p == 0) {
+    for (int e = 3 * a.nb; e < a.d; ++e) {     // dims outside the rotation blocks
+      dqr[e] = from_f32<IO>(a.dqh[prow + e]);
+      dkr[e] = from_f32<IO>(a.dkh[prow + e]);
+      dvr[e] = from_f32<IO>(a.dvh[prow + e]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <typename IO, typename GT, int DP>
+static hipError_t launch_bwd_dp(const BwdArgs& a, hipStream_t s) {
+  const int64_t nbh = (int64_t)a.B * a.H;
+  const int64_t nblk = (a.Tp + 127) / 128;
+  hipLaunchKernelGGL((bwd_prep<IO, DP>), dim3((unsigned)(nbh * a.nch)), dim3(kBwdThreads), 0, s, a);
+  hipLaunchKernelGGL((attn_bwd_dkdv<IO, DP>), dim3((unsigned)(nbh * nblk)), dim3(kBwdThreads), 0, s, a);
+  hipLaunchKernelGGL((attn_bwd_dq<IO, DP>), dim3((unsigned)(nbh * nblk)), dim3(kBwdThreads), 0, s, a);
+  hipError_t e = launch_chain_reset(a.carry, nbh * a.nch * a.nb * 2, a.ticket, s);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((link_bwd<IO, GT, DP>), dim3((unsigned)(nbh * a.nch)), dim3(kBwdThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename IO, typename GT>
+hipError_t launch_bwd(const BwdArgs& a, hipStream_t s) {
+  switch (a.Dp) {
+    case 32: return launch_bwd_dp<IO, GT, 32>(a, s);
+    case 64: return launch_bwd_dp<IO, GT, 64>(a, s);
+    case 96: return launch_bwd_dp<IO, GT, 96>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template hipError_t launch_bwd<float, float>(const BwdArgs&, hipStream_t);
+template hipError_t launch_bwd<bf16, float>(const BwdArgs&, hipStream_t);
+
+}  // namespace holo

@@ -29,6 +29,35 @@ struct AttnArgs {
   const void* qh; const void* kh; const void* vh_t; const void* P;
   void* o; int64_t o_rs, o_hs;
   int p_format;    // 0: fp32 quaternions, 1: int16 (round(32767 q/|q|))
+  float* lse;      // optional (B, H, Tp): log2 of each query's softmax normaliser, in the
+                   // log2 units of scale_log2 (max + log2(sum)); what the backward recomputes P from
+};
+
+// Backward of scan + attention. Path-frame tensors are (B, H, Tp, Dp) row-major
+// ("_t": 64-row tiles stored transposed, (B, H, Tp/64, Dp, 64)).
+struct BwdArgs {
+  int B, H, d, nb, Dp, gen_mode;
+  int64_t T, Tp, nch;
+  float scale, scale_log2, edge_scale;
+  // saved forward state
+  const void* gq; int64_t gq_rs, gq_hs;
+  const void* gk; int64_t gk_rs, gk_hs;
+  const void* qh; const void* kh; const void* vh_t; const float* P; const float* lse;
+  const void* o; int64_t o_rs, o_hs;
+  // incoming gradient of o
+  const void* dout; int64_t do_rs, do_hs;
+  // workspace
+  void* doh; void* doh_t; void* qh_t; void* kh_t; void* vh;   // io dtype
+  float* delta;                                               // (B, H, Tp): rowsum(do * o)
+  float* dqh; float* dkh; float* dvh;                         // fp32, path frame
+  float* carry;                                               // (B, H, nch, nb, 4) chained suffix sums
+  unsigned* ticket;
+  // outputs
+  void* dq; int64_t dq_rs, dq_hs;
+  void* dk; int64_t dk_rs, dk_hs;
+  void* dv; int64_t dv_rs, dv_hs;
+  float* dgq; int64_t dgq_rs, dgq_hs;
+  float* dgk; int64_t dgk_rs, dgk_hs;
 };
 
 struct DecodeGeomArgs {
@@ -60,5 +89,7 @@ template <typename T> hipError_t launch_decode_attn(const DecodeAttnArgs& a, hip
 int64_t decode_splits(int64_t t);
 template <typename T> hipError_t launch_attn(const AttnArgs& a, hipStream_t s);
 hipError_t launch_quat_to_dense(int64_t n, int d, const float* q, float* out, hipStream_t s);
+hipError_t launch_chain_reset(void* state, int64_t n_pairs, unsigned* ticket, hipStream_t s);
+template <typename IO, typename GT> hipError_t launch_bwd(const BwdArgs& a, hipStream_t s);
 
 }  // namespace holo

@@ -26,6 +26,7 @@
 // composition order, and every bit of the result, does not depend on timing.
 // Threads of a wave cover consecutive blocks of the same token rows, so the
 // token-major input rows are read contiguously.
+#include "holo_chain.h"
 #include "holo_kernels.h"
 
 namespace holo {
@@ -46,36 +47,6 @@ __device__ inline quat link_quat(const ScanArgs& a, int b, int h, int blk, int64
 size_t scan_state_bytes(int B, int64_t T, int H, int d) {
   const int64_t nch = padded_seq(T) / kChunk;
   return (size_t)B * H * nch * (d / 3) * 4 * sizeof(float) + 256;
-}
-
-// ---- chained-scan state ----------------------------------------------------
-// incl[b][h][c][blk] (product of chunks 0..c) are fp32 quaternions whose
-// 32-bit words start as kUnset. Each word is written once per scan and read
-// with agent-scope relaxed atomics, so a word is either unset or final and
-// readers need no fence: a quaternion is complete when none of its words is
-// unset. A computed word equal to kUnset (one NaN bit pattern) is stored as
-// the canonical NaN instead.
-constexpr unsigned kUnset = 0xffffffffu;
-constexpr unsigned kCanonNan = 0x7fc00000u;
-constexpr int kMaxPolls = 1 << 18;   // ~0.3 s of polling
-
-__device__ __forceinline__ void put_quat(float* slot, const quat& q) {
-  unsigned* u = reinterpret_cast<unsigned*>(slot);
-  const float v[4] = {q.w, q.x, q.y, q.z};
-  static_for<4>([&](auto k) {
-    unsigned x = __float_as_uint(v[k]);
-    if (x == kUnset) x = kCanonNan;
-    __hip_atomic_store(u + k, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  });
-}
-
-__device__ __forceinline__ bool get_quat(const float* slot, quat& q) {
-  const unsigned* u = reinterpret_cast<const unsigned*>(slot);
-  unsigned x[4];
-  static_for<4>([&](auto k) { x[k] = __hip_atomic_load(u + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); });
-  if (x[0] == kUnset || x[1] == kUnset || x[2] == kUnset || x[3] == kUnset) return false;
-  q = quat{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3])};
-  return true;
 }
 
 // clears the chained-scan state and the ticket counter before every scan
@@ -385,6 +356,13 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   constexpr int VR = kChunk / E;
   for (int idx = tid; idx < DP * VR; idx += NT)
     vdst[idx] = *reinterpret_cast<const u32x4*>(&vts[(idx / VR) * VS + (idx % VR) * E]);
+}
+
+hipError_t launch_chain_reset(void* state, int64_t n_pairs, unsigned* ticket, hipStream_t s) {
+  const int tpb = 256;
+  hipLaunchKernelGGL(scan_reset, dim3((unsigned)((n_pairs + tpb - 1) / tpb > 0 ? (n_pairs + tpb - 1) / tpb : 1)),
+                     dim3(tpb), 0, s, reinterpret_cast<uint64_t*>(state), n_pairs, ticket);
+  return hipGetLastError();
 }
 
 template <typename IO, typename GT>

@@ -2,6 +2,7 @@
 
 ``geom_scan``  -> holo_geom_scan_fwd : link rotations, prefix products, qh/kh/vh
 ``attention``  -> holo_attn_fwd      : causal attention, back-rotation
+``attention_backward`` -> holo_attn_bwd : gradients of both wrt q, k, v and the generator
 ``quat_to_dense`` -> holo_quat_to_dense
 
 Each wrapper checks devices, dtypes and strides on the host before the launch
@@ -111,10 +112,13 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
 
 
 def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
-              d: int, scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+              d: int, scale: float, out: Optional[torch.Tensor] = None,
+              lse: Optional[torch.Tensor] = None) -> torch.Tensor:
     """qh, kh, vh_t, P from geom_scan for head dimension d.
     Returns o as a (B,T,H,d) tensor (contiguous (B,T,H*d) storage unless
-    `out`, a (B,T,H,d) view, is given)."""
+    `out`, a (B,T,H,d) view, is given). `lse`, a (B, H, Tp) fp32 tensor,
+    receives each query's log2 softmax normaliser (what `attention_backward`
+    needs)."""
     lib = _lib.load()
     if P.dim() != 5:
         raise ValueError("attention: P must be (B, H, T, nb, 4)")
@@ -141,11 +145,68 @@ def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.T
     elif out.dtype != dt or out.device != dev:
         raise ValueError("attention: out must match q's dtype and device")
     o_rs, o_hs = _token_view(out, B, T, H, d, "out")
+    if lse is not None and (tuple(lse.shape) != (B, H, Tp) or lse.dtype != torch.float32
+                            or not lse.is_contiguous() or lse.device != dev):
+        raise ValueError(f"attention: lse must be a contiguous fp32 {(B, H, Tp)} tensor on {dev}")
     rc = lib.holo_attn_fwd(B, T, H, d, _DT[dt], pf, float(scale),
                            _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
-                           _ptr(out), o_rs, o_hs, _stream(dev))
+                           _ptr(out), o_rs, o_hs, _ptr(lse), _stream(dev))
     _lib.check(rc, "holo_attn_fwd")
     return out
+
+
+def attention_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge_scale: float,
+                       qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
+                       lse: torch.Tensor, o: torch.Tensor, dout: torch.Tensor, d: int, scale: float,
+                       dq: torch.Tensor, dk: torch.Tensor, dv: torch.Tensor,
+                       dgq: torch.Tensor, dgk: Optional[torch.Tensor],
+                       workspace: Optional[torch.Tensor] = None) -> None:
+    """Gradients of o = attention(geom_scan(q, k, v, gq, gk)) given dout = dL/do:
+    writes dq, dk, dv ((B,T,H,d) views, dtype of o) and dgq, dgk ((B,T,H,m)
+    fp32 views; gk/dgk None for the direct generator). P must be the fp32
+    quaternions of the same forward, lse the normalisers its attention wrote."""
+    lib = _lib.load()
+    B, H, T = (int(n) for n in P.shape[:3])
+    dev, dt = qh.device, qh.dtype
+    nb = d // 3
+    m = 3 * nb
+    Dp, Tp = padded_head_dim(d), padded_seq_len(T)
+    if P.dtype != torch.float32 or tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous():
+        raise ValueError("attention_backward: P must be the fp32 (B, H, T, nb, 4) quaternions")
+    if tuple(qh.shape) != (B, H, Tp, Dp) or not qh.is_contiguous():
+        raise ValueError("attention_backward: qh does not match the geom_scan layout")
+    if tuple(kh.shape) != (B, H, Tp, Dp) or not kh.is_contiguous() or kh.dtype != dt:
+        raise ValueError("attention_backward: kh does not match the geom_scan layout")
+    if tuple(vh_t.shape) != (B, H, Tp // 64, Dp, 64) or not vh_t.is_contiguous() or vh_t.dtype != dt:
+        raise ValueError("attention_backward: vh_t does not match the geom_scan layout")
+    if tuple(lse.shape) != (B, H, Tp) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("attention_backward: lse must be a contiguous fp32 (B, H, Tp) tensor")
+    for t in (kh, vh_t, P, lse, o, dout, dq, dk, dv, gq, dgq) + tuple(x for x in (gk, dgk) if x is not None):
+        if t.device != dev:
+            raise ValueError("attention_backward: all tensors must be on one device")
+    for name, t in (("o", o), ("dout", dout), ("dq", dq), ("dk", dk), ("dv", dv)):
+        if t.dtype != dt:
+            raise ValueError(f"attention_backward: {name} must be {dt}")
+    for name, t in (("gq", gq), ("gk", gk), ("dgq", dgq), ("dgk", dgk)):
+        if t is not None and t.dtype != torch.float32:
+            raise ValueError(f"attention_backward: {name} must be float32")
+    if (gk is None) != (dgk is None):
+        raise ValueError("attention_backward: gk and dgk go together (additive generator)")
+    views = [_token_view(t, B, T, H, d, n) for n, t in (("o", o), ("dout", dout), ("dq", dq), ("dk", dk), ("dv", dv))]
+    gv = [(0, 0) if t is None else _token_view(t, B, T, H, m, n)
+          for n, t in (("gq", gq), ("gk", gk), ("dgq", dgq), ("dgk", dgk))]
+    need = int(lib.holo_attn_bwd_workspace_size(B, T, H, d, _DT[dt]))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    mode = _lib.HOLO_GEN_ADDITIVE if gk is not None else _lib.HOLO_GEN_DIRECT
+    rc = lib.holo_attn_bwd(B, T, H, d, mode, float(edge_scale), _DT[dt], _lib.HOLO_F32, float(scale),
+                           _ptr(gq), *gv[0], _ptr(gk), *gv[1],
+                           _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(lse),
+                           _ptr(o), *views[0], _ptr(dout), *views[1],
+                           _ptr(dq), *views[2], _ptr(dk), *views[3], _ptr(dv), *views[4],
+                           _ptr(dgq), *gv[2], _ptr(dgk), *gv[3],
+                           _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(dev))
+    _lib.check(rc, "holo_attn_bwd")
 
 
 def quat_to_dense(quat: torch.Tensor, d: int) -> torch.Tensor:

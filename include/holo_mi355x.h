@@ -16,7 +16,11 @@
  *                       out_i = P_i o_i (core/attention_fast_chunked.py:119-171);
  *   holo_quat_to_dense  expands the stored rotations to the reference's dense
  *                       geometry tensors {"C": P, "H": Hol}
- *                       (core/attention_fast_chunked.py:175-177).
+ *                       (core/attention_fast_chunked.py:175-177);
+ *   holo_attn_bwd       replaces HoloAttnFn.backward (kernel/attention_kernel.py:
+ *                       174-187, which recomputes the reference forward under
+ *                       autograd): gradients of the attention output with
+ *                       respect to q, k, v and the link generator outputs.
  *
  * Conventions
  *   - Every pointer is a device pointer owned by the caller; no entry point
@@ -141,13 +145,46 @@ HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
  *                     p_format)
  *   o    : output, element (b, t, h, c) at o[(b*T + t)*o_row_stride + h*o_head_stride + c]
  *          o_i = P_i * sum_{j<=i} softmax_j(scale * qh_i . kh_j) * vh_j
+ *   lse  : optional (null to skip), (B, H, Tp) fp32: per query, log2 of the
+ *          softmax normaliser in units of scale*log2(e) times the score (what
+ *          holo_attn_bwd recomputes the probabilities from)
  * dtype is the dtype of q, kh, vh_t and o (HOLO_BF16: bf16 MFMA with fp32
  * accumulation and softmax; HOLO_F32: fp32 MFMA throughout).
  */
 HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float scale,
                   const void* qh, const void* kh, const void* vh_t, const void* P,
                   void* o, int64_t o_row_stride, int64_t o_head_stride,
-                  void* stream);
+                  float* lse, void* stream);
+
+/* Workspace bytes of holo_attn_bwd. */
+HOLO_API size_t holo_attn_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype);
+
+/*
+ * holo_attn_bwd: given dout = dL/do for the output o of holo_attn_fwd, writes
+ *   dq, dk, dv  (dtype of q: element (b, t, h, c) at ptr[(b*T + t)*row_stride + h*head_stride + c])
+ *   dgq, dgk    (fp32, layout of gq / gk): gradients of the generator outputs;
+ *               additive: a_t = edge_scale (gq_t + gk_{t+1 mod T}); direct: a_t =
+ *               edge_scale g_t (dgk, gk unused).
+ * Saved forward state: gq, gk (fp32) as given to holo_geom_scan_fwd; qh, kh,
+ * vh_t and P (p_format HOLO_QUAT_F32) as it wrote them; o and lse as
+ * holo_attn_fwd wrote them (lse (B, H, Tp) fp32: pass a non-null lse to the
+ * forward). All gradients are accumulated in fp32; the attention products
+ * use the forward's dtype on the matrix cores. Calls sharing a workspace must
+ * not overlap in time.
+ */
+HOLO_API int holo_attn_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale,
+                  int io_dtype, int gen_dtype, float scale,
+                  const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
+                  const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
+                  const void* qh, const void* kh, const void* vh_t, const float* P, const float* lse,
+                  const void* o, int64_t o_row_stride, int64_t o_head_stride,
+                  const void* dout, int64_t dout_row_stride, int64_t dout_head_stride,
+                  void* dq, int64_t dq_row_stride, int64_t dq_head_stride,
+                  void* dk, int64_t dk_row_stride, int64_t dk_head_stride,
+                  void* dv, int64_t dv_row_stride, int64_t dv_head_stride,
+                  float* dgq, int64_t dgq_row_stride, int64_t dgq_head_stride,
+                  float* dgk, int64_t dgk_row_stride, int64_t dgk_head_stride,
+                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Incremental decode (no counterpart in the reference, which only runs whole

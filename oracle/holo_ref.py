@@ -416,3 +416,106 @@ def decoder_forward(tokens: np.ndarray, W: Dict[str, np.ndarray], n_layers: int,
     if return_hidden:
         return h
     return h @ W["lm_head.weight"].T
+
+
+# --------------------------------------------------------------------------
+# backward of the block-structured forward (float64)
+# --------------------------------------------------------------------------
+def _blocks3(u: np.ndarray, nb: int) -> np.ndarray:
+    return u[..., :3 * nb].reshape(*u.shape[:-1], nb, 3)
+
+
+def link_grad_from_cross(a: np.ndarray, P: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """dL/da_t (B,H,T,nb,3) from the per-token cross-product sums c (B,H,T,nb,3).
+
+    With E_t = P_t^T dL/dP_t, the reverse recursion of P_{t+1} = G_t P_t gives
+    M_t = P_t^T Lambda_t = sum_{s>=t} E_s, and G_t^T dL/dG_t = P_t M_{t+1} P_t^T.
+    Only its antisymmetric part reaches a: vee(W - W^T) = P_t m_{t+1} with
+    m = sum_{s>t} c_s, c_s = vee(E_s - E_s^T). The skew vector a = (a01, a02, a12)
+    is phi = (-a12, a02, -a01) in the standard hat map, and
+    dL/dphi = J_r(phi)^T g, J_r^T g = g + al phi x g + be phi x (phi x g),
+    al = (1 - cos th) / th^2, be = (th - sin th) / th^3. The closing edge
+    (t = T-1) only enters the holonomy: its gradient is zero."""
+    suf = np.cumsum(c[..., ::-1, :, :], axis=-3)[..., ::-1, :, :]        # m_t = sum_{s>=t} c_s
+    m_next = np.zeros_like(c)
+    m_next[..., :-1, :, :] = suf[..., 1:, :, :]
+    g = np.einsum("...bij,...bj->...bi", P, m_next)                      # P_t m_{t+1}
+    phi = np.stack([-a[..., 2], a[..., 1], -a[..., 0]], -1)
+    th2 = (phi * phi).sum(-1)
+    th = np.sqrt(th2)
+    small = th < 1e-3
+    ths = np.where(small, 1.0, th)
+    al = np.where(small, 0.5 - th2 / 24.0 + th2 * th2 / 720.0, (1.0 - np.cos(ths)) / (ths * ths))
+    be = np.where(small, 1.0 / 6.0 - th2 / 120.0 + th2 * th2 / 5040.0, (ths - np.sin(ths)) / (ths ** 3))
+    pxg = np.cross(phi, g)
+    dphi = g + al[..., None] * pxg + be[..., None] * np.cross(phi, pxg)
+    da = np.stack([-dphi[..., 2], dphi[..., 1], -dphi[..., 0]], -1)
+    da[..., -1, :, :] = 0.0
+    return da
+
+
+def attention_backward64(qh, kh, vh, oh, doh, scale):
+    """Causal softmax attention backward in float64: (dqh, dkh, dvh)."""
+    T = qh.shape[-2]
+    s = np.einsum("...id,...jd->...ij", qh, kh) * scale
+    mask = np.tril(np.ones((T, T), dtype=bool))
+    s = np.where(mask, s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    dvh = np.einsum("...ij,...id->...jd", p, doh)
+    dp = np.einsum("...id,...jd->...ij", doh, vh)
+    delta = (doh * oh).sum(-1, keepdims=True)
+    ds = p * (dp - delta)
+    dqh = np.einsum("...ij,...jd->...id", ds, kh) * scale
+    dkh = np.einsum("...ij,...id->...jd", ds, qh) * scale
+    return dqh, dkh, dvh
+
+
+def backward_blocks(x: np.ndarray, W: Dict[str, np.ndarray], n_heads: int, edge_scale: float,
+                    dy: np.ndarray, link_mode: str = "additive") -> Dict[str, np.ndarray]:
+    """Gradients of <dy, forward_blocks(x)> in float64: the input x, every
+    weight, and the intermediates the fused backward produces (dq, dk, dv in
+    the reference frame, da the link parameters' gradient)."""
+    x = np.asarray(x, dtype=np.float64)
+    dy = np.asarray(dy, dtype=np.float64)
+    B, T, D = x.shape
+    H = n_heads
+    d = D // H
+    nb = n_blocks(d)
+    _, pt = forward_blocks(x, W, H, edge_scale, link_mode, return_parts=True)
+    P = pt["P"]
+    wout = np.asarray(W["out.weight"], np.float64)
+    o_flat = pt["o"].transpose(0, 2, 1, 3).reshape(B, T, D)
+    do = (dy @ wout).reshape(B, T, H, d).transpose(0, 2, 1, 3)
+    doh = apply_blocks_T(P, do)
+    dqh, dkh, dvh = attention_backward64(pt["qh"], pt["kh"], pt["vh"], pt["oh"], doh, 1.0 / math.sqrt(d))
+    c = (np.cross(_blocks3(pt["oh"], nb), _blocks3(doh, nb)) + np.cross(_blocks3(dqh, nb), _blocks3(pt["qh"], nb))
+         + np.cross(_blocks3(dkh, nb), _blocks3(pt["kh"], nb)) + np.cross(_blocks3(dvh, nb), _blocks3(pt["vh"], nb)))
+    da = link_grad_from_cross(pt["a"].reshape(B, H, T, nb, 3), P, c).reshape(B, H, T, 3 * nb)
+    dq, dk, dv = (apply_blocks(P, g) for g in (dqh, dkh, dvh))
+    dqkv = np.concatenate([dq, dk, dv], -1).transpose(0, 2, 1, 3).reshape(B, T, 3 * D)   # [q_h | k_h | v_h]
+    grads = {"dq": dq, "dk": dk, "dv": dv, "da": da, "dqh": dqh, "dkh": dkh, "dvh": dvh, "doh": doh,
+             "out.weight": dy.reshape(-1, D).T @ o_flat.reshape(-1, D),
+             "qkv.weight": dqkv.reshape(-1, 3 * D).T @ x.reshape(-1, D)}
+    dx = dqkv @ np.asarray(W["qkv.weight"], np.float64)
+    m = 3 * nb
+    dg = edge_scale * da.transpose(0, 2, 1, 3)                    # (B, T, H, m): dL/d(generator output)
+    if link_mode == "additive":
+        dgq = dg.reshape(B, T, H * m)
+        dgk = np.roll(dg, 1, axis=1).reshape(B, T, H * m)        # gk_{t+1} enters edge t
+        for name, g in (("gqproj.weight", dgq), ("gkproj.weight", dgk)):
+            grads[name] = g.reshape(-1, H * m).T @ x.reshape(-1, D)
+            dx = dx + g @ np.asarray(W[name], np.float64)
+    else:
+        xt = torch.as_tensor(x).requires_grad_(True)
+        Wt = {k: torch.as_tensor(np.asarray(v, np.float64)).requires_grad_(True)
+              for k, v in W.items() if k.startswith("edge_mlp")}
+        pair = torch.cat([xt, torch.roll(xt, shifts=-1, dims=1)], dim=-1)
+        h = torch.nn.functional.gelu(_linear(pair, Wt["edge_mlp.0.weight"], Wt["edge_mlp.0.bias"]))
+        g_out = _linear(h, Wt["edge_mlp.2.weight"], Wt["edge_mlp.2.bias"])
+        g_out.backward(torch.as_tensor(dg.reshape(B, T, H * m)))
+        dx = dx + xt.grad.numpy()
+        for k, v in Wt.items():
+            grads[k] = v.grad.numpy()
+    grads["x"] = dx
+    return grads

@@ -85,13 +85,51 @@ def test_scan_argument_validation(lib):
 
 def test_attention_argument_validation(lib):
     f = lib.holo_attn_fwd
-    assert f(1, 0, 1, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_BAD_SHAPE
-    assert f(1, 8, 1, 120, 0, 0, 0.3, 16, 16, 16, 16, 16, 120, 120, None) == _lib.HOLO_ERR_UNSUPPORTED
-    assert f(1, 8, 1, 12, 0, 0, 0.0, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 1, 12, 0, 0, 0.3, None, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 2, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 4, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 1, 12, 5, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 1, 12, 0, 3, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 0, 1, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_BAD_SHAPE
+    assert f(1, 8, 1, 120, 0, 0, 0.3, 16, 16, 16, 16, 16, 120, 120, None, None) == _lib.HOLO_ERR_UNSUPPORTED
+    assert f(1, 8, 1, 12, 0, 0, 0.0, 16, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 0, 0, 0.3, None, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 2, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 4, None, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 5, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 0, 3, 0.3, 16, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_INVALID_ARG
+
+
+    assert f(1, 8, 1, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, 8, None) == _lib.HOLO_ERR_INVALID_ARG   # lse misaligned
+
+
+def _bwd(lib, **kw):
+    a = dict(B=1, T=8, H=2, d=12, gen=0, es=0.1, io=_lib.HOLO_F32, gdt=_lib.HOLO_F32, sc=0.3,
+             gq=16, gk=16, qh=16, kh=16, vh=16, P=16, lse=16, o=16, do=16, dq=16, dk=16, dv=16,
+             dgq=16, dgk=16, ws=16, wsb=1 << 30, rs=64, hs=24, grs=64, ghs=24)
+    a.update(kw)
+    return lib.holo_attn_bwd(a["B"], a["T"], a["H"], a["d"], a["gen"], a["es"], a["io"], a["gdt"], a["sc"],
+                             a["gq"], a["grs"], a["ghs"], a["gk"], a["grs"], a["ghs"],
+                             a["qh"], a["kh"], a["vh"], a["P"], a["lse"],
+                             a["o"], a["rs"], a["hs"], a["do"], a["rs"], a["hs"],
+                             a["dq"], a["rs"], a["hs"], a["dk"], a["rs"], a["hs"], a["dv"], a["rs"], a["hs"],
+                             a["dgq"], a["grs"], a["ghs"], a["dgk"], a["grs"], a["ghs"],
+                             a["ws"], a["wsb"], None)
+
+
+def test_backward_argument_validation(lib):
+    # workspace: five io-dtype path-frame arrays, delta, three fp32 arrays,
+    # the chained suffix sums and the ticket block, each rounded to 256 bytes
+    n = 2 * 3 * 2048 * 96
+    r = lambda x: (x + 255) // 256 * 256
+    assert lib.holo_attn_bwd_workspace_size(2, 2048, 3, 96, _lib.HOLO_BF16) == \
+        5 * r(2 * n) + r(2 * 3 * 2048 * 4) + 3 * r(4 * n) + r(2 * 3 * 32 * 32 * 16) + 256
+    assert lib.holo_attn_bwd_workspace_size(2, 2048, 3, 96, 9) == 0
+    assert _bwd(lib, B=0) == _lib.HOLO_ERR_BAD_SHAPE
+    assert _bwd(lib, d=200) == _lib.HOLO_ERR_UNSUPPORTED
+    assert _bwd(lib, gdt=_lib.HOLO_BF16) == _lib.HOLO_ERR_UNSUPPORTED     # the backward takes an fp32 generator
+    assert _bwd(lib, gen=5) == _lib.HOLO_ERR_INVALID_ARG
+    assert _bwd(lib, lse=None) == _lib.HOLO_ERR_INVALID_ARG
+    assert _bwd(lib, gk=None) == _lib.HOLO_ERR_INVALID_ARG               # additive needs gk / dgk
+    assert _bwd(lib, hs=4) == _lib.HOLO_ERR_INVALID_ARG                  # heads overlap
+    assert _bwd(lib, P=8) == _lib.HOLO_ERR_INVALID_ARG                   # misaligned
+    assert _bwd(lib, sc=0.0) == _lib.HOLO_ERR_INVALID_ARG
+    assert _bwd(lib, wsb=1024) == _lib.HOLO_ERR_WORKSPACE
+    assert _bwd(lib, ws=None) == _lib.HOLO_ERR_WORKSPACE
 
 
 def test_status_codes_map_to_reference_exceptions(lib):
