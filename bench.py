@@ -250,6 +250,86 @@ def decode_bench(args, torch, F, synth, kernels, Module):
             "prefill_s": round(prefill_s, 3), "cpu_baseline": None}
 
 
+def train_bench(args, torch, F, synth, kernels, Module):
+    """Forward + backward of one layer at a BASELINE config (default config 2)
+    through the module's autograd path, and the fused backward (holo_attn_bwd)
+    timed alone on the saved forward state. The backward attention's
+    algorithmic work is 2.5x the forward's (recomputed QK^T, dP, dV, dK, dQ)."""
+    cfg = CONFIGS[args.config]
+    B, T, D, H, es = cfg["B"], cfg["T"], cfg["D"], cfg["H"], cfg["es"]
+    d = D // H
+    dt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+    dev = torch.device("cuda:0")
+    inp = synth.layer_inputs(2, B, T, D, H, "additive")
+    x = torch.as_tensor(inp.pop("x")).to(dev, dt)
+    m = Module(D, n_heads=H, edge_scale=es)
+    m.link_mode = "additive"
+    with torch.no_grad():
+        for k, p in m.state_dict().items():
+            if k in inp:
+                p.copy_(torch.as_tensor(inp[k]))
+    m = m.to(device=dev, dtype=dt).train()
+    mask = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
+    g = torch.Generator(device=dev).manual_seed(3)
+    dy = torch.randn(B, T, D, device=dev, generator=g).to(dt)
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        y, _ = m(x, attn_mask=mask)
+        y.backward(dy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # the fused backward alone, on the state of one forward
+    with torch.no_grad():
+        q, k, v, gq, gk = m._link_inputs(x)
+        qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, es, p_format="f32")
+        lse = torch.empty((B, H, qh.shape[2]), dtype=torch.float32, device=dev)
+        o = kernels.attention(qh, kh, vh_t, P, d, m.scale, lse=lse)
+        do = torch.randn(B, T, H, d, device=dev, generator=g).to(dt)
+        dqkv = torch.empty(B, T, H, 3 * d, dtype=dt, device=dev)
+        dgq, dgk = torch.empty_like(gq), torch.empty_like(gk)
+        ws = torch.empty(int(kernels._lib.load().holo_attn_bwd_workspace_size(B, T, H, d, kernels._DT[dt])),
+                         dtype=torch.uint8, device=dev)
+        run = lambda: kernels.attention_backward(gq, gk, es, qh, kh, vh_t, P, lse, o, do, d, m.scale,
+                                                 dqkv[..., :d], dqkv[..., d:2 * d], dqkv[..., 2 * d:],
+                                                 dgq, dgk, workspace=ws)
+        for _ in range(3):
+            run()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        bwd_ms = e0.elapsed_time(e1) / args.steps
+    fl_bwd = 2.5 * attention_core_flops(B, T, H, d)
+    peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
+    ach = fl_bwd / (bwd_ms * 1e-3) / 1e12
+    ms = wall * 1e3 / args.steps
+    return {"metric": f"training step tokens/s (forward + backward of one layer, {args.config})",
+            "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": cfg["dtype"],
+            "data": "synthetic (seeded SplitMix64/Box-Muller: x ~ N(0,1), weights ~ N(0,1/d_model); dy from "
+                    "torch.randn seeded 3)",
+            "config": {"workload": f"{args.config}: one layer forward + backward (all weight and input "
+                                   f"gradients)", "global_batch": B, "seq_len": T, "n_heads": H, "d_head": d,
+                       "d_model": D, "link_mode": "additive", "edge_scale": es, "parallelism": "single GPU"},
+            "fused_backward_ms": bwd_ms,
+            "roofline": {"kernel": "holo_attn_bwd (bwd_prep + attn_bwd_dkdv + attn_bwd_dq + link_bwd)",
+                         "bound": "mfma", "achieved": ach, "peak": peak, "unit": "TFLOP/s", "frac": ach / peak,
+                         "traffic": None,
+                         "work_per_launch": f"{fl_bwd:.4e} FLOP = 2.5 * 2*d*T*(T+1)*B*H"},
+            "cpu_baseline": None}
+
+
 DECODER_CFG = dict(V=32000, D=1536, H=16, NL=12, B=8, T=4096, es=0.05)     # config 4
 
 
@@ -379,6 +459,8 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="config 5: incremental decode after a prefill (one JSON line) and exit")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--train", action="store_true",
+                    help="forward + backward of one layer at --config (one JSON line) and exit")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSVs under DIR(s) as JSON and exit")
     args = ap.parse_args()
@@ -403,6 +485,9 @@ def main():
         return
     if args.config == "cfg4":
         print(json.dumps(decoder_bench(args, torch, F, kernels)))
+        return
+    if args.train:
+        print(json.dumps(train_bench(args, torch, F, synth, kernels, PathOrderedGeometricMHA)))
         return
     cfg = CONFIGS[args.config]
     B, T, D, H, es = cfg["B"], cfg["T"], cfg["D"], cfg["H"], cfg["es"]

@@ -177,7 +177,7 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_prep(BwdArgs a) {
 // over the accumulator rows of an earlier product uses that same order for
 // both operands, so the accumulator is the operand with no data movement.
 template <typename T, int DP>
-__global__ void __launch_bounds__(kBwdThreads) attn_bwd_dkdv(BwdArgs a) {
+__global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(2))) attn_bwd_dkdv(BwdArgs a) {
   using C = BwdCfg<T, DP>;
   typedef typename frag<T>::type frag_t;
   constexpr bool kBF = sizeof(T) == 2;
@@ -295,7 +295,7 @@ __global__ void __launch_bounds__(kBwdThreads) attn_bwd_dkdv(BwdArgs a) {
 // attention backward: dQ
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ void __launch_bounds__(kBwdThreads) attn_bwd_dq(BwdArgs a) {
+__global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(2))) attn_bwd_dq(BwdArgs a) {
   using C = BwdCfg<T, DP>;
   typedef typename frag<T>::type frag_t;
   constexpr bool kBF = sizeof(T) == 2;
@@ -400,12 +400,6 @@ __global__ void __launch_bounds__(kBwdThreads) attn_bwd_dq(BwdArgs a) {
 // link_bwd: suffix scan of the per-token cross products, link gradients,
 // and dq, dk, dv in the reference frame
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void cross_acc(float (&c)[3], const float (&u)[3], const float (&v)[3]) {
-  c[0] += u[1] * v[2] - u[2] * v[1];
-  c[1] += u[2] * v[0] - u[0] * v[2];
-  c[2] += u[0] * v[1] - u[1] * v[0];
-}
-
 // dL/da for a = (a01, a02, a12) of one block from g = vee(W - W^T),
 // W = G^T dL/dG: a is phi = (-a12, a02, -a01) in the standard hat map and
 // dL/dphi = J_r(phi)^T g = g + al phi x g + be phi x (phi x g),
@@ -434,11 +428,45 @@ __device__ inline void link_param_grad(float a0, float a1, float a2, const float
   da[2] = -dph[0];
 }
 
-template <typename IO, typename GT, int DP>
+// N contiguous elements of one row as fp32: 16-byte vector accesses on the
+// wide path (rows and spans 16-byte aligned), element accesses otherwise;
+// `n` (<= N) elements are valid.
+template <typename T, int N, bool WIDE>
+__device__ __forceinline__ void load_span(const T* p, int n, float (&v)[N]) {
+  constexpr int E = 16 / sizeof(T);
+  if constexpr (WIDE && N % E == 0) {
+    static_for<N / E>([&](auto c) {
+      const u32x4 raw = reinterpret_cast<const u32x4*>(p)[c];
+      const T* e = reinterpret_cast<const T*>(&raw);
+      static_for<E>([&](auto i) { v[c * E + i] = to_f32(e[i]); });
+    });
+  } else {
+    static_for<N>([&](auto i) { v[i] = i < n ? to_f32(p[i]) : 0.f; });
+  }
+}
+
+template <typename T, int N, bool WIDE>
+__device__ __forceinline__ void store_span(T* p, int n, const float (&v)[N]) {
+  constexpr int E = 16 / sizeof(T);
+  if constexpr (WIDE && N % E == 0) {
+    static_for<N / E>([&](auto c) {
+      u32x4 raw;
+      T* e = reinterpret_cast<T*>(&raw);
+      static_for<E>([&](auto i) { e[i] = from_f32<T>(v[c * E + i]); });
+      reinterpret_cast<u32x4*>(p)[c] = raw;
+    });
+  } else {
+    static_for<N>([&](auto i) { if (i < n) p[i] = from_f32<T>(v[i]); });
+  }
+}
+
+// Thread (token tl = tid / 4, part p = tid % 4) owns blocks p*NBJ .. p*NBJ+NBJ-1
+// of its token: 3*NBJ contiguous dims of every row it reads or writes.
+template <typename IO, typename GT, int DP, bool WIDE>
 __global__ void __launch_bounds__(kBwdThreads) link_bwd(BwdArgs a) {
-  constexpr int NBJ = (DP / 3 + 3) / 4;          // blocks per thread (thread p owns blocks p, p+4, ...)
-  constexpr int NV = 3 * NBJ;
-  __shared__ float wtot[4][4][NV];               // [wave][p][3 j + k]: the wave's inclusive suffix at its first token
+  constexpr int NBJ = (DP / 3 + 3) / 4;          // blocks per thread
+  constexpr int NV = 3 * NBJ;                    // dims per thread
+  __shared__ float wtot[4][4][NV];               // [wave][p][dim]: the wave's inclusive suffix at its first token
   __shared__ float carry[DP];                     // suffix sum of all later chunks, per (block, component)
   __shared__ unsigned s_ticket;
 
@@ -452,53 +480,58 @@ __global__ void __launch_bounds__(kBwdThreads) link_bwd(BwdArgs a) {
   const int tl = tid >> 2, p = tid & 3;
   const int64_t t = c * kChunk + tl;
   const bool in = t < a.T;
+  const int blk0 = p * NBJ;
+  const int nblk = a.nb - blk0 < 0 ? 0 : (a.nb - blk0 < NBJ ? a.nb - blk0 : NBJ);   // valid blocks
+  const int nd = 3 * nblk, e0 = 3 * blk0;
 
-  // c_t for this thread's blocks
-  float cv[NBJ][3];
-  const IO* orow = reinterpret_cast<const IO*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs;
-  const IO* drow = reinterpret_cast<const IO*>(a.dout) + (b * a.T + t) * a.do_rs + h * a.do_hs;
-  const int64_t prow = (bh * a.Tp + t) * DP;
-  static_for<NBJ>([&](auto j) {
-    const int blk = p + 4 * j;
-    cv[j][0] = cv[j][1] = cv[j][2] = 0.f;
-    if (in && blk < a.nb) {
-      const rot3 R = qmat(load_quat(a.P + ((bh * a.T + t) * a.nb + blk) * 4));
-      float o3[3], d3[3], oh[3], doh[3], qh[3], kh[3], vh[3], dqh[3], dkh[3], dvh[3];
-      static_for<3>([&](auto k) {
-        const int e = 3 * blk + k;
-        o3[k] = to_f32(orow[e]); d3[k] = to_f32(drow[e]);
-        qh[k] = to_f32(reinterpret_cast<const IO*>(a.qh)[prow + e]);
-        kh[k] = to_f32(reinterpret_cast<const IO*>(a.kh)[prow + e]);
-        vh[k] = to_f32(reinterpret_cast<const IO*>(a.vh)[prow + e]);
-        dqh[k] = a.dqh[prow + e]; dkh[k] = a.dkh[prow + e]; dvh[k] = a.dvh[prow + e];
-      });
-      rot_t_apply(R, o3[0], o3[1], o3[2], oh[0], oh[1], oh[2]);
-      rot_t_apply(R, d3[0], d3[1], d3[2], doh[0], doh[1], doh[2]);
-      cross_acc(cv[j], oh, doh);
-      cross_acc(cv[j], dqh, qh);
-      cross_acc(cv[j], dkh, kh);
-      cross_acc(cv[j], dvh, vh);
-    }
-  });
-  // inclusive suffix over the wave's 16 tokens (lane + 4 is the next token)
-  float sv[NBJ][3];
-  static_for<NBJ>([&](auto j) { static_for<3>([&](auto k) { sv[j][k] = cv[j][k]; }); });
-  static_for<4>([&](auto i) {
-    constexpr int off = 4 << i;
+  quat qP[NBJ];
+  float cv[NV];
+  static_for<NV>([&](auto i) { cv[i] = 0.f; });
+  const int64_t prow = (bh * a.Tp + t) * DP + e0;
+  if (in) {
+    const float* pq = a.P + ((bh * a.T + t) * a.nb + blk0) * 4;
+    static_for<NBJ>([&](auto j) { qP[j] = j < nblk ? load_quat(pq + 4 * j) : qident(); });
+    // c_t = oh x doh + dqh x qh + dkh x kh + dvh x vh per block
+    float u[NV], v[NV];
+    load_span<IO, NV, WIDE>(reinterpret_cast<const IO*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs + e0, nd, u);
+    load_span<IO, NV, WIDE>(reinterpret_cast<const IO*>(a.dout) + (b * a.T + t) * a.do_rs + h * a.do_hs + e0, nd, v);
     static_for<NBJ>([&](auto j) {
-      static_for<3>([&](auto k) {
-        const float u = __shfl_down(sv[j][k], off);
-        if (lane + off < 64) sv[j][k] += u;
+      const rot3 R = qmat(qP[j]);
+      float oh[3], dh[3];
+      rot_t_apply(R, u[3 * j], u[3 * j + 1], u[3 * j + 2], oh[0], oh[1], oh[2]);
+      rot_t_apply(R, v[3 * j], v[3 * j + 1], v[3 * j + 2], dh[0], dh[1], dh[2]);
+      cv[3 * j] += oh[1] * dh[2] - oh[2] * dh[1];
+      cv[3 * j + 1] += oh[2] * dh[0] - oh[0] * dh[2];
+      cv[3 * j + 2] += oh[0] * dh[1] - oh[1] * dh[0];
+    });
+    auto acc = [&](const void* gsrc, const float* src) {     // cv += grad x value
+      load_span<IO, NV, WIDE>(reinterpret_cast<const IO*>(gsrc) + prow, nd, v);
+      load_span<float, NV, WIDE>(src + prow, nd, u);
+      static_for<NBJ>([&](auto j) {
+        cv[3 * j] += u[3 * j + 1] * v[3 * j + 2] - u[3 * j + 2] * v[3 * j + 1];
+        cv[3 * j + 1] += u[3 * j + 2] * v[3 * j] - u[3 * j] * v[3 * j + 2];
+        cv[3 * j + 2] += u[3 * j] * v[3 * j + 1] - u[3 * j + 1] * v[3 * j];
       });
+    };
+    acc(a.qh, a.dqh);
+    acc(a.kh, a.dkh);
+    acc(a.vh, a.dvh);
+  }
+  // inclusive suffix over the wave's 16 tokens (lane + 4 is the next token)
+  float sv[NV];
+  static_for<NV>([&](auto i) { sv[i] = cv[i]; });
+  static_for<4>([&](auto s) {
+    constexpr int off = 4 << s;
+    static_for<NV>([&](auto i) {
+      const float x = __shfl_down(sv[i], off);
+      if (lane + off < 64) sv[i] += x;
     });
   });
-  if (lane < 4) {
-    static_for<NBJ>([&](auto j) { static_for<3>([&](auto k) { wtot[w][p][3 * j + k] = sv[j][k]; }); });
-  }
+  if (lane < 4) static_for<NV>([&](auto i) { wtot[w][p][i] = sv[i]; });
   __syncthreads();
   // chained carry: chunk c publishes (its total) + (the suffix of chunks > c)
   if (tid < a.nb) {
-    const int blk = tid, bp = blk & 3, bj = blk >> 2;
+    const int blk = tid, bp = blk / NBJ, bj = blk % NBJ;
     float tot[3];
     static_for<3>([&](auto k) {
       tot[k] = ((wtot[0][bp][3 * bj + k] + wtot[1][bp][3 * bj + k]) + wtot[2][bp][3 * bj + k]) + wtot[3][bp][3 * bj + k];
@@ -524,57 +557,48 @@ __global__ void __launch_bounds__(kBwdThreads) link_bwd(BwdArgs a) {
   __syncthreads();
   if (!in) return;
 
-  // m_{t+1} = (suffix within the chunk, tokens > t) + later waves + later chunks
-  const GT* gqr = reinterpret_cast<const GT*>(a.gq) + (b * a.T + t) * a.gq_rs + h * a.gq_hs;
+  // m_{t+1} = (suffix within the chunk, tokens > t) + later waves + later chunks;
+  // dL/da_t from P_t m_{t+1} (the closing edge's m is zero: no later tokens)
   const int64_t tn = t + 1 == a.T ? 0 : t + 1;
-  const GT* gkr = a.gen_mode == 0 ? reinterpret_cast<const GT*>(a.gk) + (b * a.T + tn) * a.gk_rs + h * a.gk_hs : gqr;
-  float* dgqr = a.dgq + (b * a.T + t) * a.dgq_rs + h * a.dgq_hs;
-  float* dgkr = a.gen_mode == 0 ? a.dgk + (b * a.T + tn) * a.dgk_rs + h * a.dgk_hs : nullptr;
-  IO* dqr = reinterpret_cast<IO*>(a.dq) + (b * a.T + t) * a.dq_rs + h * a.dq_hs;
-  IO* dkr = reinterpret_cast<IO*>(a.dk) + (b * a.T + t) * a.dk_rs + h * a.dk_hs;
-  IO* dvr = reinterpret_cast<IO*>(a.dv) + (b * a.T + t) * a.dv_rs + h * a.dv_hs;
+  float ga[NV], da[NV];
+  load_span<GT, NV, WIDE>(reinterpret_cast<const GT*>(a.gq) + (b * a.T + t) * a.gq_rs + h * a.gq_hs + e0, nd, ga);
+  if (a.gen_mode == 0) {
+    float gk[NV];
+    load_span<GT, NV, WIDE>(reinterpret_cast<const GT*>(a.gk) + (b * a.T + tn) * a.gk_rs + h * a.gk_hs + e0, nd, gk);
+    static_for<NV>([&](auto i) { ga[i] += gk[i]; });
+  }
   static_for<NBJ>([&](auto j) {
-    const int blk = p + 4 * j;
-    if (blk < a.nb) {
-      float m[3];
-      static_for<3>([&](auto k) {
-        float later = 0.f;
-        for (int w2 = w + 1; w2 < 4; ++w2) later += wtot[w2][p][3 * j + k];
-        m[k] = (sv[j][k] - cv[j][k]) + later + carry[3 * blk + k];
-      });
-      const rot3 R = qmat(load_quat(a.P + ((bh * a.T + t) * a.nb + blk) * 4));
-      float gv[3];
-      rot_apply(R, m[0], m[1], m[2], gv[0], gv[1], gv[2]);
-      float ap[3];
-      static_for<3>([&](auto k) {
-        ap[k] = to_f32(gqr[3 * blk + k]);
-        if (a.gen_mode == 0) ap[k] += to_f32(gkr[3 * blk + k]);
-        ap[k] *= a.edge_scale;
-      });
-      float da[3];
-      link_param_grad(ap[0], ap[1], ap[2], gv, da);
-      static_for<3>([&](auto k) {
-        dgqr[3 * blk + k] = a.edge_scale * da[k];
-        if (a.gen_mode == 0) dgkr[3 * blk + k] = a.edge_scale * da[k];
-      });
-      // dq = P dqh, dk = P dkh, dv = P dvh
-      float u[3], y[3];
-      static_for<3>([&](auto k) { u[k] = a.dqh[prow + 3 * blk + k]; });
-      rot_apply(R, u[0], u[1], u[2], y[0], y[1], y[2]);
-      static_for<3>([&](auto k) { dqr[3 * blk + k] = from_f32<IO>(y[k]); });
-      static_for<3>([&](auto k) { u[k] = a.dkh[prow + 3 * blk + k]; });
-      rot_apply(R, u[0], u[1], u[2], y[0], y[1], y[2]);
-      static_for<3>([&](auto k) { dkr[3 * blk + k] = from_f32<IO>(y[k]); });
-      static_for<3>([&](auto k) { u[k] = a.dvh[prow + 3 * blk + k]; });
-      rot_apply(R, u[0], u[1], u[2], y[0], y[1], y[2]);
-      static_for<3>([&](auto k) { dvr[3 * blk + k] = from_f32<IO>(y[k]); });
-    }
+    float m[3];
+    static_for<3>([&](auto k) {
+      float later = 0.f;
+      for (int w2 = w + 1; w2 < 4; ++w2) later += wtot[w2][p][3 * j + k];
+      m[k] = (sv[3 * j + k] - cv[3 * j + k]) + later + (j < nblk ? carry[e0 + 3 * j + k] : 0.f);
+    });
+    float gv[3], d3[3];
+    rot_apply(qmat(qP[j]), m[0], m[1], m[2], gv[0], gv[1], gv[2]);
+    link_param_grad(a.edge_scale * ga[3 * j], a.edge_scale * ga[3 * j + 1], a.edge_scale * ga[3 * j + 2], gv, d3);
+    static_for<3>([&](auto k) { da[3 * j + k] = a.edge_scale * d3[k]; });
   });
+  store_span<float, NV, WIDE>(a.dgq + (b * a.T + t) * a.dgq_rs + h * a.dgq_hs + e0, nd, da);
+  if (a.gen_mode == 0) store_span<float, NV, WIDE>(a.dgk + (b * a.T + tn) * a.dgk_rs + h * a.dgk_hs + e0, nd, da);
+  // dq = P dqh, dk = P dkh, dv = P dvh
+  auto rotate_out = [&](const float* src, void* dst, int64_t rs, int64_t hs) {
+    float u[NV], y[NV];
+    load_span<float, NV, WIDE>(src + prow, nd, u);
+    static_for<NBJ>([&](auto j) {
+      rot_apply(qmat(qP[j]), u[3 * j], u[3 * j + 1], u[3 * j + 2], y[3 * j], y[3 * j + 1], y[3 * j + 2]);
+    });
+    store_span<IO, NV, WIDE>(reinterpret_cast<IO*>(dst) + (b * a.T + t) * rs + h * hs + e0, nd, y);
+  };
+  rotate_out(a.dqh, a.dq, a.dq_rs, a.dq_hs);
+  rotate_out(a.dkh, a.dk, a.dk_rs, a.dk_hs);
+  rotate_out(a.dvh, a.dv, a.dv_rs, a.dv_hs);
   if (p == 0) {
+    const int64_t prow0 = (bh * a.Tp + t) * DP;
     for (int e = 3 * a.nb; e < a.d; ++e) {     // dims outside the rotation blocks
-      dqr[e] = from_f32<IO>(a.dqh[prow + e]);
-      dkr[e] = from_f32<IO>(a.dkh[prow + e]);
-      dvr[e] = from_f32<IO>(a.dvh[prow + e]);
+      reinterpret_cast<IO*>(a.dq)[(b * a.T + t) * a.dq_rs + h * a.dq_hs + e] = from_f32<IO>(a.dqh[prow0 + e]);
+      reinterpret_cast<IO*>(a.dk)[(b * a.T + t) * a.dk_rs + h * a.dk_hs + e] = from_f32<IO>(a.dkh[prow0 + e]);
+      reinterpret_cast<IO*>(a.dv)[(b * a.T + t) * a.dv_rs + h * a.dv_hs + e] = from_f32<IO>(a.dvh[prow0 + e]);
     }
   }
 }
@@ -589,7 +613,21 @@ static hipError_t launch_bwd_dp(const BwdArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((attn_bwd_dq<IO, DP>), dim3((unsigned)(nbh * nblk)), dim3(kBwdThreads), 0, s, a);
   hipError_t e = launch_chain_reset(a.carry, nbh * a.nch * a.nb * 2, a.ticket, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((link_bwd<IO, GT, DP>), dim3((unsigned)(nbh * a.nch)), dim3(kBwdThreads), 0, s, a);
+  // 16-byte spans: 8 blocks (24 dims) per thread at d = 96, every row and
+  // head stride of the token-major tensors a multiple of 16 bytes
+  auto al = [](const void* ptr, int64_t rs, int64_t hs, size_t es) {
+    return ptr == nullptr || ((reinterpret_cast<uintptr_t>(ptr) & 15) == 0 && (rs * (int64_t)es) % 16 == 0 &&
+                              (hs * (int64_t)es) % 16 == 0);
+  };
+  const bool wide = DP == 96 && a.d == 96 && al(a.o, a.o_rs, a.o_hs, sizeof(IO)) &&
+                    al(a.dout, a.do_rs, a.do_hs, sizeof(IO)) && al(a.dq, a.dq_rs, a.dq_hs, sizeof(IO)) &&
+                    al(a.dk, a.dk_rs, a.dk_hs, sizeof(IO)) && al(a.dv, a.dv_rs, a.dv_hs, sizeof(IO)) &&
+                    al(a.gq, a.gq_rs, a.gq_hs, sizeof(GT)) && al(a.gk, a.gk_rs, a.gk_hs, sizeof(GT)) &&
+                    al(a.dgq, a.dgq_rs, a.dgq_hs, 4) && al(a.dgk, a.dgk_rs, a.dgk_hs, 4);
+  if (wide)
+    hipLaunchKernelGGL((link_bwd<IO, GT, DP, true>), dim3((unsigned)(nbh * a.nch)), dim3(kBwdThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((link_bwd<IO, GT, DP, false>), dim3((unsigned)(nbh * a.nch)), dim3(kBwdThreads), 0, s, a);
   return hipGetLastError();
 }
 
