@@ -51,29 +51,50 @@ template <typename T> struct frag;
 template <> struct frag<bf16> { typedef bf16x8 type; };
 template <> struct frag<float> { typedef float type; };
 
-// 32 rows r0.. of a (rows, DP) row-major array into LDS (stride RS)
-template <typename T, int DP>
-__device__ __forceinline__ void load_rows(T* dst, const T* src, int tid) {
+// Cooperative copies of one 32-row / 32-column tile into LDS. All of a
+// thread's global loads are issued before its LDS stores (one memory round
+// trip per tile, not one per chunk).
+template <typename T, int DP> struct TileCopy {
   using C = BwdCfg<T, DP>;
-  constexpr int CPR = DP / C::E;
-  for (int i = tid; i < kBT * CPR; i += kBwdThreads) {
-    const int r = i / CPR, cc = i % CPR;
-    *reinterpret_cast<u32x4*>(&dst[r * C::RS + cc * C::E]) =
-        *reinterpret_cast<const u32x4*>(&src[(int64_t)r * DP + cc * C::E]);
-  }
-}
-
-// columns j0 .. j0+31 of a transposed (DP, 64) tile into LDS (stride TS)
-template <typename T, int DP>
-__device__ __forceinline__ void load_cols(T* dst, const T* tile, int j0, int tid) {
-  using C = BwdCfg<T, DP>;
-  constexpr int CPR = kBT / C::E;
-  for (int i = tid; i < DP * CPR; i += kBwdThreads) {
-    const int r = i / CPR, cc = i % CPR;
-    *reinterpret_cast<u32x4*>(&dst[r * C::TS + cc * C::E]) =
-        *reinterpret_cast<const u32x4*>(&tile[(int64_t)r * kChunk + j0 + cc * C::E]);
-  }
-}
+  static constexpr int RCPR = DP / C::E, TCPR = kBT / C::E;    // 16-byte chunks per row
+  static constexpr int RN = kBT * RCPR, TN = DP * TCPR;         // chunks per tile
+  // NA tiles at once, flattened over the threads: tile k's chunk i is flat
+  // index k*RN + i (row-major tiles first, then transposed ones)
+  template <int NR, int NT>
+  struct Multi {
+    static constexpr int N = NR * RN + NT * TN;
+    static constexpr int IT = (N + kBwdThreads - 1) / kBwdThreads;
+    static __device__ __forceinline__ void load(u32x4 (&r)[IT], const T* const (&rows)[NR], const T* const (&cols)[NT],
+                                                int j0, int tid) {
+      static_for<IT>([&](auto it) {
+        const int f = tid + kBwdThreads * it;
+        if (f < NR * RN) {
+          const int k = f / RN, i = f % RN;
+          r[it] = *reinterpret_cast<const u32x4*>(&rows[k][(int64_t)(i / RCPR) * DP + (i % RCPR) * C::E]);
+        } else if (f < N) {
+          const int k = (f - NR * RN) / TN, i = (f - NR * RN) % TN;
+          r[it] = *reinterpret_cast<const u32x4*>(&cols[k][(int64_t)(i / TCPR) * kChunk + j0 + (i % TCPR) * C::E]);
+        }
+      });
+    }
+    // LDS destination: the NR row-major tiles (kBT * RS elements each), then
+    // the NT transposed tiles (DP * TS each), back to back from `lds`
+    static constexpr int kRowTile = kBT * C::RS, kColTile = DP * C::TS;
+    static constexpr int kElems = NR * kRowTile + NT * kColTile;
+    static __device__ __forceinline__ void store(T* lds, const u32x4 (&r)[IT], int tid) {
+      static_for<IT>([&](auto it) {
+        const int f = tid + kBwdThreads * it;
+        if (f < NR * RN) {
+          const int k = f / RN, i = f % RN;
+          *reinterpret_cast<u32x4*>(&lds[k * kRowTile + (i / RCPR) * C::RS + (i % RCPR) * C::E]) = r[it];
+        } else if (f < N) {
+          const int k = (f - NR * RN) / TN, i = (f - NR * RN) % TN;
+          *reinterpret_cast<u32x4*>(&lds[NR * kRowTile + k * kColTile + (i / TCPR) * C::TS + (i % TCPR) * C::E]) = r[it];
+        }
+      });
+    }
+  };
+};
 
 // ---------------------------------------------------------------------------
 // bwd_prep
@@ -177,15 +198,17 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_prep(BwdArgs a) {
 // over the accumulator rows of an earlier product uses that same order for
 // both operands, so the accumulator is the operand with no data movement.
 template <typename T, int DP>
-__global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(2))) attn_bwd_dkdv(BwdArgs a) {
+__global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1))) attn_bwd_dkdv(BwdArgs a) {
   using C = BwdCfg<T, DP>;
   typedef typename frag<T>::type frag_t;
   constexpr bool kBF = sizeof(T) == 2;
-  __shared__ __align__(16) T Qs[kBT * C::RS];
-  __shared__ __align__(16) T dOs[kBT * C::RS];
-  __shared__ __align__(16) T QTs[DP * C::TS];
-  __shared__ __align__(16) T dOTs[DP * C::TS];
+  using M = typename TileCopy<T, DP>::template Multi<2, 2>;
+  __shared__ __align__(16) T tiles[M::kElems];   // Q, dO (row-major), Q^T, dO^T
   __shared__ float lse_s[kBT], del_s[kBT];
+  const T* const Qs = tiles;
+  const T* const dOs = tiles + M::kRowTile;
+  const T* const QTs = tiles + 2 * M::kRowTile;
+  const T* const dOTs = tiles + 2 * M::kRowTile + M::kColTile;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, g = lane >> 5;
   const int64_t nbh = (int64_t)a.B * a.H;
@@ -216,18 +239,21 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
   const int nqt = (int)((a.T + kBT - 1) / kBT);
   for (int qt = (int)(k0 / kBT); qt < nqt; ++qt) {
     const int64_t q0 = (int64_t)qt * kBT;
-    __syncthreads();
-    load_rows<T, DP>(Qs, reinterpret_cast<const T*>(a.qh) + (bh * a.Tp + q0) * DP, tid);
-    load_rows<T, DP>(dOs, reinterpret_cast<const T*>(a.doh) + (bh * a.Tp + q0) * DP, tid);
-    const int64_t tile = (bh * a.nch + q0 / kChunk) * DP * kChunk;
-    load_cols<T, DP>(QTs, reinterpret_cast<const T*>(a.qh_t) + tile, (int)(q0 % kChunk), tid);
-    load_cols<T, DP>(dOTs, reinterpret_cast<const T*>(a.doh_t) + tile, (int)(q0 % kChunk), tid);
-    if (tid < kBT) {
-      const bool qin = q0 + tid < a.T;
-      lse_s[tid] = qin ? a.lse[bh * a.Tp + q0 + tid] : INFINITY;
-      del_s[tid] = qin ? a.delta[bh * a.Tp + q0 + tid] : 0.f;
+    {
+      u32x4 r[M::IT];
+      const int64_t tile = (bh * a.nch + q0 / kChunk) * DP * kChunk;
+      const T* const rows[2] = {reinterpret_cast<const T*>(a.qh) + (bh * a.Tp + q0) * DP,
+                                reinterpret_cast<const T*>(a.doh) + (bh * a.Tp + q0) * DP};
+      const T* const cols[2] = {reinterpret_cast<const T*>(a.qh_t) + tile, reinterpret_cast<const T*>(a.doh_t) + tile};
+      M::load(r, rows, cols, (int)(q0 % kChunk), tid);
+      const bool qin = tid < kBT && q0 + tid < a.T;
+      const float ls = qin ? a.lse[bh * a.Tp + q0 + tid] : INFINITY;
+      const float dl = qin ? a.delta[bh * a.Tp + q0 + tid] : 0.f;
+      __syncthreads();                      // the previous tile is consumed
+      M::store(tiles, r, tid);
+      if (tid < kBT) { lse_s[tid] = ls; del_s[tid] = dl; }
+      __syncthreads();
     }
-    __syncthreads();
     if (!wave_in || q0 + kBT - 1 < kw0) continue;     // no query of the tile sees these keys
 
     // S = Q K^T and dP = dO V^T (queries on the rows, this wave's keys on the lanes)
@@ -295,13 +321,15 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
 // attention backward: dQ
 // ---------------------------------------------------------------------------
 template <typename T, int DP>
-__global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(2))) attn_bwd_dq(BwdArgs a) {
+__global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1))) attn_bwd_dq(BwdArgs a) {
   using C = BwdCfg<T, DP>;
   typedef typename frag<T>::type frag_t;
   constexpr bool kBF = sizeof(T) == 2;
-  __shared__ __align__(16) T Ks[kBT * C::RS];
-  __shared__ __align__(16) T Vs[kBT * C::RS];
-  __shared__ __align__(16) T KTs[DP * C::TS];
+  using M = typename TileCopy<T, DP>::template Multi<2, 1>;
+  __shared__ __align__(16) T tiles[M::kElems];   // K, V (row-major), K^T
+  const T* const Ks = tiles;
+  const T* const Vs = tiles + M::kRowTile;
+  const T* const KTs = tiles + 2 * M::kRowTile;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, g = lane >> 5;
   const int64_t nbh = (int64_t)a.B * a.H;
@@ -336,12 +364,16 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
   const int nkt = qlast >= q0 ? (int)(qlast / kBT) + 1 : 0;
   for (int kt = 0; kt < nkt; ++kt) {
     const int64_t k0 = (int64_t)kt * kBT;
-    __syncthreads();
-    load_rows<T, DP>(Ks, reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + k0) * DP, tid);
-    load_rows<T, DP>(Vs, reinterpret_cast<const T*>(a.vh) + (bh * a.Tp + k0) * DP, tid);
-    load_cols<T, DP>(KTs, reinterpret_cast<const T*>(a.kh_t) + (bh * a.nch + k0 / kChunk) * DP * kChunk,
-                     (int)(k0 % kChunk), tid);
-    __syncthreads();
+    {
+      u32x4 r[M::IT];
+      const T* const rows[2] = {reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + k0) * DP,
+                                reinterpret_cast<const T*>(a.vh) + (bh * a.Tp + k0) * DP};
+      const T* const cols[1] = {reinterpret_cast<const T*>(a.kh_t) + (bh * a.nch + k0 / kChunk) * DP * kChunk};
+      M::load(r, rows, cols, (int)(k0 % kChunk), tid);
+      __syncthreads();                      // the previous tile is consumed
+      M::store(tiles, r, tid);
+      __syncthreads();
+    }
     if (qw0 >= a.T || k0 > qw0 + kBT - 1) continue;     // every key of the tile is after every query
 
     // S^T = K Q^T and dP^T = V dO^T (keys on the rows, this wave's queries on the lanes)
@@ -504,7 +536,9 @@ __global__ void __launch_bounds__(kBwdThreads) link_bwd(BwdArgs a) {
       cv[3 * j + 1] += oh[2] * dh[0] - oh[0] * dh[2];
       cv[3 * j + 2] += oh[0] * dh[1] - oh[1] * dh[0];
     });
-    auto acc = [&](const void* gsrc, const float* src) {     // cv += grad x value
+    // cv += grad x value, and the gradient rotated back to the reference
+    // frame (dq = P dqh, ...) while it is in registers
+    auto acc = [&](const void* gsrc, const float* src, void* dst, int64_t rs, int64_t hs) {
       load_span<IO, NV, WIDE>(reinterpret_cast<const IO*>(gsrc) + prow, nd, v);
       load_span<float, NV, WIDE>(src + prow, nd, u);
       static_for<NBJ>([&](auto j) {
@@ -512,10 +546,14 @@ __global__ void __launch_bounds__(kBwdThreads) link_bwd(BwdArgs a) {
         cv[3 * j + 1] += u[3 * j + 2] * v[3 * j] - u[3 * j] * v[3 * j + 2];
         cv[3 * j + 2] += u[3 * j] * v[3 * j + 1] - u[3 * j + 1] * v[3 * j];
       });
+      static_for<NBJ>([&](auto j) {
+        rot_apply(qmat(qP[j]), u[3 * j], u[3 * j + 1], u[3 * j + 2], v[3 * j], v[3 * j + 1], v[3 * j + 2]);
+      });
+      store_span<IO, NV, WIDE>(reinterpret_cast<IO*>(dst) + (b * a.T + t) * rs + h * hs + e0, nd, v);
     };
-    acc(a.qh, a.dqh);
-    acc(a.kh, a.dkh);
-    acc(a.vh, a.dvh);
+    acc(a.qh, a.dqh, a.dq, a.dq_rs, a.dq_hs);
+    acc(a.kh, a.dkh, a.dk, a.dk_rs, a.dk_hs);
+    acc(a.vh, a.dvh, a.dv, a.dv_rs, a.dv_hs);
   }
   // inclusive suffix over the wave's 16 tokens (lane + 4 is the next token)
   float sv[NV];
@@ -581,18 +619,6 @@ __global__ void __launch_bounds__(kBwdThreads) link_bwd(BwdArgs a) {
   });
   store_span<float, NV, WIDE>(a.dgq + (b * a.T + t) * a.dgq_rs + h * a.dgq_hs + e0, nd, da);
   if (a.gen_mode == 0) store_span<float, NV, WIDE>(a.dgk + (b * a.T + tn) * a.dgk_rs + h * a.dgk_hs + e0, nd, da);
-  // dq = P dqh, dk = P dkh, dv = P dvh
-  auto rotate_out = [&](const float* src, void* dst, int64_t rs, int64_t hs) {
-    float u[NV], y[NV];
-    load_span<float, NV, WIDE>(src + prow, nd, u);
-    static_for<NBJ>([&](auto j) {
-      rot_apply(qmat(qP[j]), u[3 * j], u[3 * j + 1], u[3 * j + 2], y[3 * j], y[3 * j + 1], y[3 * j + 2]);
-    });
-    store_span<IO, NV, WIDE>(reinterpret_cast<IO*>(dst) + (b * a.T + t) * rs + h * hs + e0, nd, y);
-  };
-  rotate_out(a.dqh, a.dq, a.dq_rs, a.dq_hs);
-  rotate_out(a.dkh, a.dk, a.dk_rs, a.dk_hs);
-  rotate_out(a.dvh, a.dv, a.dv_rs, a.dv_hs);
   if (p == 0) {
     const int64_t prow0 = (bh * a.Tp + t) * DP;
     for (int e = 3 * a.nb; e < a.d; ++e) {     // dims outside the rotation blocks
