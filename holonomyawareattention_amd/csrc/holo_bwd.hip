@@ -38,12 +38,17 @@
 namespace holo {
 
 constexpr int kBT = 32;              // queries / keys per backward MFMA tile
+constexpr int kFill = 64;            // rows per LDS fill of the dQ kernel (two MFMA tiles)
+#ifndef HOLO_DKDV_FILL
+#define HOLO_DKDV_FILL 32
+#endif
+constexpr int kFillKV = HOLO_DKDV_FILL;   // query rows per LDS fill of the dK/dV kernel
 constexpr int kBwdThreads = 256;     // 4 waves
 
-template <typename T, int DP> struct BwdCfg {
+template <typename T, int DP, int ROWS = kFill> struct BwdCfg {
   static constexpr int E = 16 / sizeof(T);        // elements per 16 bytes
   static constexpr int RS = DP + E;               // LDS stride of a row-major tile row
-  static constexpr int TS = kBT + E;              // LDS stride of a transposed tile row (16 B aligned)
+  static constexpr int TS = ROWS + E;             // LDS stride of a transposed tile row (16 B aligned)
   static constexpr int QF = sizeof(T) == 2 ? DP / 16 : DP / 2;   // MFMA k-steps over DP
 };
 
@@ -51,13 +56,13 @@ template <typename T> struct frag;
 template <> struct frag<bf16> { typedef bf16x8 type; };
 template <> struct frag<float> { typedef float type; };
 
-// Cooperative copies of one 32-row / 32-column tile into LDS. All of a
+// Cooperative copies of ROWS-row / ROWS-column tiles into LDS. All of a
 // thread's global loads are issued before its LDS stores (one memory round
 // trip per tile, not one per chunk).
-template <typename T, int DP> struct TileCopy {
-  using C = BwdCfg<T, DP>;
-  static constexpr int RCPR = DP / C::E, TCPR = kBT / C::E;    // 16-byte chunks per row
-  static constexpr int RN = kBT * RCPR, TN = DP * TCPR;         // chunks per tile
+template <typename T, int DP, int ROWS = kFill> struct TileCopy {
+  using C = BwdCfg<T, DP, ROWS>;
+  static constexpr int RCPR = DP / C::E, TCPR = ROWS / C::E;   // 16-byte chunks per row
+  static constexpr int RN = ROWS * RCPR, TN = DP * TCPR;        // chunks per tile
   // NA tiles at once, flattened over the threads: tile k's chunk i is flat
   // index k*RN + i (row-major tiles first, then transposed ones)
   template <int NR, int NT>
@@ -77,9 +82,9 @@ template <typename T, int DP> struct TileCopy {
         }
       });
     }
-    // LDS destination: the NR row-major tiles (kBT * RS elements each), then
+    // LDS destination: the NR row-major tiles (ROWS * RS elements each), then
     // the NT transposed tiles (DP * TS each), back to back from `lds`
-    static constexpr int kRowTile = kBT * C::RS, kColTile = DP * C::TS;
+    static constexpr int kRowTile = ROWS * C::RS, kColTile = DP * C::TS;
     static constexpr int kElems = NR * kRowTile + NT * kColTile;
     static __device__ __forceinline__ void store(T* lds, const u32x4 (&r)[IT], int tid) {
       static_for<IT>([&](auto it) {
@@ -199,12 +204,12 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_prep(BwdArgs a) {
 // both operands, so the accumulator is the operand with no data movement.
 template <typename T, int DP>
 __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1))) attn_bwd_dkdv(BwdArgs a) {
-  using C = BwdCfg<T, DP>;
+  using C = BwdCfg<T, DP, kFillKV>;
   typedef typename frag<T>::type frag_t;
   constexpr bool kBF = sizeof(T) == 2;
-  using M = typename TileCopy<T, DP>::template Multi<2, 2>;
+  using M = typename TileCopy<T, DP, kFillKV>::template Multi<2, 2>;
   __shared__ __align__(16) T tiles[M::kElems];   // Q, dO (row-major), Q^T, dO^T
-  __shared__ float lse_s[kBT], del_s[kBT];
+  __shared__ float lse_s[kFillKV], del_s[kFillKV];
   const T* const Qs = tiles;
   const T* const dOs = tiles + M::kRowTile;
   const T* const QTs = tiles + 2 * M::kRowTile;
@@ -236,9 +241,9 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
   static_for<DP / 32>([&](auto i) { dK[i] = f32x16{}; dV[i] = f32x16{}; });
   const float cl = a.scale_log2;
   const int64_t key = kw0 + lr;
-  const int nqt = (int)((a.T + kBT - 1) / kBT);
-  for (int qt = (int)(k0 / kBT); qt < nqt; ++qt) {
-    const int64_t q0 = (int64_t)qt * kBT;
+  const int nfill = (int)((a.T + kFillKV - 1) / kFillKV);
+  for (int qf = (int)(k0 / kFillKV); qf < nfill; ++qf) {
+    const int64_t q0 = (int64_t)qf * kFillKV;
     {
       u32x4 r[M::IT];
       const int64_t tile = (bh * a.nch + q0 / kChunk) * DP * kChunk;
@@ -246,65 +251,69 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
                                 reinterpret_cast<const T*>(a.doh) + (bh * a.Tp + q0) * DP};
       const T* const cols[2] = {reinterpret_cast<const T*>(a.qh_t) + tile, reinterpret_cast<const T*>(a.doh_t) + tile};
       M::load(r, rows, cols, (int)(q0 % kChunk), tid);
-      const bool qin = tid < kBT && q0 + tid < a.T;
+      const bool qin = tid < kFillKV && q0 + tid < a.T;
       const float ls = qin ? a.lse[bh * a.Tp + q0 + tid] : INFINITY;
       const float dl = qin ? a.delta[bh * a.Tp + q0 + tid] : 0.f;
-      __syncthreads();                      // the previous tile is consumed
+      __syncthreads();                      // the previous fill is consumed
       M::store(tiles, r, tid);
-      if (tid < kBT) { lse_s[tid] = ls; del_s[tid] = dl; }
+      if (tid < kFillKV) { lse_s[tid] = ls; del_s[tid] = dl; }
       __syncthreads();
     }
-    if (!wave_in || q0 + kBT - 1 < kw0) continue;     // no query of the tile sees these keys
+    static_for<kFillKV / kBT>([&](auto sub) {
+      const int64_t qs0 = q0 + kBT * sub;
+      if (!wave_in || qs0 + kBT - 1 < kw0) return;    // no query of the tile sees these keys
+      const int ro = kBT * sub;                       // row offset of the tile within the fill
 
-    // S = Q K^T and dP = dO V^T (queries on the rows, this wave's keys on the lanes)
-    f32x16 S = f32x16{}, dP = f32x16{};
-    static_for<C::QF>([&](auto s) {
-      if constexpr (kBF) {
-        const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&Qs[lr * C::RS + 16 * s + 8 * g]);
-        const bf16x8 da = *reinterpret_cast<const bf16x8*>(&dOs[lr * C::RS + 16 * s + 8 * g]);
-        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, kf[s], S, 0, 0, 0);
-        dP = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, vf[s], dP, 0, 0, 0);
-      } else {
-        S = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[lr * C::RS + 2 * s + g], kf[s], S, 0, 0, 0);
-        dP = __builtin_amdgcn_mfma_f32_32x32x2f32(dOs[lr * C::RS + 2 * s + g], vf[s], dP, 0, 0, 0);
-      }
-    });
-    // Pm = exp2(scale_log2 S - lse) (zero above the diagonal and for padding
-    // keys; padding queries carry lse = +inf), dS = Pm (dP - delta)
-    static_for<16>([&](auto r) {
-      const int qr = 8 * (r >> 2) + 4 * g + (r & 3);
-      float pm = exp2f(__builtin_fmaf(S[(int)r], cl, -lse_s[qr]));
-      if (key > q0 + qr || key >= a.T) pm = 0.f;
-      S[(int)r] = pm;
-      dP[(int)r] = pm * (dP[(int)r] - del_s[qr]);
-    });
-    // dV += Pm^T dO, dK += dS^T Q (this wave's keys on the rows, dims on the lanes)
-    if constexpr (kBF) {
-      bf16x8 pb[2], sb[2];
-      static_for<2>([&](auto hh) {
-        static_for<8>([&](auto e) { pb[hh][(int)e] = (bf16)S[8 * hh + e]; sb[hh][(int)e] = (bf16)dP[8 * hh + e]; });
+      // S = Q K^T and dP = dO V^T (queries on the rows, this wave's keys on the lanes)
+      f32x16 S = f32x16{}, dP = f32x16{};
+      static_for<C::QF>([&](auto s) {
+        if constexpr (kBF) {
+          const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&Qs[(ro + lr) * C::RS + 16 * s + 8 * g]);
+          const bf16x8 da = *reinterpret_cast<const bf16x8*>(&dOs[(ro + lr) * C::RS + 16 * s + 8 * g]);
+          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, kf[s], S, 0, 0, 0);
+          dP = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, vf[s], dP, 0, 0, 0);
+        } else {
+          S = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[(ro + lr) * C::RS + 2 * s + g], kf[s], S, 0, 0, 0);
+          dP = __builtin_amdgcn_mfma_f32_32x32x2f32(dOs[(ro + lr) * C::RS + 2 * s + g], vf[s], dP, 0, 0, 0);
+        }
       });
-      static_for<2>([&](auto hh) {
-        static_for<DP / 32>([&](auto db) {
-          const T* dr = &dOTs[(32 * db + lr) * C::TS + 16 * hh + 4 * g];
-          const T* qr = &QTs[(32 * db + lr) * C::TS + 16 * hh + 4 * g];
-          const bf16x4 dlo = *reinterpret_cast<const bf16x4*>(dr), dhi = *reinterpret_cast<const bf16x4*>(dr + 8);
-          const bf16x4 qlo = *reinterpret_cast<const bf16x4*>(qr), qhi = *reinterpret_cast<const bf16x4*>(qr + 8);
-          const bf16x8 bo = {dlo[0], dlo[1], dlo[2], dlo[3], dhi[0], dhi[1], dhi[2], dhi[3]};
-          const bf16x8 bq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
-          dV[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pb[hh], bo, dV[db], 0, 0, 0);
-          dK[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sb[hh], bq, dK[db], 0, 0, 0);
-        });
-      });
-    } else {
+      // Pm = exp2(scale_log2 S - lse) (zero above the diagonal and for padding
+      // keys; padding queries carry lse = +inf), dS = Pm (dP - delta)
       static_for<16>([&](auto r) {
         const int qr = 8 * (r >> 2) + 4 * g + (r & 3);
-        static_for<DP / 32>([&](auto db) {
-          dV[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(S[(int)r], dOTs[(32 * db + lr) * C::TS + qr], dV[db], 0, 0, 0);
-          dK[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(dP[(int)r], QTs[(32 * db + lr) * C::TS + qr], dK[db], 0, 0, 0);
-        });
+        float pm = exp2f(__builtin_fmaf(S[(int)r], cl, -lse_s[ro + qr]));
+        if (key > qs0 + qr || key >= a.T) pm = 0.f;
+        S[(int)r] = pm;
+        dP[(int)r] = pm * (dP[(int)r] - del_s[ro + qr]);
       });
-    }
+      // dV += Pm^T dO, dK += dS^T Q (this wave's keys on the rows, dims on the lanes)
+      if constexpr (kBF) {
+        bf16x8 pb[2], sb[2];
+        static_for<2>([&](auto hh) {
+          static_for<8>([&](auto e) { pb[hh][(int)e] = (bf16)S[8 * hh + e]; sb[hh][(int)e] = (bf16)dP[8 * hh + e]; });
+        });
+        static_for<2>([&](auto hh) {
+          static_for<DP / 32>([&](auto db) {
+            const T* dr = &dOTs[(32 * db + lr) * C::TS + ro + 16 * hh + 4 * g];
+            const T* qr = &QTs[(32 * db + lr) * C::TS + ro + 16 * hh + 4 * g];
+            const bf16x4 dlo = *reinterpret_cast<const bf16x4*>(dr), dhi = *reinterpret_cast<const bf16x4*>(dr + 8);
+            const bf16x4 qlo = *reinterpret_cast<const bf16x4*>(qr), qhi = *reinterpret_cast<const bf16x4*>(qr + 8);
+            const bf16x8 bo = {dlo[0], dlo[1], dlo[2], dlo[3], dhi[0], dhi[1], dhi[2], dhi[3]};
+            const bf16x8 bq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
+            dV[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pb[hh], bo, dV[db], 0, 0, 0);
+            dK[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sb[hh], bq, dK[db], 0, 0, 0);
+          });
+        });
+      } else {
+        static_for<16>([&](auto r) {
+          const int qr = ro + 8 * (r >> 2) + 4 * g + (r & 3);
+          static_for<DP / 32>([&](auto db) {
+            dV[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(S[(int)r], dOTs[(32 * db + lr) * C::TS + qr], dV[db], 0, 0, 0);
+            dK[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(dP[(int)r], QTs[(32 * db + lr) * C::TS + qr], dK[db], 0, 0, 0);
+          });
+        });
+      }
+    });
   }
   if (kw0 < a.Tp) {
     static_for<DP / 32>([&](auto db) {
@@ -361,60 +370,64 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
   static_for<DP / 32>([&](auto i) { dQ[i] = f32x16{}; });
 
   int64_t qlast = q0 + 127 < a.T - 1 ? q0 + 127 : a.T - 1;    // the workgroup's last query
-  const int nkt = qlast >= q0 ? (int)(qlast / kBT) + 1 : 0;
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int64_t k0 = (int64_t)kt * kBT;
+  const int nfill = qlast >= q0 ? (int)(qlast / kFill) + 1 : 0;
+  for (int kfi = 0; kfi < nfill; ++kfi) {
+    const int64_t k0 = (int64_t)kfi * kFill;
     {
       u32x4 r[M::IT];
       const T* const rows[2] = {reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + k0) * DP,
                                 reinterpret_cast<const T*>(a.vh) + (bh * a.Tp + k0) * DP};
       const T* const cols[1] = {reinterpret_cast<const T*>(a.kh_t) + (bh * a.nch + k0 / kChunk) * DP * kChunk};
-      M::load(r, rows, cols, (int)(k0 % kChunk), tid);
-      __syncthreads();                      // the previous tile is consumed
+      M::load(r, rows, cols, 0, tid);
+      __syncthreads();                      // the previous fill is consumed
       M::store(tiles, r, tid);
       __syncthreads();
     }
-    if (qw0 >= a.T || k0 > qw0 + kBT - 1) continue;     // every key of the tile is after every query
+    static_for<kFill / kBT>([&](auto sub) {
+      const int64_t ks0 = k0 + kBT * sub;
+      if (qw0 >= a.T || ks0 > qw0 + kBT - 1) return;     // every key of the tile is after every query
+      const int ro = kBT * sub;
 
-    // S^T = K Q^T and dP^T = V dO^T (keys on the rows, this wave's queries on the lanes)
-    f32x16 S = f32x16{}, dP = f32x16{};
-    static_for<C::QF>([&](auto s) {
+      // S^T = K Q^T and dP^T = V dO^T (keys on the rows, this wave's queries on the lanes)
+      f32x16 S = f32x16{}, dP = f32x16{};
+      static_for<C::QF>([&](auto s) {
+        if constexpr (kBF) {
+          const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[(ro + lr) * C::RS + 16 * s + 8 * g]);
+          const bf16x8 va = *reinterpret_cast<const bf16x8*>(&Vs[(ro + lr) * C::RS + 16 * s + 8 * g]);
+          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], S, 0, 0, 0);
+          dP = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, df[s], dP, 0, 0, 0);
+        } else {
+          S = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(ro + lr) * C::RS + 2 * s + g], qf[s], S, 0, 0, 0);
+          dP = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[(ro + lr) * C::RS + 2 * s + g], df[s], dP, 0, 0, 0);
+        }
+      });
+      static_for<16>([&](auto r) {
+        const int64_t kr = ks0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        float pm = exp2f(__builtin_fmaf(S[(int)r], cl, -lse));
+        if (kr > q || kr >= a.T) pm = 0.f;
+        dP[(int)r] = pm * (dP[(int)r] - del);
+      });
+      // dQ^T += K^T dS^T (dims on the rows, queries on the lanes)
       if constexpr (kBF) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&Ks[lr * C::RS + 16 * s + 8 * g]);
-        const bf16x8 va = *reinterpret_cast<const bf16x8*>(&Vs[lr * C::RS + 16 * s + 8 * g]);
-        S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[s], S, 0, 0, 0);
-        dP = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, df[s], dP, 0, 0, 0);
+        bf16x8 sb[2];
+        static_for<2>([&](auto hh) { static_for<8>([&](auto e) { sb[hh][(int)e] = (bf16)dP[8 * hh + e]; }); });
+        static_for<2>([&](auto hh) {
+          static_for<DP / 32>([&](auto db) {
+            const T* kr = &KTs[(32 * db + lr) * C::TS + ro + 16 * hh + 4 * g];
+            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kr), hi = *reinterpret_cast<const bf16x4*>(kr + 8);
+            const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            dQ[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, sb[hh], dQ[db], 0, 0, 0);
+          });
+        });
       } else {
-        S = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[lr * C::RS + 2 * s + g], qf[s], S, 0, 0, 0);
-        dP = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[lr * C::RS + 2 * s + g], df[s], dP, 0, 0, 0);
+        static_for<16>([&](auto r) {
+          const int kr = ro + 8 * (r >> 2) + 4 * g + (r & 3);
+          static_for<DP / 32>([&](auto db) {
+            dQ[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(KTs[(32 * db + lr) * C::TS + kr], dP[(int)r], dQ[db], 0, 0, 0);
+          });
+        });
       }
     });
-    static_for<16>([&](auto r) {
-      const int64_t kr = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
-      float pm = exp2f(__builtin_fmaf(S[(int)r], cl, -lse));
-      if (kr > q || kr >= a.T) pm = 0.f;
-      dP[(int)r] = pm * (dP[(int)r] - del);
-    });
-    // dQ^T += K^T dS^T (dims on the rows, queries on the lanes)
-    if constexpr (kBF) {
-      bf16x8 sb[2];
-      static_for<2>([&](auto hh) { static_for<8>([&](auto e) { sb[hh][(int)e] = (bf16)dP[8 * hh + e]; }); });
-      static_for<2>([&](auto hh) {
-        static_for<DP / 32>([&](auto db) {
-          const T* kr = &KTs[(32 * db + lr) * C::TS + 16 * hh + 4 * g];
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kr), hi = *reinterpret_cast<const bf16x4*>(kr + 8);
-          const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          dQ[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, sb[hh], dQ[db], 0, 0, 0);
-        });
-      });
-    } else {
-      static_for<16>([&](auto r) {
-        const int kr = 8 * (r >> 2) + 4 * g + (r & 3);
-        static_for<DP / 32>([&](auto db) {
-          dQ[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(KTs[(32 * db + lr) * C::TS + kr], dP[(int)r], dQ[db], 0, 0, 0);
-        });
-      });
-    }
   }
   if (qw0 < a.Tp) {
     float* dst = a.dqh + (bh * a.Tp + q) * DP;
