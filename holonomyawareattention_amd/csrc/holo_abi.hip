@@ -157,9 +157,9 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
              al(q, q_rs, q_hs, ie) && al(k, k_rs, k_hs, ie) && al(v, v_rs, v_hs, ie);
   }
   {
-    // chained-scan state: chunk inclusive prefixes, then the ticket counter
-    // and time-out flag (cleared by the scan's own reset launch)
-    const size_t nq = (size_t)B * H * a.nch * nb * 4;
+    // chained-scan state: chunk products and inclusive prefixes, then the
+    // ticket counter and time-out flag (cleared by the scan's own reset launch)
+    const size_t nq = (size_t)B * H * 2 * a.nch * nb * 4;
     a.incl = static_cast<float*>(workspace);
     a.ticket = reinterpret_cast<unsigned*>(a.incl + nq);
   }

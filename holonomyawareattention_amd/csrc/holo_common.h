@@ -45,12 +45,15 @@ template <> __device__ inline bf16 from_f32<bf16>(float x) { return (bf16)x; }
 // Quaternion (w, x, y, z); R(a (x) b) = R(a) R(b).
 struct quat { float w, x, y, z; };
 
+// Explicit fused multiply-adds: the rounding of a product is the same
+// wherever it is inlined (no context-dependent contraction), so a scan's
+// result does not depend on how its carries are grouped.
 __device__ inline quat qmul(const quat& a, const quat& b) {
   quat r;
-  r.w = a.w * b.w - a.x * b.x - a.y * b.y - a.z * b.z;
-  r.x = a.w * b.x + a.x * b.w + a.y * b.z - a.z * b.y;
-  r.y = a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x;
-  r.z = a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w;
+  r.w = __builtin_fmaf(a.w, b.w, -__builtin_fmaf(a.x, b.x, __builtin_fmaf(a.y, b.y, a.z * b.z)));
+  r.x = __builtin_fmaf(a.w, b.x, __builtin_fmaf(a.x, b.w, __builtin_fmaf(a.y, b.z, -(a.z * b.y))));
+  r.y = __builtin_fmaf(a.w, b.y, __builtin_fmaf(-a.x, b.z, __builtin_fmaf(a.y, b.w, a.z * b.x)));
+  r.z = __builtin_fmaf(a.w, b.z, __builtin_fmaf(a.x, b.y, __builtin_fmaf(-a.y, b.x, a.z * b.w)));
   return r;
 }
 

@@ -17,10 +17,11 @@ struct ScanArgs {
   void* qh; void* kh; void* vh_t; float* P; float* hol;
   int p_format;    // 0: fp32 quaternions, 1: int16 (round(32767 q/|q|))
   int wide;        // 16-byte row path of the scan (d in {48, 72, 96}, aligned rows)
-  float* incl;     // (B, H, nch, nb, 4) prefix product through each chunk (chained-scan state)
+  float* incl;     // chained-scan state: chunk products (B, H, nch, nb, 4), then inclusive prefixes (same shape)
   unsigned* ticket;  // [0]: chunk ticket counter, [1]: carry-wait time-out flag
 };
 size_t scan_state_bytes(int B, int64_t T, int H, int d);
+constexpr int kScanGroup = 16;   // chunks per carry-chain hop of the scan when the chain lags
 
 struct AttnArgs {
   int B, H, d, nb, Dp;

@@ -13,17 +13,21 @@
 // (b, h, chunk):
 //   1. link quaternions of the chunk's links -> LDS;
 //   2. prefixes within the chunk over all threads (8 segments of 8 links per
-//      block), the chunk product T_c, a wait for the product of all earlier
-//      chunks C = incl[c-1] published by the previous chunk's workgroup, and
-//      incl[c] = T_c C published for the next one (a chained scan through the
-//      workspace);
+//      block) and the chunk product T_c, published at once; the product of
+//      all earlier chunks C_c = incl[c-1], read from the previous chunk when
+//      it has published it, otherwise composed as T_{c-1} ... T_{c0}
+//      incl[c0-1] from the products of the earlier chunks of its group of 16
+//      (c0 = 16 floor(c/16)) and the group boundary's prefix, so a lagging
+//      chain advances one group per hop instead of one chunk; then
+//      incl[c] = T_c C_c is published (a chained scan through the workspace);
 //   3. all threads: P_t, written to P, and the transported qh, kh, vh.
 // Workgroups take chunks in ticket order (a global counter), chunk-major, so a
-// chunk only ever waits on a chunk that was handed out earlier and is running
-// or done: the wait always ends. Its polls are bounded anyway; a time-out
+// chunk only ever waits on chunks that were handed out earlier and are running
+// or done: the waits always end. Polls are bounded anyway; a time-out
 // (impossible in a conforming launch) sets a flag in the workspace and the
-// chunk's outputs become NaN. The carry is always incl[c-1], so the
-// composition order, and every bit of the result, does not depend on timing.
+// chunk's outputs become NaN. C_c is always the same nested product
+// T_{c-1} (T_{c-2} (... (T_0 I))), so the composition order, and every bit of
+// the result, does not depend on timing.
 // Threads of a wave cover consecutive blocks of the same token rows, so the
 // token-major input rows are read contiguously.
 #include "holo_chain.h"
@@ -46,7 +50,7 @@ __device__ inline quat link_quat(const ScanArgs& a, int b, int h, int blk, int64
 
 size_t scan_state_bytes(int B, int64_t T, int H, int d) {
   const int64_t nch = padded_seq(T) / kChunk;
-  return (size_t)B * H * nch * (d / 3) * 4 * sizeof(float) + 256;
+  return (size_t)B * H * 2 * nch * (d / 3) * 4 * sizeof(float) + 256;
 }
 
 // clears the chained-scan state and the ticket counter before every scan
@@ -71,12 +75,12 @@ __device__ __forceinline__ void take_ticket(const ScanArgs& a, int64_t& bh, int6
   bh = tk % nbh;
 }
 
-// product of chunks 0 .. c-1 for one block (c >= 1): the inclusive prefix
-// that chunk c-1 publishes. Waiting for exactly that value (rather than
-// composing whatever predecessor state happens to be ready) keeps the
-// association, and so every bit of the result, independent of timing.
-__device__ inline quat wait_prefix(const ScanArgs& a, int64_t bh, int64_t c, int blk) {
-  const float* slot = a.incl + ((bh * a.nch + c - 1) * a.nb + blk) * 4;
+// A published slot of the chained state (a chunk product, or a group's
+// prefix), waited for with bounded polls. Waiting for exactly these values
+// (rather than composing whatever predecessor state happens to be ready)
+// keeps the association, and so every bit of the result, independent of
+// timing.
+__device__ inline quat wait_slot(const ScanArgs& a, const float* slot) {
   quat x;
   for (int polls = 0; polls < kMaxPolls; ++polls) {
     if (get_quat(slot, x)) return x;
@@ -118,8 +122,36 @@ __device__ inline void chunk_prefix(const ScanArgs& a, float* gs, float* ss, flo
     for (int k = 0; k < seg; ++k) E = qmul(load_quat(&ss[(k * nb + blk) * 4]), E);
     if (seg == 7) {
       const quat Tc = qmul(load_quat(&ss[(7 * nb + blk) * 4]), E);       // chunk product
-      const quat C = c == 0 ? qident() : wait_prefix(a, bh, c, blk);
-      if (c + 1 < a.nch) put_quat(a.incl + ((bh * a.nch + c) * nb + blk) * 4, qmul(Tc, C));
+      // C_c = T_{c-1} (T_{c-2} (... (T_{c0} incl[c0-1]))) = incl[c-1]: taken
+      // from incl[c-1] when chunk c-1 has published it, otherwise composed
+      // from the group boundary's incl[c0-1] and the products T_j of the
+      // group's earlier chunks (published before any wait). Both give the
+      // same bits (same nesting, context-independent qmul), so the result
+      // does not depend on which one was ready.
+      const int64_t c0 = c / kScanGroup * kScanGroup;
+      float* tot = a.incl + (bh * a.nch * nb + blk) * 4;                 // T_j at tot[j * nb * 4]
+      float* inc = a.incl + ((int64_t)a.B * a.H * a.nch + bh * a.nch) * nb * 4 + blk * 4;   // incl[j]
+      if (c - c0 < kScanGroup - 1 && c + 1 < a.nch) put_quat(tot + c * nb * 4, Tc);   // read by the group's later chunks
+      quat C = qident();
+      if (c > 0 && !get_quat(inc + (c - 1) * nb * 4, C)) {
+        if (c == c0) {
+          C = wait_slot(a, inc + (c - 1) * nb * 4);
+        } else {
+          C = c0 == 0 ? qident() : wait_slot(a, inc + (c0 - 1) * nb * 4);
+          for (int64_t j = c0; j < c; j += 4) {      // four products per memory round trip
+            quat tj[4];
+            bool ok[4];
+            static_for<4>([&](auto i) { ok[i] = j + i < c ? get_quat(tot + (j + i) * nb * 4, tj[i]) : true; });
+            static_for<4>([&](auto i) {
+              if (j + i < c) {
+                if (!ok[i]) tj[i] = wait_slot(a, tot + (j + i) * nb * 4);
+                C = qmul(tj[i], C);
+              }
+            });
+          }
+        }
+      }
+      if (c + 1 < a.nch) put_quat(inc + c * nb * 4, qmul(Tc, C));
       store_quat(&cs[blk * 4], C);
     }
   }
@@ -368,7 +400,7 @@ hipError_t launch_chain_reset(void* state, int64_t n_pairs, unsigned* ticket, hi
 template <typename IO, typename GT>
 hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
   const int tpb = 256;
-  const int64_t n_pairs = (int64_t)a.B * a.H * a.nch * a.nb * 2;    // 64-bit words of incl
+  const int64_t n_pairs = (int64_t)a.B * a.H * 2 * a.nch * a.nb * 2;    // 64-bit words of the state
   hipLaunchKernelGGL(scan_reset, dim3((unsigned)((n_pairs + tpb - 1) / tpb > 0 ? (n_pairs + tpb - 1) / tpb : 1)),
                      dim3(tpb), 0, s, reinterpret_cast<uint64_t*>(a.incl), n_pairs, a.ticket);
   const dim3 grid((unsigned)((int64_t)a.B * a.H * a.nch));

@@ -48,9 +48,10 @@ def test_version_and_layout_queries(lib):
     assert lib.holo_abi_version() >> 16 >= 2
     assert [lib.holo_padded_head_dim(d) for d in (1, 12, 32, 33, 48, 96)] == [32, 32, 32, 64, 64, 96]
     assert [lib.holo_padded_seq_len(t) for t in (1, 64, 65, 2048)] == [64, 64, 128, 2048]
-    # chained-scan state: one fp32 quaternion array (chunk inclusive prefixes)
-    # of B*H*chunks*nb, then 256 bytes for the ticket counter and flag
-    assert lib.holo_geom_scan_workspace_size(16, 2048, 16, 96) == 16 * 16 * 32 * 32 * 16 + 256
+    # chained-scan state: fp32 quaternions for every chunk product and every
+    # chunk inclusive prefix per (b, h, block), then 256 bytes for the ticket
+    # counter and flag
+    assert lib.holo_geom_scan_workspace_size(16, 2048, 16, 96) == 16 * 16 * 2 * 32 * 32 * 16 + 256
     assert lib.holo_geom_scan_workspace_size(1, 1, 1, 2) == 256
     assert lib.holo_geom_scan_workspace_size(0, 2048, 16, 96) == 0
 
