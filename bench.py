@@ -40,12 +40,14 @@ CONFIGS = {
 }
 
 
-def scan_bytes_per_token_head(d: int, io_bytes: int, gen_bytes: int = 4, quat_bytes: int = 16) -> int:
-    """Algorithmic HBM bytes of the scan stage per (token, head): read the two
-    generator halves gq, gk (3*nb each, fp32) and q, k, v (d each); write qh,
-    kh, vh (d each) and P (nb quaternions: 16 B in fp32, 8 B as int16)."""
+def scan_bytes_per_token_head(d: int, io_bytes: int, gen_bytes: int = 4, quat_bytes: int = 16,
+                              gen_reads: int = 2) -> int:
+    """Algorithmic HBM bytes of the scan stage per (token, head): read the
+    generator output (gq and gk for the additive generator, one edge-MLP
+    output for the interaction one: 3*nb fp32 each) and q, k, v (d each);
+    write qh, kh, vh (d each) and P (nb quaternions: 16 B in fp32, 8 B as int16)."""
     nb = d // 3
-    return 2 * 3 * nb * gen_bytes + 3 * d * io_bytes + 3 * d * io_bytes + nb * quat_bytes
+    return gen_reads * 3 * nb * gen_bytes + 3 * d * io_bytes + 3 * d * io_bytes + nb * quat_bytes
 
 
 def attention_core_flops(B, T, H, d) -> float:
@@ -58,7 +60,7 @@ def projection_flops(B, T, D, m_total) -> float:
     return 2.0 * B * T * D * (3 * D + 2 * m_total + D)
 
 
-def cpu_baseline(cfg, x_np, W, min_seconds=10.0):
+def cpu_baseline(cfg, x_np, W, min_seconds=10.0, link_mode="additive"):
     """Oracle restatement of core/attention_fast_chunked.py (fp32, dense
     matrix_exp, sequential scan, BLOCK_K=64 streaming with the wrap branch),
     timed on whole batch rows of the workload (full T) until min_seconds have
@@ -72,10 +74,10 @@ def cpu_baseline(cfg, x_np, W, min_seconds=10.0):
     Wt = {k: torch.as_tensor(v).float() for k, v in W.items()}
     rows = 0
     with torch.no_grad():
-        holo_ref.forward_chunked(torch.as_tensor(x_np[:1, :64]).float(), Wt, H, cfg["es"])  # warm-up
+        holo_ref.forward_chunked(torch.as_tensor(x_np[:1, :64]).float(), Wt, H, cfg["es"], link_mode)  # warm-up
         t0 = time.perf_counter()
         while rows < B and (rows == 0 or time.perf_counter() - t0 < min_seconds):
-            holo_ref.forward_chunked(torch.as_tensor(x_np[rows:rows + 1, :Ts]).float(), Wt, H, cfg["es"])
+            holo_ref.forward_chunked(torch.as_tensor(x_np[rows:rows + 1, :Ts]).float(), Wt, H, cfg["es"], link_mode)
             rows += 1
         dt = time.perf_counter() - t0
     span = f"full T={T} each" if Ts == T else (f"the first {Ts} of T={T} tokens each (a prefix: the "
@@ -459,6 +461,9 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="config 5: incremental decode after a prefill (one JSON line) and exit")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--link", default="additive", choices=["additive", "interaction"],
+                    help="link generator of the layer (the reference module's default is interaction; the "
+                         "configured workloads use the additive one)")
     ap.add_argument("--train", action="store_true",
                     help="forward + backward of one layer at --config (one JSON line) and exit")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
@@ -495,10 +500,10 @@ def main():
     dt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
     dev = torch.device("cuda:0")
 
-    inp = synth.layer_inputs(2, B, T, D, H, "additive")
+    inp = synth.layer_inputs(2, B, T, D, H, args.link)
     x_np = inp.pop("x")
     m = PathOrderedGeometricMHA(D, n_heads=H, edge_scale=es)
-    m.link_mode = "additive"
+    m.link_mode = args.link
     with torch.no_grad():
         for k, p in m.state_dict().items():
             if k in inp:
@@ -549,9 +554,13 @@ def main():
     tokens = B * T
     m_total = H * m.m_dim
     fl_core = attention_core_flops(B, T, H, d)
-    fl_proj = projection_flops(B, T, D, m_total)
+    if args.link == "additive":
+        fl_proj = projection_flops(B, T, D, m_total)
+    else:                                   # qkv + out, and the edge MLP 2D -> 4D -> H*m
+        fl_proj = 2.0 * B * T * D * 4 * D + 2.0 * B * T * (2 * D * 4 * D + 4 * D * m_total)
     io_bytes = 2 if dt == torch.bfloat16 else 4
-    scan_bytes = scan_bytes_per_token_head(d, io_bytes, quat_bytes=qbytes) * B * T * H
+    greads = 2 if args.link == "additive" else 1
+    scan_bytes = scan_bytes_per_token_head(d, io_bytes, quat_bytes=qbytes, gen_reads=greads) * B * T * H
     core_peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
     core_tflops = fl_core / (stage_ms[2] * 1e-3) / 1e12
     scan_gbs = scan_bytes / (stage_ms[1] * 1e-3) / 1e9
@@ -571,7 +580,7 @@ def main():
         "data": "synthetic (seeded SplitMix64/Box-Muller: x ~ N(0,1), weights ~ N(0,1/d_model))",
         "config": {"workload": f"{args.config}: one path-ordered attention layer forward",
                    "global_batch": B, "seq_len": T, "n_heads": H, "d_head": d, "d_model": D,
-                   "rotation": f"{d // 3} SO(3) blocks per head", "link_mode": "additive",
+                   "rotation": f"{d // 3} SO(3) blocks per head", "link_mode": args.link,
                    "edge_scale": es, "parallelism": "single GPU"},
         "layer_tflops": (fl_core + fl_proj) / (ms_per_step * 1e-3) / 1e12,
         "stages_ms": {"projections": stage_ms[0], "geom_scan": stage_ms[1],
@@ -585,15 +594,17 @@ def main():
         "roofline_scan": {"kernels": "scan_reset + chunk_apply (holo_geom_scan_fwd)",
                           "bound": "hbm", "achieved": scan_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": scan_gbs / PEAK_HBM_GBS,
-                          "traffic": traffic_from_profile(args.config, ["scan_reset", "chunk_apply"]),
+                          "traffic": (traffic_from_profile(args.config, ["scan_reset", "chunk_apply"])
+                                      if args.link == "additive" else None),
                           "bytes_per_launch": scan_bytes,
-                          "bytes_per_token_head": scan_bytes_per_token_head(d, io_bytes, quat_bytes=qbytes),
+                          "bytes_per_token_head": scan_bytes_per_token_head(d, io_bytes, quat_bytes=qbytes,
+                                                                            gen_reads=greads),
                           "p_format": pfmt},
     }
     if not args.no_cpu_baseline:
         W = {k: v for k, v in inp.items()}
         try:
-            out["cpu_baseline"] = cpu_baseline(cfg, x_np, W)
+            out["cpu_baseline"] = cpu_baseline(cfg, x_np, W, link_mode=args.link)
         except Exception as e:   # the GPU figure stands on its own
             out["cpu_baseline"] = {"error": repr(e)}
     print(json.dumps(out), flush=True)
