@@ -53,6 +53,7 @@ SIGNATURES = [
                            _P, _L, _L, _P, _L, _L,
                            _P, _S, _P]),
     ("holo_quat_to_dense", _I, [_L, _I, _P, _P, _P]),
+    ("holo_add_layernorm_fwd", _I, [_L, _I, _I, _F, _P, _L, _P, _L, _P, _P, _P, _L, _P, _L, _P]),
     ("holo_decode_geom_fwd", _I, [_I, _I, _I, _L, _L, _I, _F, _I, _I,
                                   _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L,
                                   _P, _P, _P, _P, _P]),

@@ -277,6 +277,35 @@ int holo_attn_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale
   return HOLO_OK;
 }
 
+int holo_add_layernorm_fwd(int64_t n, int d, int dtype, float eps, const void* x, int64_t x_rs,
+                           const void* delta, int64_t delta_rs, const void* weight, const void* bias,
+                           void* h, int64_t h_rs, void* y, int64_t y_rs, void* stream) {
+  g_last_error.clear();
+  if (n < 0 || d <= 0) return fail(HOLO_ERR_BAD_SHAPE, "n must be >= 0 and d > 0");
+  if (dtype != HOLO_F32 && dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "dtype %d is not HOLO_F32 or HOLO_BF16", dtype);
+  const int64_t e16 = dtype == HOLO_F32 ? 4 : 8;       // elements per 16 bytes
+  if (d % e16 || d > 1024 * e16)
+    return fail(HOLO_ERR_UNSUPPORTED, "d = %d: must be a multiple of %d and at most %d for this dtype", d,
+                (int)e16, (int)(1024 * e16));
+  if (!(eps > 0.f)) return fail(HOLO_ERR_INVALID_ARG, "eps must be positive");
+  if (n == 0) return HOLO_OK;
+  if (!x || !delta || !weight || !bias || !h || !y) return fail(HOLO_ERR_INVALID_ARG, "null pointer");
+  for (const int64_t rs : {x_rs, delta_rs, h_rs, y_rs})
+    if (rs < d || rs % e16) return fail(HOLO_ERR_INVALID_ARG, "row strides must be >= d and 16-byte multiples");
+  if (!aligned16(x) || !aligned16(delta) || !aligned16(weight) || !aligned16(bias) || !aligned16(h) || !aligned16(y))
+    return fail(HOLO_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
+  holo::AddNormArgs a;
+  a.n = n; a.d = d; a.eps = eps;
+  a.x = x; a.x_rs = x_rs; a.delta = delta; a.delta_rs = delta_rs; a.w = weight; a.b = bias;
+  a.h = h; a.h_rs = h_rs; a.y = y; a.y_rs = y_rs;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = dtype == HOLO_F32 ? holo::launch_add_layernorm<float>(a, s)
+                                   : holo::launch_add_layernorm<holo::bf16>(a, s);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "add_layernorm launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
 int holo_quat_to_dense(int64_t n, int d, const float* quat, float* dense, void* stream) {
   g_last_error.clear();
   if (n < 0 || d <= 0) return fail(HOLO_ERR_BAD_SHAPE, "n must be >= 0 and d > 0");

@@ -84,7 +84,18 @@ struct DecodeAttnArgs {
   float* ws;                       // (B, H, nsplit, Dp + 2) partials
 };
 
+// residual add + LayerNorm over rows of d (d a multiple of 16 bytes, at most 1024 such chunks)
+struct AddNormArgs {
+  int64_t n; int d; float eps;
+  const void* x; int64_t x_rs;
+  const void* delta; int64_t delta_rs;
+  const void* w; const void* b;
+  void* h; int64_t h_rs;
+  void* y; int64_t y_rs;
+};
+
 template <typename IO, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
+template <typename T> hipError_t launch_add_layernorm(const AddNormArgs& a, hipStream_t s);
 template <typename IO, typename GT> hipError_t launch_decode_geom(const DecodeGeomArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_decode_attn(const DecodeAttnArgs& a, hipStream_t s);
 int64_t decode_splits(int64_t t);

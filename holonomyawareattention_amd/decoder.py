@@ -7,16 +7,21 @@ that block and its parameter names, so its state_dict keys match the
 reference's (`core.*`, `ln1.*`, `ln2.*`, `ff.0.*`, `ff.2.*`), and adds a
 decoder with an LM head for the full-model benchmark.
 
-The attention runs on the gfx950 kernels of `attention_kernel`; LayerNorm,
-GELU and the MLP GEMMs are PyTorch operators (hipBLASLt GEMMs with fused bias).
+The attention runs on the gfx950 kernels of `attention_kernel`. Outside
+autograd every residual add and the LayerNorm that follows it run as one
+gfx950 kernel (`kernels.add_layernorm`); GELU and the MLP GEMMs are PyTorch
+operators (hipBLASLt GEMMs with fused bias), and under autograd the norms and
+adds are too (their gradients are torch's).
 """
 from __future__ import annotations
 
-from typing import Dict, Tuple
+from typing import Dict, Optional, Tuple
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
+from . import kernels
 from .attention_kernel import PathOrderedGeometricMHA
 
 
@@ -32,8 +37,39 @@ class HoloBlock(nn.Module):
         self.ff = nn.Sequential(nn.Linear(d_model, 4 * d_model), nn.GELU(), nn.Linear(4 * d_model, d_model))
 
     def forward(self, h: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        if _fused_norms(self, h):
+            return self.forward_fused(h, _ln(self.ln1, h), mask, None)[0]
         h = h + self.core(self.ln1(h), attn_mask=mask, return_geometry=False)[0]
         return h + self.ff(self.ln2(h))
+
+    def forward_fused(self, h: torch.Tensor, a: torch.Tensor, mask: torch.Tensor,
+                      next_ln: Optional[nn.LayerNorm]) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """The block outside autograd, given a = ln1(h): each residual add runs
+        fused with the LayerNorm after it (this block's ln2, then `next_ln`, the
+        next block's ln1, when given). Returns (h_out, next_ln(h_out) or None)."""
+        c = self.core(a, attn_mask=mask, return_geometry=False)[0]
+        h, a = kernels.add_layernorm(h, c, self.ln2.weight, self.ln2.bias, self.ln2.eps)
+        f = self.ff(a)
+        if next_ln is None:
+            return h + f, None
+        return kernels.add_layernorm(h, f, next_ln.weight, next_ln.bias, next_ln.eps)
+
+
+def _ln(ln: nn.LayerNorm, h: torch.Tensor) -> torch.Tensor:
+    return F.layer_norm(h, ln.normalized_shape, ln.weight, ln.bias, ln.eps)
+
+
+def _fused_norms(mod: nn.Module, h: torch.Tensor) -> bool:
+    """The fused add + LayerNorm kernel serves calls outside autograd on the GPU
+    (fp32 / bf16 rows whose width it supports); under autograd torch's
+    differentiable ops run instead."""
+    if not h.is_cuda or h.dtype not in (torch.float32, torch.bfloat16):
+        return False
+    if torch.is_grad_enabled() and (h.requires_grad or any(p.requires_grad for p in mod.parameters())):
+        return False
+    e16 = 16 // h.element_size()
+    d = h.shape[-1]
+    return d % e16 == 0 and d <= 1024 * e16
 
 
 class HoloDecoder(nn.Module):
@@ -66,6 +102,12 @@ class HoloDecoder(nn.Module):
     def hidden(self, tokens: torch.Tensor) -> torch.Tensor:
         h = self.embed(tokens)
         mask = self.causal_mask(h.shape[1], h.device)
+        if len(self.blocks) and _fused_norms(self, h):
+            a = _ln(self.blocks[0].ln1, h)
+            for i, b in enumerate(self.blocks):
+                nxt = self.blocks[i + 1].ln1 if i + 1 < len(self.blocks) else None
+                h, a = b.forward_fused(h, a, mask, nxt)
+            return h
         for b in self.blocks:
             h = b(h, mask)
         return h

@@ -4,6 +4,7 @@
 ``attention``  -> holo_attn_fwd      : causal attention, back-rotation
 ``attention_backward`` -> holo_attn_bwd : gradients of both wrt q, k, v and the generator
 ``quat_to_dense`` -> holo_quat_to_dense
+``add_layernorm`` -> holo_add_layernorm_fwd : residual add + LayerNorm of the decoder stack
 
 Each wrapper checks devices, dtypes and strides on the host before the launch
 (the kernels index exactly what these shapes describe), allocates its outputs
@@ -298,3 +299,27 @@ def decode_attention(qh: torch.Tensor, kh_cache: torch.Tensor, vh_cache: torch.T
                                   workspace.numel() * workspace.element_size(), _stream(dev))
     _lib.check(rc, "holo_decode_attn_fwd")
     return out
+
+
+def add_layernorm(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                  eps: float = 1e-5) -> Tuple[torch.Tensor, torch.Tensor]:
+    """h = x + delta and y = LayerNorm(h) (weight, bias, eps over the last
+    dimension) in one pass: the residual add and the next norm of a pre-LN
+    decoder. Returns (h, y), both shaped like x."""
+    lib = _lib.load()
+    if x.shape != delta.shape or x.dtype != delta.dtype or x.dtype not in _DT or x.device.type != "cuda":
+        raise ValueError("add_layernorm: x and delta must be GPU tensors of one shape and dtype (fp32/bf16)")
+    d = int(x.shape[-1])
+    if tuple(weight.shape) != (d,) or tuple(bias.shape) != (d,) or weight.dtype != x.dtype or bias.dtype != x.dtype:
+        raise ValueError("add_layernorm: weight and bias must be (d,) tensors of x's dtype")
+    x2, d2 = x.reshape(-1, d), delta.reshape(-1, d)
+    if x2.stride(-1) != 1 or d2.stride(-1) != 1:
+        raise ValueError("add_layernorm: rows must be contiguous")
+    w, b = weight.contiguous(), bias.contiguous()
+    h = torch.empty_like(x2)
+    y = torch.empty_like(x2)
+    rc = lib.holo_add_layernorm_fwd(x2.shape[0], d, _DT[x.dtype], float(eps), _ptr(x2), x2.stride(0),
+                                    _ptr(d2), d2.stride(0), _ptr(w), _ptr(b), _ptr(h), h.stride(0),
+                                    _ptr(y), y.stride(0), _stream(x.device))
+    _lib.check(rc, "holo_add_layernorm_fwd")
+    return h.view_as(x), y.view_as(x)

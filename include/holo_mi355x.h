@@ -228,6 +228,21 @@ HOLO_API int holo_decode_attn_fwd(int B, int H, int d, int64_t t, int64_t capaci
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Residual add fused with LayerNorm (the decoder stack's norms; no counterpart
+ * in the reference's path ABI: it replaces the torch add and nn.LayerNorm of
+ * the pre-LN block, experiments/session_cherry.py:292-294):
+ *   h = x + delta  (rounded to dtype),  y = (h - mean) / sqrt(var + eps) * weight + bias
+ * over the last dimension d of n rows (biased variance, fp32 statistics of the
+ * rounded h). Rows at ptr[r * row_stride]; weight and bias have dtype `dtype`.
+ * d a multiple of 16 bytes of dtype and at most 1024 such chunks (bf16: 8192,
+ * fp32: 4096); row strides 16-byte multiples, pointers 16-byte aligned.
+ */
+HOLO_API int holo_add_layernorm_fwd(int64_t n, int d, int dtype, float eps,
+                           const void* x, int64_t x_row_stride, const void* delta, int64_t delta_row_stride,
+                           const void* weight, const void* bias,
+                           void* h, int64_t h_row_stride, void* y, int64_t y_row_stride, void* stream);
+
+/*
  * Expand fp32 quaternions (n, nb, 4) to dense fp32 rotation matrices (n, d, d):
  * block b on dims 3b..3b+2, identity on the leftover dims.
  */

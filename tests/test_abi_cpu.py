@@ -168,3 +168,26 @@ def test_decode_argument_validation(lib):
     assert f(1, 2, 12, 300, 320, 0, 0.3, 16, 16, 16, 16, 16, 24, 12, 16, 16, None) == _lib.HOLO_ERR_WORKSPACE
     assert f(1, 2, 12, 400, 320, 0, 0.3, 16, 16, 16, 16, 16, 24, 12, 16, need, None) == _lib.HOLO_ERR_BAD_SHAPE
     assert f(1, 2, 12, 3, 64, 0, 0.3, 16, 16, 16, 16, 16, 24, 4, 16, need, None) == _lib.HOLO_ERR_INVALID_ARG
+
+
+def _addln(lib, **kw):
+    a = dict(n=4, d=96, dt=_lib.HOLO_F32, eps=1e-5, x=16, xs=96, dl=16, ds=96, w=16, b=16, h=16, hs=96,
+             y=16, ys=96)
+    a.update(kw)
+    return lib.holo_add_layernorm_fwd(a["n"], a["d"], a["dt"], a["eps"], a["x"], a["xs"], a["dl"], a["ds"],
+                                      a["w"], a["b"], a["h"], a["hs"], a["y"], a["ys"], None)
+
+
+def test_add_layernorm_argument_validation(lib):
+    assert _addln(lib, n=0) == _lib.HOLO_OK                               # no rows: nothing launched
+    assert _addln(lib, n=-1) == _lib.HOLO_ERR_BAD_SHAPE
+    assert _addln(lib, d=0) == _lib.HOLO_ERR_BAD_SHAPE
+    assert _addln(lib, dt=7) == _lib.HOLO_ERR_INVALID_ARG
+    assert _addln(lib, d=98) == _lib.HOLO_ERR_UNSUPPORTED                 # not a 16-byte multiple (fp32)
+    assert _addln(lib, d=100, dt=_lib.HOLO_BF16, xs=104, ds=104, hs=104, ys=104) == _lib.HOLO_ERR_UNSUPPORTED
+    assert _addln(lib, d=4100, xs=4100, ds=4100, hs=4100, ys=4100) == _lib.HOLO_ERR_UNSUPPORTED   # > 4096 fp32
+    assert _addln(lib, eps=0.0) == _lib.HOLO_ERR_INVALID_ARG
+    assert _addln(lib, w=None) == _lib.HOLO_ERR_INVALID_ARG
+    assert _addln(lib, xs=90) == _lib.HOLO_ERR_INVALID_ARG                # stride below d
+    assert _addln(lib, ys=98) == _lib.HOLO_ERR_INVALID_ARG                # stride not a 16-byte multiple
+    assert _addln(lib, h=8) == _lib.HOLO_ERR_INVALID_ARG                  # misaligned
