@@ -25,7 +25,12 @@ all written from the reference's behaviour, not copied:
   golden fixtures at small sizes.
 * ``forward_arc_walk`` is the brute-force O(L^3) definition of
   ``core/attention.py:156-192`` (walk the ring arc j -> i composing edge
-  rotations), for tiny L.
+  rotations; inert mode: endpoint transport C_i^T C_j), any mask, for tiny L.
+* ``forward_exact_blocks`` / ``exact_attention64`` restate the reference's
+  exact path for every mode and mask (``kernel/attention_fast.py:84-166``,
+  which the reference's kernel module runs off its kernel path): the wrap
+  branch through Hol, the inert endpoint transport, -inf masking; fp64 on the
+  block structure.
 
 Pinning (every function has at least one independent check in tests/):
   skew_from_vec / block scatter / geometry / forward_chunked
@@ -34,6 +39,11 @@ Pinning (every function has at least one independent check in tests/):
   rodrigues -> torch.linalg.matrix_exp in fp64, G^T G = I, det = +1,
            exp(0)=I, exp(A)exp(-A)=I, small-angle series, angle pi;
   scan  -> brute-force products, P_0 = I, orthogonality;
+  forward_exact_blocks -> forward_arc_walk for causal and inert mode with no
+           mask, the ring mask (core/utils.py:59-75) and random masks;
+           forward_blocks under causal + tril; at edge_scale = 0 torch's
+           scaled_dot_product_attention with the same boolean mask (NaN rows
+           where a row allows nothing, as torch.softmax gives).
   forward_blocks -> forward_chunked (fp64), flat-connection reduction
            (edge_scale = 0 gives torch's causal scaled_dot_product_attention),
            gauge invariance, causal prefix consistency, forward_arc_walk.
@@ -300,6 +310,61 @@ def causal_attention64(qh: np.ndarray, kh: np.ndarray, vh: np.ndarray, scale: fl
     return out
 
 
+def ring_mask(T: int) -> np.ndarray:
+    """Local ring mask of core/utils.py:59-75: token i may attend to itself and
+    to its ring neighbours (i - 1) mod T and (i + 1) mod T (True = allowed)."""
+    m = np.zeros((T, T), dtype=bool)
+    i = np.arange(T)
+    m[i, i] = True
+    m[i, (i - 1) % T] = True
+    m[i, (i + 1) % T] = True
+    return m
+
+
+def exact_attention64(q: np.ndarray, k: np.ndarray, v: np.ndarray, P: np.ndarray, Hol: np.ndarray,
+                      scale: float, mask: Optional[np.ndarray] = None, mode: str = "causal") -> np.ndarray:
+    """Per-head outputs (B, H, T, d) of the reference's exact path for any
+    mask and mode (kernel/attention_fast.py:129-162, which
+    kernel/attention_kernel.py:211-213 runs for every call off the kernel
+    path), float64, on the block structure.
+
+    The reference transports key/value j to query i by G_arc[i, j] =
+    P_i P_j^T (i >= j) or P_i Hol P_j^T (i < j) in causal mode (:130-141) and
+    by P_i^T P_j in inert mode (:142-144), masks disallowed scores with -inf
+    (:154-157; a row with no allowed key gives NaN, as torch.softmax does) and
+    returns sum_j a_ij G_arc[i, j] v_j. In transported coordinates
+    (u^ = P^T u in causal mode, u' = P u in inert mode):
+      causal: s_ij = q^_i . (Hol k^_j if i < j else k^_j),
+              o_i  = P_i (sum_{j<=i} a_ij v^_j + Hol sum_{j>i} a_ij v^_j)
+      inert:  s_ij = q'_i . k'_j,   o_i = P_i^T sum_j a_ij v'_j
+    q, k, v (B, H, T, d); P (B, H, T, nb, 3, 3); Hol (B, H, nb, 3, 3);
+    mask (T, T) bool or None (everything allowed)."""
+    T = q.shape[-2]
+    allowed = np.ones((T, T), dtype=bool) if mask is None else np.asarray(mask, dtype=bool)
+    if mode == "causal":
+        qh, kh, vh = (apply_blocks_T(P, u) for u in (q, k, v))
+        Hb = Hol[:, :, None]                                  # broadcast over tokens
+        khw, vhw = apply_blocks(Hb, kh), apply_blocks(Hb, vh)
+        base = np.arange(T)[:, None] >= np.arange(T)[None, :]
+        s = np.where(base, np.einsum("...id,...jd->...ij", qh, kh),
+                     np.einsum("...id,...jd->...ij", qh, khw)) * scale
+    elif mode == "inert":
+        qh, kh, vh = (apply_blocks(P, u) for u in (q, k, v))
+        s = np.einsum("...id,...jd->...ij", qh, kh) * scale
+    else:
+        raise ValueError(mode)
+    s = np.where(allowed, s, -np.inf)
+    with np.errstate(invalid="ignore"):
+        s = s - s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p = p / p.sum(axis=-1, keepdims=True)
+    if mode == "causal":
+        oh = np.einsum("...ij,...jd->...id", np.where(base, p, 0.0), vh) + \
+            np.einsum("...ij,...jd->...id", np.where(base, 0.0, p), vhw)
+        return apply_blocks(P, oh)
+    return apply_blocks_T(P, np.einsum("...ij,...jd->...id", p, vh))
+
+
 def geometry_blocks(a: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
     """a (B,H,T,m_blk) -> P (B,H,T,nb,3,3) and Hol (B,H,nb,3,3), float64."""
     B, H, T, m = a.shape
@@ -333,6 +398,30 @@ def forward_blocks(x: np.ndarray, W: Dict[str, np.ndarray], n_heads: int,
     return y
 
 
+def forward_exact_blocks(x: np.ndarray, W: Dict[str, np.ndarray], n_heads: int, edge_scale: float,
+                         link_mode: str = "additive", mask: Optional[np.ndarray] = None,
+                         mode: str = "causal", a: Optional[np.ndarray] = None,
+                         return_parts: bool = False):
+    """float64 forward of the layer for any mask and mode (the reference's
+    exact path, kernel/attention_fast.py:84-166); with mode "causal" and a tril
+    mask it is forward_blocks."""
+    x = np.asarray(x, dtype=np.float64)
+    B, T, D = x.shape
+    H = n_heads
+    d = D // H
+    Wt = {k: torch.as_tensor(np.asarray(w, dtype=np.float64)) for k, w in W.items()}
+    xt = torch.as_tensor(x)
+    q, k, v = (t.numpy() for t in split_qkv(xt, Wt["qkv.weight"], H))
+    if a is None:
+        a = generator_params(xt, Wt, H, edge_scale, link_mode).numpy()
+    P, Hol = geometry_blocks(np.asarray(a, dtype=np.float64))
+    o = exact_attention64(q, k, v, P, Hol, 1.0 / math.sqrt(d), mask, mode)
+    y = o.transpose(0, 2, 1, 3).reshape(B, T, D) @ np.asarray(W["out.weight"], np.float64).T
+    if return_parts:
+        return y, dict(q=q, k=k, v=v, a=a, P=P, Hol=Hol, o=o)
+    return y
+
+
 def blocks_to_dense(Pb: np.ndarray, d: int) -> np.ndarray:
     """(..., nb, 3, 3) block rotations -> (..., d, d) with identity leftovers."""
     nb = Pb.shape[-3]
@@ -348,10 +437,15 @@ def blocks_to_dense(Pb: np.ndarray, d: int) -> np.ndarray:
 # brute-force definition (core/attention.py:156-192), tiny L only
 # --------------------------------------------------------------------------
 def forward_arc_walk(x: np.ndarray, W: Dict[str, np.ndarray], n_heads: int,
-                     edge_scale: float, link_mode: str = "additive") -> np.ndarray:
+                     edge_scale: float, link_mode: str = "additive", mask="tril",
+                     mode: str = "causal") -> np.ndarray:
     """Transport key/value j to query i by walking the ring arc j -> j+1 -> ...
     -> i with the edge rotations (crossing the closing edge when i < j), then
-    softmax over the allowed (tril) keys. float64, O(L^3)."""
+    softmax over the allowed keys. float64, O(L^3). `mask`: "tril" (default),
+    None (everything allowed) or a (T, T) bool array; a row with no allowed key
+    is NaN (softmax over -inf only). mode "inert" replaces the walk by the
+    endpoint transport C_i^T C_j of the prefix products C_t = G_{t-1}...G_0
+    (core/attention.py:150-167)."""
     x = np.asarray(x, dtype=np.float64)
     B, T, D = x.shape
     H = n_heads
@@ -361,23 +455,35 @@ def forward_arc_walk(x: np.ndarray, W: Dict[str, np.ndarray], n_heads: int,
     q, k, v = (t.numpy() for t in split_qkv(xt, Wt["qkv.weight"], H))
     a = generator_params(xt, Wt, H, edge_scale, link_mode).numpy()
     G = blocks_to_dense(rodrigues(a.reshape(B, H, T, -1, 3)), d)     # (B,H,T,d,d)
+    if isinstance(mask, str):
+        allowed = np.tril(np.ones((T, T), dtype=bool))
+    else:
+        allowed = np.ones((T, T), dtype=bool) if mask is None else np.asarray(mask, dtype=bool)
+    C = np.empty((B, H, T, d, d))
+    C[:, :, 0] = np.eye(d)
+    for t in range(T - 1):
+        C[:, :, t + 1] = G[:, :, t] @ C[:, :, t]
     out = np.zeros((B, H, T, d))
     for i in range(T):
         Kt = np.zeros((B, H, T, d))
         Vt = np.zeros((B, H, T, d))
         for j in range(T):
-            U = np.broadcast_to(np.eye(d), (B, H, d, d)).copy()
-            t = j
-            while t != i:
-                U = G[:, :, t] @ U
-                t = (t + 1) % T
+            if mode == "inert":
+                U = np.swapaxes(C[:, :, i], -1, -2) @ C[:, :, j]
+            else:
+                U = np.broadcast_to(np.eye(d), (B, H, d, d)).copy()
+                t = j
+                while t != i:
+                    U = G[:, :, t] @ U
+                    t = (t + 1) % T
             Kt[:, :, j] = np.einsum("bhdf,bhf->bhd", U, k[:, :, j])
             Vt[:, :, j] = np.einsum("bhdf,bhf->bhd", U, v[:, :, j])
         s = np.einsum("bhd,bhjd->bhj", q[:, :, i], Kt) / math.sqrt(d)
-        s[..., i + 1:] = -np.inf
-        s = s - s.max(-1, keepdims=True)
-        p = np.exp(s)
-        p /= p.sum(-1, keepdims=True)
+        s = np.where(allowed[i], s, -np.inf)
+        with np.errstate(invalid="ignore"):
+            s = s - s.max(-1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(-1, keepdims=True)
         out[:, :, i] = np.einsum("bhj,bhjd->bhd", p, Vt)
     return out.transpose(0, 2, 1, 3).reshape(B, T, D) @ np.asarray(W["out.weight"], np.float64).T
 
