@@ -28,6 +28,9 @@ HOLO_GEN_DIRECT = 1
 HOLO_QUAT_F32 = 0
 HOLO_QUAT_SNORM16 = 1
 
+HOLO_MODE_CAUSAL = 0
+HOLO_MODE_INERT = 1
+
 # (name, restype, argtypes) for every exported symbol of the header
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -40,10 +43,13 @@ SIGNATURES = [
     ("holo_padded_head_dim", _I, [_I]),
     ("holo_padded_seq_len", _L, [_L]),
     ("holo_geom_scan_workspace_size", _S, [_I, _L, _I, _I]),
-    ("holo_geom_scan_fwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I,
+    ("holo_geom_scan_fwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I, _I,
                                 _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L,
                                 _P, _P, _P, _P, _P, _P, _S, _P]),
     ("holo_attn_fwd", _I, [_I, _L, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _L, _L, _P, _P]),
+    ("holo_attn_masked_workspace_size", _S, [_I, _L, _I, _I, _I, _I, _I]),
+    ("holo_attn_masked_fwd", _I, [_I, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _L,
+                                  _P, _L, _L, _P, _S, _P]),
     ("holo_attn_bwd_workspace_size", _S, [_I, _L, _I, _I, _I]),
     ("holo_attn_bwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _F,
                            _P, _L, _L, _P, _L, _L,

@@ -19,16 +19,19 @@ the reference's row-major upper-triangle order (core/utils.py:20-26). Leftover
 dims (d mod 3) are not rotated. This is the reference's dense SO(d) model
 restricted to block-diagonal generators.
 
-The kernel path runs when mode == "causal", attn_mask is exactly tril(L),
-dropout is inactive and x is on the GPU (the conditions of
-kernel/attention_kernel.py:203-208; return_geometry is also supported).
-Anything else raises NotImplementedError, as the guarded reference does
-(kernel/attention_fast_chunked.py:106-114): there is no second code path.
+Dispatch follows the reference's kernel module (kernel/attention_kernel.py:
+203-213): mode == "causal" with attn_mask exactly tril(L) runs the causal
+kernels (holo_attn_fwd; return_geometry is also supported); every other call
+-- no mask, the ring mask or any (L, L) boolean mask, inert mode -- runs the
+exact-path kernels (holo_attn_masked_fwd), where the reference falls back to
+kernel/attention_fast.py. Both need x on the GPU and dropout inactive;
+anything else raises NotImplementedError (there is no CPU path).
 Under autograd the projections are ordinary differentiable torch GEMMs and the
 scan + attention core is one autograd function whose backward is the gfx950
 backward (holo_attn_bwd; the reference recomputes its forward under autograd,
-kernel/attention_kernel.py:174-187). The geometry output is not differentiable
-(return_geometry under autograd raises NotImplementedError).
+kernel/attention_kernel.py:174-187); that backward covers the causal + tril
+path, and other calls under autograd raise NotImplementedError. The geometry
+output is not differentiable (return_geometry under autograd raises).
 """
 from __future__ import annotations
 
@@ -146,29 +149,40 @@ class PathOrderedGeometricMHA(nn.Module):
 
     # ---- dispatch predicate (kernel/attention_kernel.py:203-208) ----
     def _unsupported_reason(self, x, attn_mask, causal_implied: bool = False) -> Optional[str]:
-        if self.mode != "causal":
-            return f"mode={self.mode!r} (only 'causal' runs on the kernel path)"
         if not x.is_cuda:
             return "input is not on the GPU"
         if self.dropout.p != 0.0 and self.training:
-            return "attention dropout is active (the kernel applies none)"
+            return "attention dropout is active (the kernels apply none)"
         if x.dtype not in (torch.float32, torch.bfloat16):
             return f"dtype {x.dtype} (float32 and bfloat16 are supported)"
         if self.link_mode not in ("additive", "interaction"):
             return f"link_mode={self.link_mode!r}"
-        if causal_implied:                    # prefill / decode: the causal mask is the definition
-            return None
+        if causal_implied:                    # prefill / decode: the causal tril path by definition
+            return None if self.mode == "causal" else f"mode={self.mode!r} (decode runs the causal mode)"
         L = x.shape[1]
-        key = None if attn_mask is None else (attn_mask.data_ptr(), attn_mask._version,
-                                              tuple(attn_mask.shape), attn_mask.device)
-        if key is None or key != self._mask_ok:
-            if not _is_exact_tril(attn_mask, L):
-                return "attn_mask is not exactly tril(L)"
-            self._mask_ok = key
+        if attn_mask is not None and (tuple(attn_mask.shape) != (L, L) or attn_mask.device != x.device):
+            return f"attn_mask must be an ({L}, {L}) tensor on {x.device}"
         return None
 
+    def _tril_path(self, attn_mask, L: int) -> bool:
+        """causal mode with attn_mask exactly tril(L): the reference's kernel
+        path (kernel/attention_kernel.py:203-208), here the causal kernels
+        with their fused backward. The check runs once per mask tensor."""
+        if self.mode != "causal" or attn_mask is None:
+            return False
+        key = (attn_mask.data_ptr(), attn_mask._version, tuple(attn_mask.shape), attn_mask.device)
+        if key == self._mask_ok:
+            return True
+        if not _is_exact_tril(attn_mask, L):
+            return False
+        self._mask_ok = key
+        return True
+
     def _kernel_supported(self, x, attn_mask, return_geometry=False) -> bool:
-        return self._unsupported_reason(x, attn_mask) is None
+        """The reference's dispatch predicate (kernel/attention_kernel.py:203-208):
+        True for calls on its kernel path (causal + tril, no dropout, GPU).
+        Every other GPU call runs the exact-path kernels (holo_attn_masked_fwd)."""
+        return self._unsupported_reason(x, attn_mask) is None and self._tril_path(attn_mask, x.shape[1])
 
     def _cat_weight(self, mods) -> torch.Tensor:
         """Row-concatenated weights of `mods` for one GEMM, rebuilt only when a
@@ -254,6 +268,7 @@ class PathOrderedGeometricMHA(nn.Module):
             raise NotImplementedError(
                 f"holonomyawareattention_amd kernel path does not support this call: {reason}")
         B, L, D = x.shape
+        tril = self._tril_path(attn_mask, L)
         params = [p for p in self.parameters() if p.requires_grad]
         track = torch.is_grad_enabled() and (x.requires_grad or bool(params))
         if track:
@@ -261,7 +276,13 @@ class PathOrderedGeometricMHA(nn.Module):
                 raise NotImplementedError(
                     "holonomyawareattention_amd kernel path does not support this call: "
                     "return_geometry under autograd (the geometry output is not differentiable)")
+            if not tril:
+                raise NotImplementedError(
+                    "holonomyawareattention_amd kernel path does not support this call: under autograd "
+                    "only causal mode with attn_mask == tril(L) (the fused backward's path) is supported")
             return self._forward_autograd(x), None
+        if not tril:
+            return self._forward_exact(x, attn_mask, return_geometry)
         ev = self._stage_events
         with torch.no_grad():
             if ev is not None:
@@ -285,6 +306,31 @@ class PathOrderedGeometricMHA(nn.Module):
         d = self.d
         C = kernels.quat_to_dense(P, d).to(x.dtype)
         Hm = kernels.quat_to_dense(hol, d).to(x.dtype)
+        return y, {"C": C, "H": Hm}
+
+    def _forward_exact(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor], return_geometry: bool
+                       ) -> Tuple[torch.Tensor, Optional[Dict[str, torch.Tensor]]]:
+        """Every call off the causal + tril path: any mask (None = every pair,
+        e.g. the ring mask of core/utils.py:59-75), causal mode (the wrap branch
+        through the holonomy) or inert mode, as the reference's kernel module
+        runs them on its exact path (kernel/attention_kernel.py:211-213 ->
+        kernel/attention_fast.py:129-166). Rows whose mask allows no key are NaN,
+        as there."""
+        B, L, D = x.shape
+        causal = self.mode == "causal"
+        with torch.no_grad():
+            q, k, v, gq, gk = self._link_inputs(x)
+            qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
+                                                     want_hol=causal or return_geometry,
+                                                     p_format=self._p_format(x, return_geometry),
+                                                     mode=self.mode)
+            o = kernels.attention_masked(qh, kh, vh_t, P, hol, self.d, self.scale, mode=self.mode,
+                                         mask=attn_mask)
+            y = F.linear(o.view(B, L, D), self.out.weight)
+        if not return_geometry:
+            return y, None
+        C = kernels.quat_to_dense(P, self.d).to(x.dtype)
+        Hm = kernels.quat_to_dense(hol, self.d).to(x.dtype)
         return y, {"C": C, "H": Hm}
 
     # ---- incremental decode (no counterpart in the reference) ----

@@ -81,7 +81,7 @@ extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (4 << 16) | 0; }
+int holo_abi_version(void) { return (5 << 16) | 0; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -93,7 +93,7 @@ size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d) {
 }
 
 int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
-                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype, int p_format,
+                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype, int p_format, int mode,
                        const void* gq, int64_t gq_rs, int64_t gq_hs,
                        const void* gk, int64_t gk_rs, int64_t gk_hs,
                        const void* q, int64_t q_rs, int64_t q_hs,
@@ -114,6 +114,8 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
     return fail(HOLO_ERR_INVALID_ARG, "gen_mode %d unknown", gen_mode);
   if (p_format != HOLO_QUAT_F32 && p_format != HOLO_QUAT_SNORM16)
     return fail(HOLO_ERR_INVALID_ARG, "p_format %d is not HOLO_QUAT_F32 or HOLO_QUAT_SNORM16", p_format);
+  if (mode != HOLO_MODE_CAUSAL && mode != HOLO_MODE_INERT)
+    return fail(HOLO_ERR_INVALID_ARG, "mode %d is not HOLO_MODE_CAUSAL or HOLO_MODE_INERT", mode);
   const int nb = d / 3;
   if (!gq || !q || !k || !v || !qh || !kh || !vh_t || (nb > 0 && !P))
     return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
@@ -147,6 +149,7 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
   a.v = v; a.v_rs = v_rs; a.v_hs = v_hs;
   a.qh = qh; a.kh = kh; a.vh_t = vh_t; a.P = P; a.hol = hol;
   a.p_format = p_format;
+  a.inert = mode == HOLO_MODE_INERT;
   {
     // 16-byte vector rows: every row start of gq/gk/k/v must be 16-byte aligned
     const size_t ge = gen_dtype == HOLO_F32 ? 4 : 2, ie = io_dtype == HOLO_F32 ? 4 : 2;
@@ -204,6 +207,75 @@ int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = dtype == HOLO_F32 ? holo::launch_attn<float>(a, s)
                                    : holo::launch_attn<holo::bf16>(a, s);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "attention launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+size_t holo_attn_masked_workspace_size(int B, int64_t T, int H, int d, int dtype, int mode, int has_mask) {
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || (dtype != HOLO_F32 && dtype != HOLO_BF16)) return 0;
+  const int64_t Tp = holo::padded_seq(T);
+  size_t n = 0;
+  if (mode == HOLO_MODE_CAUSAL)       // wrap queries Hol^T qh, (B, H, Tp, Dp)
+    n += ((size_t)B * H * Tp * holo::padded_head_dim(d) * (dtype == HOLO_F32 ? 4 : 2) + 255) / 256 * 256;
+  if (has_mask) n += (size_t)Tp * (Tp / 64) * 8;   // mask bits
+  return n;
+}
+
+int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, int mode, float scale,
+                         const void* qh, const void* kh, const void* vh_t, const void* P, const float* hol,
+                         const uint8_t* mask, int64_t mask_rs,
+                         void* o, int64_t o_rs, int64_t o_hs,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  int rc = check_common(B, T, H, d);
+  if (rc) return rc;
+  if (dtype != HOLO_F32 && dtype != HOLO_BF16)
+    return fail(HOLO_ERR_INVALID_ARG, "dtype %d is not HOLO_F32 or HOLO_BF16", dtype);
+  if (p_format != HOLO_QUAT_F32 && p_format != HOLO_QUAT_SNORM16)
+    return fail(HOLO_ERR_INVALID_ARG, "p_format %d is not HOLO_QUAT_F32 or HOLO_QUAT_SNORM16", p_format);
+  if (mode != HOLO_MODE_CAUSAL && mode != HOLO_MODE_INERT)
+    return fail(HOLO_ERR_INVALID_ARG, "mode %d is not HOLO_MODE_CAUSAL or HOLO_MODE_INERT", mode);
+  const int nb = d / 3;
+  if (!qh || !kh || !vh_t || !o || (nb > 0 && !P))
+    return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if (mode == HOLO_MODE_CAUSAL && nb > 0 && !hol)
+    return fail(HOLO_ERR_INVALID_ARG, "causal mode needs the holonomy (hol)");
+  if (mask && mask_rs < T)
+    return fail(HOLO_ERR_INVALID_ARG, "mask row stride %lld is below T = %lld", (long long)mask_rs, (long long)T);
+  if ((rc = check_layout("o", o_rs, o_hs, H, d))) return rc;
+  if (!aligned16(qh) || !aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)) || (hol && !aligned16(hol)))
+    return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t, P and hol must be 16-byte aligned");
+  if (!(scale > 0.f) || !(scale < 1e30f))
+    return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
+  const size_t need = holo_attn_masked_workspace_size(B, T, H, d, dtype, mode, mask != nullptr);
+  if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+    return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
+                need, workspace ? workspace_bytes : (size_t)0);
+
+  holo::MaskedArgs a;
+  a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d); a.mode = mode;
+  a.T = T; a.Tp = holo::padded_seq(T);
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.qh = qh; a.qhw = nullptr; a.kh = kh; a.vh_t = vh_t; a.P = P; a.hol = hol;
+  a.mask_bits = nullptr;
+  a.o = o; a.o_rs = o_rs; a.o_hs = o_hs;
+  a.p_format = p_format;
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  if (mode == HOLO_MODE_CAUSAL) {
+    a.qhw = ws;
+    ws += ((size_t)B * H * a.Tp * a.Dp * (dtype == HOLO_F32 ? 4 : 2) + 255) / 256 * 256;
+    e = dtype == HOLO_F32 ? holo::launch_wrap_queries<float>(a, const_cast<void*>(a.qhw), s)
+                          : holo::launch_wrap_queries<holo::bf16>(a, const_cast<void*>(a.qhw), s);
+    if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "wrap query launch: %s", hipGetErrorString(e));
+  }
+  if (mask) {
+    a.mask_bits = reinterpret_cast<const uint64_t*>(ws);
+    e = holo::launch_pack_mask(mask, mask_rs, T, a.Tp, reinterpret_cast<uint64_t*>(ws), s);
+    if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "mask packing launch: %s", hipGetErrorString(e));
+  }
+  e = dtype == HOLO_F32 ? holo::launch_attn_masked<float>(a, s) : holo::launch_attn_masked<holo::bf16>(a, s);
   if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "attention launch: %s", hipGetErrorString(e));
   return HOLO_OK;
 }

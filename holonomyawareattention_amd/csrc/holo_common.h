@@ -59,6 +59,9 @@ __device__ inline quat qmul(const quat& a, const quat& b) {
 
 __device__ inline quat qident() { return quat{1.f, 0.f, 0.f, 0.f}; }
 
+// conjugate: the rotation of conj(q) is R(q)^T
+__device__ inline quat qconj(const quat& q) { return quat{q.w, -q.x, -q.y, -q.z}; }
+
 // exp of the skew block A = [[0,a0,a1],[-a0,0,a2],[-a1,-a2,0]]. A is the cross-
 // product matrix of w = (-a2, a1, -a0), so exp(A) is the rotation by |w| about
 // w: quaternion (cos(th/2), sin(th/2)/th * w). Below th = 1e-4 the two

@@ -17,6 +17,7 @@ struct ScanArgs {
   void* qh; void* kh; void* vh_t; float* P; float* hol;
   int p_format;    // 0: fp32 quaternions, 1: int16 (round(32767 q/|q|))
   int wide;        // 16-byte row path of the scan (d in {48, 72, 96}, aligned rows)
+  int inert;       // transport u' = P u (inert mode) instead of u^ = P^T u
   float* incl;     // chained-scan state: chunk products (B, H, nch, nb, 4), then inclusive prefixes (same shape)
   unsigned* ticket;  // [0]: chunk ticket counter, [1]: carry-wait time-out flag
 };
@@ -32,6 +33,19 @@ struct AttnArgs {
   int p_format;    // 0: fp32 quaternions, 1: int16 (round(32767 q/|q|))
   float* lse;      // optional (B, H, Tp): log2 of each query's softmax normaliser, in the
                    // log2 units of scale_log2 (max + log2(sum)); what the backward recomputes P from
+};
+
+// Attention for any mask and either mode (the exact path): mode 0 causal, with
+// the wrap branch (key j > query i) through the holonomy; mode 1 inert.
+struct MaskedArgs {
+  int B, H, d, nb, Dp, mode;
+  int64_t T, Tp;
+  float scale_log2;
+  const void* qh; const void* qhw;       // qhw = Hol^T qh per block (causal mode)
+  const void* kh; const void* vh_t; const void* P; const float* hol;
+  const uint64_t* mask_bits;             // (Tp, Tp/64): bit e of word w = allowed(i, 64 w + e); null = all
+  void* o; int64_t o_rs, o_hs;
+  int p_format;
 };
 
 // Backward of scan + attention. Path-frame tensors are (B, H, Tp, Dp) row-major
@@ -96,6 +110,10 @@ struct AddNormArgs {
 
 template <typename IO, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_add_layernorm(const AddNormArgs& a, hipStream_t s);
+hipError_t launch_pack_mask(const uint8_t* mask, int64_t mask_rs, int64_t T, int64_t Tp, uint64_t* bits,
+                            hipStream_t s);
+template <typename T> hipError_t launch_wrap_queries(const MaskedArgs& a, void* qhw, hipStream_t s);
+template <typename T> hipError_t launch_attn_masked(const MaskedArgs& a, hipStream_t s);
 template <typename IO, typename GT> hipError_t launch_decode_geom(const DecodeGeomArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_decode_attn(const DecodeAttnArgs& a, hipStream_t s);
 int64_t decode_splits(int64_t t);

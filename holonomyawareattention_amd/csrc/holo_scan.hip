@@ -231,7 +231,8 @@ __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
       for (int j = 0; j < 3; ++j)
         if (c0 + j < a.d) { q3[j] = to_f32(qr[j]); k3[j] = to_f32(kr[j]); v3[j] = to_f32(vr[j]); }
       if (blk < nb) {
-        rot3 R = qmat(load_quat(&gs[(i * nb + blk) * 4]));
+        const quat pt = load_quat(&gs[(i * nb + blk) * 4]);
+        rot3 R = qmat(a.inert ? qconj(pt) : pt);          // R^T applied below: P^T u, or P u
         float y0, y1, y2;
         rot_t_apply(R, q3[0], q3[1], q3[2], y0, y1, y2);
         q3[0] = y0; q3[1] = y1; q3[2] = y2;
@@ -350,7 +351,8 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   chunk_prefix<GT>(a, gs, ss, cs, bh, c, tid);
   // ---- transport: kh row to global, vh into the transposed tile ----
   static_for<8>([&](auto j) {
-    rot3 R = qmat(load_quat(&gs[(i * NB + 8 * g + j) * 4]));
+    const quat pt = load_quat(&gs[(i * NB + 8 * g + j) * 4]);
+    rot3 R = qmat(a.inert ? qconj(pt) : pt);              // R^T applied below: P^T u, or P u
     float y0, y1, y2;
     rot_t_apply(R, qv[3 * j], qv[3 * j + 1], qv[3 * j + 2], y0, y1, y2);
     qv[3 * j] = y0; qv[3 * j + 1] = y1; qv[3 * j + 2] = y2;

@@ -2,6 +2,7 @@
 
 ``geom_scan``  -> holo_geom_scan_fwd : link rotations, prefix products, qh/kh/vh
 ``attention``  -> holo_attn_fwd      : causal attention, back-rotation
+``attention_masked`` -> holo_attn_masked_fwd : any mask, causal (wrap through Hol) or inert mode
 ``attention_backward`` -> holo_attn_bwd : gradients of both wrt q, k, v and the generator
 ``quat_to_dense`` -> holo_quat_to_dense
 ``add_layernorm`` -> holo_add_layernorm_fwd : residual add + LayerNorm of the decoder stack
@@ -21,6 +22,7 @@ from . import _lib
 _DT = {torch.float32: _lib.HOLO_F32, torch.bfloat16: _lib.HOLO_BF16}
 # storage of P: name -> (holo_quat_format, torch dtype of the (B, H, T, nb, 4) tensor)
 _PFMT = {"f32": (_lib.HOLO_QUAT_F32, torch.float32), "snorm16": (_lib.HOLO_QUAT_SNORM16, torch.int16)}
+_MODE = {"causal": _lib.HOLO_MODE_CAUSAL, "inert": _lib.HOLO_MODE_INERT}
 
 
 def _ptr(t: Optional[torch.Tensor]):
@@ -59,7 +61,7 @@ def padded_seq_len(T: int) -> int:
 
 def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor,
               gk: Optional[torch.Tensor], edge_scale: float, want_hol: bool = False,
-              p_format: str = "f32"
+              p_format: str = "f32", mode: str = "causal"
               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """q, k, v: (B,T,H,d) views; gq, gk: (B,T,H,3*nb) views (gk None: gq is the
     full link parameter g and a_t = edge_scale * g_t). The generator may be
@@ -67,7 +69,8 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     Returns qh, kh (B,H,Tp,Dp), vh_t (B,H,Tp/64,Dp,64), P (B,H,T,nb,4) and
     Hol (B,H,nb,4) fp32 or None. P is fp32 quaternions (p_format "f32") or
     round(32767 q/|q|) as int16 ("snorm16", half the bytes; the attention
-    epilogue uses either, quat_to_dense takes fp32)."""
+    epilogue uses either, quat_to_dense takes fp32). mode "causal" transports
+    u^ = P^T u, "inert" u' = P u (for attention_masked in inert mode)."""
     lib = _lib.load()
     B, T, H, d = k.shape
     nb = d // 3
@@ -97,13 +100,15 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     vh_t = torch.empty((B, H, Tp // 64, Dp, 64), dtype=dt, device=dev)
     if p_format not in _PFMT:
         raise ValueError(f"geom_scan: p_format must be one of {sorted(_PFMT)}")
+    if mode not in _MODE:
+        raise ValueError(f"geom_scan: mode must be one of {sorted(_MODE)}")
     P = torch.empty((B, H, T, nb, 4), dtype=_PFMT[p_format][1], device=dev)
     hol = torch.empty((B, H, nb, 4), dtype=torch.float32, device=dev) if want_hol else None
     ws_bytes = int(lib.holo_geom_scan_workspace_size(B, T, H, d))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     rc = lib.holo_geom_scan_fwd(
         B, T, H, d, _lib.HOLO_GEN_DIRECT if gk is None else _lib.HOLO_GEN_ADDITIVE,
-        float(edge_scale), _DT[dt], _DT[gdt], _PFMT[p_format][0],
+        float(edge_scale), _DT[dt], _DT[gdt], _PFMT[p_format][0], _MODE[mode],
         _ptr(gq), gq_rs, gq_hs, _ptr(gk), gk_rs, gk_hs,
         _ptr(q), q_rs, q_hs, _ptr(k), k_rs, k_hs, _ptr(v), v_rs, v_hs,
         _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(hol),
@@ -153,6 +158,57 @@ def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.T
                            _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
                            _ptr(out), o_rs, o_hs, _ptr(lse), _stream(dev))
     _lib.check(rc, "holo_attn_fwd")
+    return out
+
+
+def attention_masked(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
+                     hol: Optional[torch.Tensor], d: int, scale: float, mode: str = "causal",
+                     mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention for any mask and either mode (the reference's exact path):
+    qh, kh, vh_t, P from geom_scan in the same `mode`; hol (B, H, nb, 4) fp32
+    (the scan's holonomy, needed in causal mode); mask (T, T) bool (True =
+    allowed) or None (every pair allowed). A row that allows no key is NaN.
+    Returns o as a (B,T,H,d) tensor, or writes `out`."""
+    lib = _lib.load()
+    if mode not in _MODE:
+        raise ValueError(f"attention_masked: mode must be one of {sorted(_MODE)}")
+    if P.dim() != 5:
+        raise ValueError("attention_masked: P must be (B, H, T, nb, 4)")
+    B, H, T = (int(n) for n in P.shape[:3])
+    nb = d // 3
+    dev, dt = qh.device, qh.dtype
+    if dev.type != "cuda" or dt not in _DT:
+        raise ValueError(f"attention_masked: qh must be a float32/bfloat16 GPU tensor (got {dt} on {dev})")
+    Dp, Tp = padded_head_dim(d), padded_seq_len(T)
+    for name, t, shape in (("qh", qh, (B, H, Tp, Dp)), ("kh", kh, (B, H, Tp, Dp)),
+                           ("vh_t", vh_t, (B, H, Tp // 64, Dp, 64))):
+        if tuple(t.shape) != shape or not t.is_contiguous() or t.dtype != dt or t.device != dev:
+            raise ValueError(f"attention_masked: {name} does not match the geom_scan layout")
+    pf = {torch.float32: _lib.HOLO_QUAT_F32, torch.int16: _lib.HOLO_QUAT_SNORM16}.get(P.dtype)
+    if tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous() or pf is None or P.device != dev:
+        raise ValueError("attention_masked: P does not match the geom_scan layout")
+    if mode == "causal" and nb:
+        if hol is None or tuple(hol.shape) != (B, H, nb, 4) or hol.dtype != torch.float32 \
+                or not hol.is_contiguous() or hol.device != dev:
+            raise ValueError("attention_masked: causal mode needs hol, a contiguous fp32 (B, H, nb, 4) tensor")
+    m8, m_rs = None, 0
+    if mask is not None:
+        if tuple(mask.shape) != (T, T) or mask.device != dev:
+            raise ValueError(f"attention_masked: mask must be ({T}, {T}) on {dev}")
+        m8 = mask.to(torch.bool).contiguous().view(torch.uint8)
+        m_rs = T
+    if out is None:
+        out = torch.empty((B, T, H, d), dtype=dt, device=dev)
+    elif out.dtype != dt or out.device != dev:
+        raise ValueError("attention_masked: out must match q's dtype and device")
+    o_rs, o_hs = _token_view(out, B, T, H, d, "out")
+    ws_bytes = int(lib.holo_attn_masked_workspace_size(B, T, H, d, _DT[dt], _MODE[mode], int(mask is not None)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    rc = lib.holo_attn_masked_fwd(B, T, H, d, _DT[dt], pf, _MODE[mode], float(scale),
+                                  _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
+                                  _ptr(hol) if mode == "causal" else None, _ptr(m8), m_rs,
+                                  _ptr(out), o_rs, o_hs, _ptr(ws), ws_bytes, _stream(dev))
+    _lib.check(rc, "holo_attn_masked_fwd")
     return out
 
 

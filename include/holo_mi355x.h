@@ -14,6 +14,9 @@
  *                       causal online-softmax attention on the transported
  *                       queries/keys/values and the back-rotation
  *                       out_i = P_i o_i (core/attention_fast_chunked.py:119-171);
+ *   holo_attn_masked_fwd replaces the reference's exact path for every other
+ *                       call (any mask, inert mode: kernel/attention_fast.py:
+ *                       129-166, reached from kernel/attention_kernel.py:211-213);
  *   holo_quat_to_dense  expands the stored rotations to the reference's dense
  *                       geometry tensors {"C": P, "H": Hol}
  *                       (core/attention_fast_chunked.py:175-177);
@@ -87,6 +90,15 @@ typedef enum holo_gen_mode {
   HOLO_GEN_DIRECT = 1
 } holo_gen_mode;
 
+/* Attention mode (PathOrderedGeometricMHA(mode=...), core/attention.py:31-40). */
+typedef enum holo_mode {
+  /* arc transport: key j reaches query i along the ring arc j -> i, through
+     the closing edge (the holonomy) when i < j                              */
+  HOLO_MODE_CAUSAL = 0,
+  /* endpoint transport P_i^T P_j (the holonomy never enters)                */
+  HOLO_MODE_INERT = 1
+} holo_mode;
+
 /* Message for the last failing call on this thread ("" if none). */
 HOLO_API const char* holo_last_error(void);
 
@@ -113,6 +125,10 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  *   q, k, v: dtype `io_dtype`.
  *   q      : like k, v.
  *            element (b, t, h, c) at ptr[(b*T + t)*row_stride + h*head_stride + c], c < d.
+ *   mode   : HOLO_MODE_CAUSAL transports u^ = P^T u (the written formulas);
+ *            HOLO_MODE_INERT transports u' = P u instead (the endpoint
+ *            transport of inert mode, kernel/attention_fast.py:142-144), for
+ *            holo_attn_masked_fwd in that mode.
  * Outputs:
  *   qh   (B, H, Tp, Dp)        io_dtype, qh[t] = P_t^T q_t   (Tp = padded T, Dp = padded d)
  *   kh   (B, H, Tp, Dp)        io_dtype, kh[t] = P_t^T k_t
@@ -130,7 +146,7 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  * calls that share one workspace must not run concurrently.
  */
 HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
-                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype, int p_format,
+                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype, int p_format, int mode,
                        const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
                        const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
                        const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -155,6 +171,34 @@ HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_form
                   const void* qh, const void* kh, const void* vh_t, const void* P,
                   void* o, int64_t o_row_stride, int64_t o_head_stride,
                   float* lse, void* stream);
+
+/* Workspace bytes of holo_attn_masked_fwd (has_mask: a mask will be passed). */
+HOLO_API size_t holo_attn_masked_workspace_size(int B, int64_t T, int H, int d, int dtype, int mode,
+                                                int has_mask);
+
+/*
+ * Path-ordered attention for any mask and either mode: the reference's exact
+ * path (kernel/attention_fast.py:129-166), which its kernel module runs for
+ * every call that is not causal + exactly tril(T) (kernel/attention_kernel.py:
+ * 203-213), e.g. no mask, the ring mask (core/utils.py:59-75) or inert mode.
+ *   mode HOLO_MODE_CAUSAL: qh, kh, vh_t from holo_geom_scan_fwd in that mode,
+ *     hol required:
+ *       s_ij = scale * qh_i . (Hol kh_j if i < j else kh_j)
+ *       o_i  = P_i (sum_{j<=i} a_ij vh_j + Hol sum_{j>i} a_ij vh_j)
+ *   mode HOLO_MODE_INERT: qh, kh, vh_t from the scan in inert mode (u' = P u),
+ *     hol unused:
+ *       s_ij = scale * qh_i . kh_j,   o_i = P_i^T sum_j a_ij vh_j
+ *   a_ij = softmax_j over the allowed keys; mask (T, T), element (i, j) at
+ *   mask[i * mask_row_stride + j], nonzero = allowed, NULL = every pair
+ *   allowed. Disallowed scores are -inf, so a row that allows no key is NaN
+ *   (as torch.softmax gives). Workspace: holo_attn_masked_workspace_size
+ *   bytes (the wrap queries Hol^T qh and the mask as bits), filled by the call.
+ */
+HOLO_API int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, int mode, float scale,
+                         const void* qh, const void* kh, const void* vh_t, const void* P, const float* hol,
+                         const uint8_t* mask, int64_t mask_row_stride,
+                         void* o, int64_t o_row_stride, int64_t o_head_stride,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes of holo_attn_bwd. */
 HOLO_API size_t holo_attn_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype);

@@ -58,12 +58,12 @@ def test_version_and_layout_queries(lib):
 
 def _scan(lib, **kw):
     args = dict(B=1, T=8, H=2, d=12, gen=0, es=0.1, io=_lib.HOLO_F32, gdt=_lib.HOLO_F32, pf=_lib.HOLO_QUAT_F32,
-                gq=16, gk=16, q=16, k=16, v=16, qh=16, kh=16, vh=16, P=16, hol=None, ws=16, wsb=1 << 20,
+                mode=_lib.HOLO_MODE_CAUSAL, gq=16, gk=16, q=16, k=16, v=16, qh=16, kh=16, vh=16, P=16, hol=None, ws=16, wsb=1 << 20,
                 rs=64, hs=24)
     args.update(kw)
     a = args
     return lib.holo_geom_scan_fwd(a["B"], a["T"], a["H"], a["d"], a["gen"], a["es"], a["io"], a["gdt"], a["pf"],
-                                  a["gq"], a["rs"], a["hs"], a["gk"], a["rs"], a["hs"],
+                                  a["mode"], a["gq"], a["rs"], a["hs"], a["gk"], a["rs"], a["hs"],
                                   a["q"], a["rs"], a["hs"], a["k"], a["rs"], a["hs"], a["v"], a["rs"], a["hs"],
                                   a["qh"], a["kh"], a["vh"], a["P"], a["hol"], a["ws"], a["wsb"], None)
 
@@ -74,6 +74,7 @@ def test_scan_argument_validation(lib):
     assert _scan(lib, d=200) == _lib.HOLO_ERR_UNSUPPORTED
     assert _scan(lib, io=7) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, pf=2) == _lib.HOLO_ERR_INVALID_ARG
+    assert _scan(lib, mode=2) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, io=_lib.HOLO_F32, gdt=_lib.HOLO_BF16) == _lib.HOLO_ERR_UNSUPPORTED
     assert _scan(lib, k=None) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, gen=_lib.HOLO_GEN_ADDITIVE, gk=None) == _lib.HOLO_ERR_INVALID_ARG
@@ -191,3 +192,33 @@ def test_add_layernorm_argument_validation(lib):
     assert _addln(lib, xs=90) == _lib.HOLO_ERR_INVALID_ARG                # stride below d
     assert _addln(lib, ys=98) == _lib.HOLO_ERR_INVALID_ARG                # stride not a 16-byte multiple
     assert _addln(lib, h=8) == _lib.HOLO_ERR_INVALID_ARG                  # misaligned
+
+
+def _masked(lib, **kw):
+    a = dict(B=1, T=8, H=2, d=12, dt=_lib.HOLO_F32, pf=_lib.HOLO_QUAT_F32, mode=_lib.HOLO_MODE_CAUSAL, sc=0.3,
+             qh=16, kh=16, vh=16, P=16, hol=16, mask=16, mrs=8, o=16, rs=24, hs=12, ws=16, wsb=1 << 20)
+    a.update(kw)
+    return lib.holo_attn_masked_fwd(a["B"], a["T"], a["H"], a["d"], a["dt"], a["pf"], a["mode"], a["sc"],
+                                    a["qh"], a["kh"], a["vh"], a["P"], a["hol"], a["mask"], a["mrs"],
+                                    a["o"], a["rs"], a["hs"], a["ws"], a["wsb"], None)
+
+
+def test_masked_attention_argument_validation(lib):
+    ws = lib.holo_attn_masked_workspace_size
+    # causal: the wrap queries (B*H*Tp*Dp, 256-byte rounded), then Tp * Tp/64 mask words
+    assert ws(2, 100, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_CAUSAL, 1) == \
+        (2 * 3 * 128 * 64 * 2 + 255) // 256 * 256 + 128 * 2 * 8
+    assert ws(2, 100, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_INERT, 0) == 0
+    assert ws(2, 100, 3, 48, 9, _lib.HOLO_MODE_INERT, 0) == 0
+    assert _masked(lib, T=0) == _lib.HOLO_ERR_BAD_SHAPE
+    assert _masked(lib, d=120) == _lib.HOLO_ERR_UNSUPPORTED
+    assert _masked(lib, mode=2) == _lib.HOLO_ERR_INVALID_ARG
+    assert _masked(lib, dt=3) == _lib.HOLO_ERR_INVALID_ARG
+    assert _masked(lib, pf=5) == _lib.HOLO_ERR_INVALID_ARG
+    assert _masked(lib, hol=None) == _lib.HOLO_ERR_INVALID_ARG            # causal mode needs the holonomy
+    assert _masked(lib, mrs=7) == _lib.HOLO_ERR_INVALID_ARG               # mask rows shorter than T
+    assert _masked(lib, hs=4) == _lib.HOLO_ERR_INVALID_ARG                # output heads overlap
+    assert _masked(lib, kh=8) == _lib.HOLO_ERR_INVALID_ARG                # misaligned
+    assert _masked(lib, sc=0.0) == _lib.HOLO_ERR_INVALID_ARG
+    assert _masked(lib, wsb=64) == _lib.HOLO_ERR_WORKSPACE
+    assert _masked(lib, ws=None) == _lib.HOLO_ERR_WORKSPACE

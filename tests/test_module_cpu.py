@@ -40,10 +40,26 @@ def test_exact_tril_predicate():
     assert _is_exact_tril(tril.int(), T)
 
 
+def test_dispatch_between_tril_and_exact_paths():
+    """causal + exactly tril(L) is the reference's kernel path
+    (kernel/attention_kernel.py:203-208); every other mask or mode goes to the
+    exact-path kernels (its kernel/attention_fast.py fallback)."""
+    T = 9
+    tril = torch.ones(T, T, dtype=torch.bool).tril()
+    ring = tril.clone(); ring[0, T - 1] = True
+    causal = PathOrderedGeometricMHA(24, n_heads=2)
+    inert = PathOrderedGeometricMHA(24, n_heads=2, mode="inert")
+    assert causal._tril_path(tril, T)
+    assert causal._tril_path(tril, T)                     # cached by tensor identity
+    assert not causal._tril_path(None, T) and not causal._tril_path(ring, T)
+    assert not inert._tril_path(tril, T)
+
+
 @pytest.mark.parametrize("kind", ["cpu", "inert", "nomask", "ring", "dropout", "dtype"])
 def test_unsupported_calls_raise(kind):
-    """No second code path: everything outside the kernel conditions raises,
-    as the guarded reference does (kernel/attention_fast_chunked.py:106-114)."""
+    """No CPU path and no dropout: such calls raise NotImplementedError (the
+    guarded reference's exception, kernel/attention_fast_chunked.py:106-114)
+    whatever the mask and mode."""
     T = 6
     m = PathOrderedGeometricMHA(24, n_heads=2, mode="inert" if kind == "inert" else "causal",
                                 dropout=0.1 if kind == "dropout" else 0.0)
