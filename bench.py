@@ -464,6 +464,11 @@ def main():
     ap.add_argument("--link", default="additive", choices=["additive", "interaction"],
                     help="link generator of the layer (the reference module's default is interaction; the "
                          "configured workloads use the additive one)")
+    ap.add_argument("--mask", default="tril", choices=["tril", "none", "ring"],
+                    help="attention mask of the layer: tril (the configured workloads, the causal kernels) or, "
+                         "on the exact-path kernels, none / the ring mask of core/utils.py:59-75")
+    ap.add_argument("--mode", default="causal", choices=["causal", "inert"],
+                    help="attention mode (inert runs the exact-path kernels with any mask)")
     ap.add_argument("--train", action="store_true",
                     help="forward + backward of one layer at --config (one JSON line) and exit")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
@@ -502,7 +507,7 @@ def main():
 
     inp = synth.layer_inputs(2, B, T, D, H, args.link)
     x_np = inp.pop("x")
-    m = PathOrderedGeometricMHA(D, n_heads=H, edge_scale=es)
+    m = PathOrderedGeometricMHA(D, n_heads=H, edge_scale=es, mode=args.mode)
     m.link_mode = args.link
     with torch.no_grad():
         for k, p in m.state_dict().items():
@@ -513,7 +518,18 @@ def main():
     if args.ortho:
         print(json.dumps(orthogonality_report(m, x, args.config, kernels, torch)))
         return
-    mask = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
+    if args.mask == "tril":
+        mask = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
+        pairs = T * (T + 1) // 2
+    elif args.mask == "ring":
+        i = torch.arange(T, device=dev)
+        mask = torch.zeros(T, T, dtype=torch.bool, device=dev)
+        for off in (-1, 0, 1):
+            mask[i, (i + off) % T] = True
+        pairs = int(mask.sum())
+    else:
+        mask, pairs = None, T * T
+    exact = not m._tril_path(mask, T)
 
     pfmt = m._p_format(x, False)
     qbytes = 8 if pfmt == "snorm16" else 16
@@ -553,7 +569,7 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     tokens = B * T
     m_total = H * m.m_dim
-    fl_core = attention_core_flops(B, T, H, d)
+    fl_core = 4.0 * d * pairs * B * H          # QK^T and PV over the allowed (i, j) pairs
     if args.link == "additive":
         fl_proj = projection_flops(B, T, D, m_total)
     else:                                   # qkv + out, and the edge MLP 2D -> 4D -> H*m
@@ -578,19 +594,22 @@ def main():
         "vs_baseline": None,
         "dtype": cfg["dtype"],
         "data": "synthetic (seeded SplitMix64/Box-Muller: x ~ N(0,1), weights ~ N(0,1/d_model))",
-        "config": {"workload": f"{args.config}: one path-ordered attention layer forward",
+        "config": {"workload": f"{args.config}: one path-ordered attention layer forward"
+                               + (f" ({args.mode} mode, mask {args.mask}: exact-path kernels)" if exact else ""),
                    "global_batch": B, "seq_len": T, "n_heads": H, "d_head": d, "d_model": D,
                    "rotation": f"{d // 3} SO(3) blocks per head", "link_mode": args.link,
+                   "mode": args.mode, "mask": args.mask,
                    "edge_scale": es, "parallelism": "single GPU"},
         "layer_tflops": (fl_core + fl_proj) / (ms_per_step * 1e-3) / 1e12,
         "stages_ms": {"projections": stage_ms[0], "geom_scan": stage_ms[1],
                       "attention_core": stage_ms[2], "out_projection": stage_ms[3],
                       "sum": float(stage_ms.sum())},
-        "roofline": {"kernel": "attn_fwd (holo_attn_fwd)", "bound": "mfma",
+        "roofline": {"kernel": ("attn_masked + wrap_queries + pack_mask (holo_attn_masked_fwd)" if exact
+                                else "attn_fwd (holo_attn_fwd)"), "bound": "mfma",
                      "achieved": core_tflops, "peak": core_peak, "unit": "TFLOP/s",
                      "frac": core_tflops / core_peak,
-                     "traffic": traffic_from_profile(args.config, ["attn_fwd"]),
-                     "work_per_launch": f"{fl_core:.4e} FLOP = 2*d*T*(T+1)*B*H"},
+                     "traffic": None if exact else traffic_from_profile(args.config, ["attn_fwd"]),
+                     "work_per_launch": f"{fl_core:.4e} FLOP = 4*d*(allowed pairs {pairs})*B*H"},
         "roofline_scan": {"kernels": "scan_reset + chunk_apply (holo_geom_scan_fwd)",
                           "bound": "hbm", "achieved": scan_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": scan_gbs / PEAK_HBM_GBS,
@@ -601,7 +620,7 @@ def main():
                                                                             gen_reads=greads),
                           "p_format": pfmt},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not exact:
         W = {k: v for k, v in inp.items()}
         try:
             out["cpu_baseline"] = cpu_baseline(cfg, x_np, W, link_mode=args.link)

@@ -318,15 +318,26 @@ class PathOrderedGeometricMHA(nn.Module):
         as there."""
         B, L, D = x.shape
         causal = self.mode == "causal"
+        ev = self._stage_events
         with torch.no_grad():
+            if ev is not None:
+                ev[0].record()
             q, k, v, gq, gk = self._link_inputs(x)
+            if ev is not None:
+                ev[1].record()
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
                                                      want_hol=causal or return_geometry,
                                                      p_format=self._p_format(x, return_geometry),
                                                      mode=self.mode)
+            if ev is not None:
+                ev[2].record()
             o = kernels.attention_masked(qh, kh, vh_t, P, hol, self.d, self.scale, mode=self.mode,
                                          mask=attn_mask)
+            if ev is not None:
+                ev[3].record()
             y = F.linear(o.view(B, L, D), self.out.weight)
+            if ev is not None:
+                ev[4].record()
         if not return_geometry:
             return y, None
         C = kernels.quat_to_dense(P, self.d).to(x.dtype)

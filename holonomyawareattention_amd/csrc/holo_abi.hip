@@ -215,9 +215,8 @@ size_t holo_attn_masked_workspace_size(int B, int64_t T, int H, int d, int dtype
   if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || (dtype != HOLO_F32 && dtype != HOLO_BF16)) return 0;
   const int64_t Tp = holo::padded_seq(T);
   size_t n = 0;
-  if (mode == HOLO_MODE_CAUSAL)       // wrap queries Hol^T qh, (B, H, Tp, Dp)
-    n += ((size_t)B * H * Tp * holo::padded_head_dim(d) * (dtype == HOLO_F32 ? 4 : 2) + 255) / 256 * 256;
-  if (has_mask) n += (size_t)Tp * (Tp / 64) * 8;   // mask bits
+  if (has_mask)                       // mask bits, then the map of open tiles
+    n += (size_t)Tp * (Tp / 64) * 8 + (size_t)((T + 127) / 128) * (Tp / 64);
   return n;
 }
 
@@ -256,23 +255,19 @@ int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format
   a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d); a.mode = mode;
   a.T = T; a.Tp = holo::padded_seq(T);
   a.scale_log2 = scale * 1.4426950408889634f;
-  a.qh = qh; a.qhw = nullptr; a.kh = kh; a.vh_t = vh_t; a.P = P; a.hol = hol;
+  a.qh = qh; a.kh = kh; a.vh_t = vh_t; a.P = P; a.hol = hol;
   a.mask_bits = nullptr;
+  a.tile_act = nullptr;
   a.o = o; a.o_rs = o_rs; a.o_hs = o_hs;
   a.p_format = p_format;
   char* ws = static_cast<char*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
-  if (mode == HOLO_MODE_CAUSAL) {
-    a.qhw = ws;
-    ws += ((size_t)B * H * a.Tp * a.Dp * (dtype == HOLO_F32 ? 4 : 2) + 255) / 256 * 256;
-    e = dtype == HOLO_F32 ? holo::launch_wrap_queries<float>(a, const_cast<void*>(a.qhw), s)
-                          : holo::launch_wrap_queries<holo::bf16>(a, const_cast<void*>(a.qhw), s);
-    if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "wrap query launch: %s", hipGetErrorString(e));
-  }
   if (mask) {
     a.mask_bits = reinterpret_cast<const uint64_t*>(ws);
-    e = holo::launch_pack_mask(mask, mask_rs, T, a.Tp, reinterpret_cast<uint64_t*>(ws), s);
+    a.tile_act = reinterpret_cast<const uint8_t*>(ws + (size_t)a.Tp * (a.Tp / 64) * 8);
+    e = holo::launch_pack_mask(mask, mask_rs, T, a.Tp, reinterpret_cast<uint64_t*>(ws),
+                               const_cast<uint8_t*>(a.tile_act), s);
     if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "mask packing launch: %s", hipGetErrorString(e));
   }
   e = dtype == HOLO_F32 ? holo::launch_attn_masked<float>(a, s) : holo::launch_attn_masked<holo::bf16>(a, s);

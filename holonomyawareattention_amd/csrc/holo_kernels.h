@@ -41,9 +41,10 @@ struct MaskedArgs {
   int B, H, d, nb, Dp, mode;
   int64_t T, Tp;
   float scale_log2;
-  const void* qh; const void* qhw;       // qhw = Hol^T qh per block (causal mode)
+  const void* qh;
   const void* kh; const void* vh_t; const void* P; const float* hol;
   const uint64_t* mask_bits;             // (Tp, Tp/64): bit e of word w = allowed(i, 64 w + e); null = all
+  const uint8_t* tile_act;               // (ceil(T/128), Tp/64): 1 = the tile pair has an allowed pair
   void* o; int64_t o_rs, o_hs;
   int p_format;
 };
@@ -111,8 +112,7 @@ struct AddNormArgs {
 template <typename IO, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_add_layernorm(const AddNormArgs& a, hipStream_t s);
 hipError_t launch_pack_mask(const uint8_t* mask, int64_t mask_rs, int64_t T, int64_t Tp, uint64_t* bits,
-                            hipStream_t s);
-template <typename T> hipError_t launch_wrap_queries(const MaskedArgs& a, void* qhw, hipStream_t s);
+                            uint8_t* tile_act, hipStream_t s);
 template <typename T> hipError_t launch_attn_masked(const MaskedArgs& a, hipStream_t s);
 template <typename IO, typename GT> hipError_t launch_decode_geom(const DecodeGeomArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_decode_attn(const DecodeAttnArgs& a, hipStream_t s);

@@ -205,10 +205,10 @@ def _masked(lib, **kw):
 
 def test_masked_attention_argument_validation(lib):
     ws = lib.holo_attn_masked_workspace_size
-    # causal: the wrap queries (B*H*Tp*Dp, 256-byte rounded), then Tp * Tp/64 mask words
-    assert ws(2, 100, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_CAUSAL, 1) == \
-        (2 * 3 * 128 * 64 * 2 + 255) // 256 * 256 + 128 * 2 * 8
-    assert ws(2, 100, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_INERT, 0) == 0
+    # with a mask: Tp * Tp/64 mask words and the ceil(T/128) x Tp/64 map of open tiles
+    assert ws(2, 100, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_CAUSAL, 1) == 128 * 2 * 8 + 1 * 2
+    assert ws(2, 300, 3, 48, _lib.HOLO_F32, _lib.HOLO_MODE_INERT, 1) == 320 * 5 * 8 + 3 * 5
+    assert ws(2, 100, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_CAUSAL, 0) == 0
     assert ws(2, 100, 3, 48, 9, _lib.HOLO_MODE_INERT, 0) == 0
     assert _masked(lib, T=0) == _lib.HOLO_ERR_BAD_SHAPE
     assert _masked(lib, d=120) == _lib.HOLO_ERR_UNSUPPORTED
@@ -222,3 +222,4 @@ def test_masked_attention_argument_validation(lib):
     assert _masked(lib, sc=0.0) == _lib.HOLO_ERR_INVALID_ARG
     assert _masked(lib, wsb=64) == _lib.HOLO_ERR_WORKSPACE
     assert _masked(lib, ws=None) == _lib.HOLO_ERR_WORKSPACE
+    assert _masked(lib, mask=None, ws=None, wsb=0, T=0) == _lib.HOLO_ERR_BAD_SHAPE   # no mask: no workspace
