@@ -64,5 +64,27 @@ def build_library(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+C_SMOKE_SRC = os.path.join(REPO, "tests", "c", "abi_smoke.c")
+C_SMOKE_BIN = os.path.join(PKG, "_build", "abi_smoke")
+
+
+def build_c_smoke() -> str:
+    """Compile the C caller of the ABI (tests/c/abi_smoke.c) with gcc against
+    the HIP runtime and this library (no PyTorch); returns the binary's path."""
+    os.makedirs(os.path.dirname(C_SMOKE_BIN), exist_ok=True)
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no C compiler found for the ABI smoke driver")
+    cmd = [cc, "-std=c99", "-O2", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+           "-I/opt/rocm/include", "-I", os.path.join(REPO, "include"), C_SMOKE_SRC, "-o", C_SMOKE_BIN,
+           "-L", PKG, "-lholo_mi355x", "-L/opt/rocm/lib", "-lamdhip64", "-lm", "-Wl,-rpath," + PKG,
+           "-Wl,-rpath,$ORIGIN/.."]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"C ABI smoke driver failed to build:\n{r.stderr[-4000:]}")
+    return C_SMOKE_BIN
+
+
 if __name__ == "__main__":
     print(build_library(verbose="-v" in sys.argv))
+    print(build_c_smoke())
