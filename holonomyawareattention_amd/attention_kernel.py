@@ -218,10 +218,28 @@ class PathOrderedGeometricMHA(nn.Module):
             gk = g[..., H * m:].view(B, L, H, m)
         else:
             qkv = F.linear(x, self.qkv.weight).view(B, L, H, 3 * d)
-            pair = torch.cat([x, torch.roll(x, shifts=-1, dims=1)], dim=-1)
-            gq = self._edge_params(pair).view(B, L, H, m)        # a_t = es * g_t
-            gk = None
+            hid = self.edge_mlp[1](self.edge_mlp[0](self._pairs(x))).reshape(B * L, 4 * D)
+            lin2 = self.edge_mlp[2]
+            if x.dtype == torch.float32:
+                gq = F.linear(hid, lin2.weight).view(B, L, H, m)
+            else:
+                gq = torch.mm(hid, lin2.weight.t(), out_dtype=torch.float32).view(B, L, H, m)
+            if lin2.bias is not None:   # a_t = es * (g_t + bias): the scan adds the bias per head
+                gk = lin2.bias.detach().float().view(1, 1, H, m).expand(B, L, H, m)
+            else:
+                gk = None
         return qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], gq, gk
+
+    @staticmethod
+    def _pairs(x: torch.Tensor) -> torch.Tensor:
+        """[x_t ; x_{(t+1) mod L}] (B, L, 2D), the edge MLP's input
+        (core/attention_fast_chunked.py:74-75), written in two copies."""
+        B, L, D = x.shape
+        pair = torch.empty((B, L, 2 * D), dtype=x.dtype, device=x.device)
+        pair[..., :D] = x
+        pair[:, :L - 1, D:] = x[:, 1:]
+        pair[:, L - 1, D:] = x[:, 0]
+        return pair
 
     def _edge_params(self, pair: torch.Tensor) -> torch.Tensor:
         """Interaction generator on (..., 2D) pairs [x_t ; x_{t+1}]

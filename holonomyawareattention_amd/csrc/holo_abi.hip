@@ -125,7 +125,9 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
     return fail(HOLO_ERR_INVALID_ARG, "direct generator takes no gk");
   if (nb > 0) {
     if ((rc = check_layout("gq", gq_rs, gq_hs, H, 3 * nb))) return rc;
-    if (gk && (rc = check_layout("gk", gk_rs, gk_hs, H, 3 * nb))) return rc;
+    // gk row stride 0: one row for every token (a per-head constant)
+    if (gk && (rc = check_layout("gk", gk_rs == 0 ? (int64_t)(H - 1) * gk_hs + 3 * nb : gk_rs, gk_hs, H, 3 * nb)))
+      return rc;
   }
   if ((rc = check_layout("q", q_rs, q_hs, H, d))) return rc;
   if ((rc = check_layout("k", k_rs, k_hs, H, d))) return rc;

@@ -35,12 +35,15 @@ def _stream(dev: torch.device) -> int:
 
 def _token_view(t: torch.Tensor, B: int, T: int, H: int, width: int, name: str):
     """(B, T, H, width) view with unit inner stride and row-major (b, t) rows.
-    Returns (row_stride, head_stride) in elements."""
+    Returns (row_stride, head_stride) in elements (row stride 0: one row
+    broadcast to every token, strides (0, 0, hs, 1))."""
     if t.dim() != 4 or tuple(t.shape) != (B, T, H, width):
         raise ValueError(f"{name}: expected shape {(B, T, H, width)}, got {tuple(t.shape)}")
     sb, st, sh, sc = t.stride()
     if width > 1 and sc != 1:
         raise ValueError(f"{name}: needs unit inner stride (strides {t.stride()})")
+    if sb == 0 and st == 0:
+        return 0, (sh if H > 1 else width)
     hs = sh if H > 1 else width
     if T > 1:
         rs = st
@@ -64,7 +67,8 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
               p_format: str = "f32", mode: str = "causal"
               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """q, k, v: (B,T,H,d) views; gq, gk: (B,T,H,3*nb) views (gk None: gq is the
-    full link parameter g and a_t = edge_scale * g_t). The generator may be
+    full link parameter g and a_t = edge_scale * g_t; gk with strides
+    (0, 0, m, 1): a per-head constant, a_t = edge_scale * (gq_t + gk)). The generator may be
     fp32 with bf16 q/k/v (link parameters are composed in fp32 either way).
     Returns qh, kh (B,H,Tp,Dp), vh_t (B,H,Tp/64,Dp,64), P (B,H,T,nb,4) and
     Hol (B,H,nb,4) fp32 or None. P is fp32 quaternions (p_format "f32") or
@@ -93,6 +97,8 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     k_rs, k_hs = _token_view(k, B, T, H, d, "k")
     v_rs, v_hs = _token_view(v, B, T, H, d, "v")
     gq_rs, gq_hs = _token_view(gq, B, T, H, 3 * nb, "gq")
+    if gq_rs == 0:
+        raise ValueError("geom_scan: gq must have one row per token")
     gk_rs, gk_hs = (0, 0) if gk is None else _token_view(gk, B, T, H, 3 * nb, "gk")
     Dp, Tp = padded_head_dim(d), padded_seq_len(T)
     qh = torch.empty((B, H, Tp, Dp), dtype=dt, device=dev)

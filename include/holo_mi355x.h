@@ -122,6 +122,10 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  *            at ptr[(b*T + t)*row_stride + h*head_stride + j], j < 3*nb.
  *            In HOLO_GEN_DIRECT mode gk must be NULL. Link parameters are
  *            accumulated and composed in fp32 whatever their storage type.
+ *            A gk row stride of 0 reads the same row for every token: with
+ *            HOLO_GEN_ADDITIVE that gives a_t = edge_scale * (gq_t + c) for a
+ *            per-head constant c (e.g. the interaction edge MLP's output bias,
+ *            with gq its unbiased output).
  *   q, k, v: dtype `io_dtype`.
  *   q      : like k, v.
  *            element (b, t, h, c) at ptr[(b*T + t)*row_stride + h*head_stride + c], c < d.
