@@ -22,7 +22,7 @@ struct ScanArgs {
   unsigned* ticket;  // [0]: chunk ticket counter, [1]: carry-wait time-out flag
 };
 size_t scan_state_bytes(int B, int64_t T, int H, int d);
-constexpr int kScanGroup = 16;   // chunks per carry-chain hop of the scan when the chain lags
+constexpr int kScanGroup = 8;    // chunks per carry-chain hop of the scan when the chain lags
 
 struct AttnArgs {
   int B, H, d, nb, Dp;

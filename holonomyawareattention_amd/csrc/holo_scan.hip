@@ -16,7 +16,7 @@
 //      block) and the chunk product T_c, published at once; the product of
 //      all earlier chunks C_c = incl[c-1], read from the previous chunk when
 //      it has published it, otherwise composed as T_{c-1} ... T_{c0}
-//      incl[c0-1] from the products of the earlier chunks of its group of 16
+//      incl[c0-1] from the products of the earlier chunks of its group of 8
 //      (c0 = 16 floor(c/16)) and the group boundary's prefix, so a lagging
 //      chain advances one group per hop instead of one chunk; then
 //      incl[c] = T_c C_c is published (a chained scan through the workspace);
