@@ -21,10 +21,12 @@
 //                 tile-transposed), delta, and the other operand layouts the
 //                 MFMA kernels read (qh_t, kh_t, vh row-major)
 //   attn_bwd_dkdv one workgroup per (b, h, 128 keys); each wave keeps its 32
-//                 keys' K and V rows as MFMA operands in registers and sweeps
-//                 the causal query tiles: S, dP, then dV += Pm^T dO and
-//                 dK += dS^T Q with the probabilities already in the operand
-//                 layout of the second product
+//                 keys' V rows as MFMA operands in registers (the K rows of
+//                 the workgroup's keys sit in LDS) and sweeps the causal query
+//                 tiles, the next fill's loads in flight while the current one
+//                 is computed: S, dP, then dV += Pm^T dO and dK += dS^T Q with
+//                 the probabilities already in the operand layout of the
+//                 second product
 //   attn_bwd_dq   one workgroup per (b, h, 128 queries), each wave 32 queries
 //                 in registers, sweeping key tiles: dQ^T += K^T dS^T
 //   link_bwd      chained suffix scan over 64-token chunks (reverse ticket
@@ -210,6 +212,7 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
   using M = typename TileCopy<T, DP, kFillKV>::template Multi<2, 2>;
   __shared__ __align__(16) T tiles[M::kElems];   // Q, dO (row-major), Q^T, dO^T
   __shared__ float lse_s[kFillKV], del_s[kFillKV];
+  __shared__ __align__(16) T Kw[128 * C::RS];      // the workgroup's 128 key rows (B operand of S = Q K^T)
   const T* const Qs = tiles;
   const T* const dOs = tiles + M::kRowTile;
   const T* const QTs = tiles + 2 * M::kRowTile;
@@ -221,44 +224,54 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
   const int64_t k0 = kb * 128, kw0 = k0 + 32 * w;
   const bool wave_in = kw0 < a.T;
 
-  // this wave's 32 keys: K and V rows as B operands (key = lane % 32)
-  frag_t kf[C::QF], vf[C::QF];
+  // this wave's 32 keys: V rows as B operands in registers (key = lane % 32),
+  // the K rows of all 128 keys in LDS
+  frag_t vf[C::QF];
   {
     const bool in = kw0 < a.Tp;
-    const T* krow = reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + kw0 + lr) * DP;
     const T* vrow = reinterpret_cast<const T*>(a.vh) + (bh * a.Tp + kw0 + lr) * DP;
     static_for<C::QF>([&](auto s) {
-      if constexpr (kBF) {
-        kf[s] = in ? *reinterpret_cast<const bf16x8*>(krow + 16 * s + 8 * g) : bf16x8{};
-        vf[s] = in ? *reinterpret_cast<const bf16x8*>(vrow + 16 * s + 8 * g) : bf16x8{};
-      } else {
-        kf[s] = in ? krow[2 * s + g] : 0.f;
-        vf[s] = in ? vrow[2 * s + g] : 0.f;
-      }
+      if constexpr (kBF) vf[s] = in ? *reinterpret_cast<const bf16x8*>(vrow + 16 * s + 8 * g) : bf16x8{};
+      else vf[s] = in ? vrow[2 * s + g] : 0.f;
     });
+    constexpr int E = C::E, RCH = DP / E;
+    for (int i = tid; i < 128 * RCH; i += kBwdThreads) {
+      const int r = i / RCH, cc = i % RCH;
+      const bool rin = k0 + r < a.Tp;
+      const u32x4 v = rin ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + k0 + r) * DP + cc * E)
+                          : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&Kw[r * C::RS + cc * E]) = v;
+    }
   }
   f32x16 dK[DP / 32], dV[DP / 32];
   static_for<DP / 32>([&](auto i) { dK[i] = f32x16{}; dV[i] = f32x16{}; });
   const float cl = a.scale_log2;
   const int64_t key = kw0 + lr;
   const int nfill = (int)((a.T + kFillKV - 1) / kFillKV);
-  for (int qf = (int)(k0 / kFillKV); qf < nfill; ++qf) {
+  const int qf0 = (int)(k0 / kFillKV);
+  // fill qf+1 is loaded into registers while fill qf is computed from LDS
+  u32x4 r[M::IT];
+  float ls = INFINITY, dl = 0.f;
+  auto load_fill = [&](int qf) {
     const int64_t q0 = (int64_t)qf * kFillKV;
-    {
-      u32x4 r[M::IT];
-      const int64_t tile = (bh * a.nch + q0 / kChunk) * DP * kChunk;
-      const T* const rows[2] = {reinterpret_cast<const T*>(a.qh) + (bh * a.Tp + q0) * DP,
-                                reinterpret_cast<const T*>(a.doh) + (bh * a.Tp + q0) * DP};
-      const T* const cols[2] = {reinterpret_cast<const T*>(a.qh_t) + tile, reinterpret_cast<const T*>(a.doh_t) + tile};
-      M::load(r, rows, cols, (int)(q0 % kChunk), tid);
-      const bool qin = tid < kFillKV && q0 + tid < a.T;
-      const float ls = qin ? a.lse[bh * a.Tp + q0 + tid] : INFINITY;
-      const float dl = qin ? a.delta[bh * a.Tp + q0 + tid] : 0.f;
-      __syncthreads();                      // the previous fill is consumed
-      M::store(tiles, r, tid);
-      if (tid < kFillKV) { lse_s[tid] = ls; del_s[tid] = dl; }
-      __syncthreads();
-    }
+    const int64_t tile = (bh * a.nch + q0 / kChunk) * DP * kChunk;
+    const T* const rows[2] = {reinterpret_cast<const T*>(a.qh) + (bh * a.Tp + q0) * DP,
+                              reinterpret_cast<const T*>(a.doh) + (bh * a.Tp + q0) * DP};
+    const T* const cols[2] = {reinterpret_cast<const T*>(a.qh_t) + tile, reinterpret_cast<const T*>(a.doh_t) + tile};
+    M::load(r, rows, cols, (int)(q0 % kChunk), tid);
+    const bool qin = tid < kFillKV && q0 + tid < a.T;
+    ls = qin ? a.lse[bh * a.Tp + q0 + tid] : INFINITY;
+    dl = qin ? a.delta[bh * a.Tp + q0 + tid] : 0.f;
+  };
+  auto store_fill = [&]() {
+    M::store(tiles, r, tid);
+    if (tid < kFillKV) { lse_s[tid] = ls; del_s[tid] = dl; }
+  };
+  if (qf0 < nfill) { load_fill(qf0); store_fill(); }
+  __syncthreads();
+  for (int qf = qf0; qf < nfill; ++qf) {
+    const int64_t q0 = (int64_t)qf * kFillKV;
+    if (qf + 1 < nfill) load_fill(qf + 1);
     static_for<kFillKV / kBT>([&](auto sub) {
       const int64_t qs0 = q0 + kBT * sub;
       if (!wave_in || qs0 + kBT - 1 < kw0) return;    // no query of the tile sees these keys
@@ -270,10 +283,11 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
         if constexpr (kBF) {
           const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&Qs[(ro + lr) * C::RS + 16 * s + 8 * g]);
           const bf16x8 da = *reinterpret_cast<const bf16x8*>(&dOs[(ro + lr) * C::RS + 16 * s + 8 * g]);
-          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, kf[s], S, 0, 0, 0);
+          const bf16x8 kb = *reinterpret_cast<const bf16x8*>(&Kw[(32 * w + lr) * C::RS + 16 * s + 8 * g]);
+          S = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qa, kb, S, 0, 0, 0);
           dP = __builtin_amdgcn_mfma_f32_32x32x16_bf16(da, vf[s], dP, 0, 0, 0);
         } else {
-          S = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[(ro + lr) * C::RS + 2 * s + g], kf[s], S, 0, 0, 0);
+          S = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[(ro + lr) * C::RS + 2 * s + g], Kw[(32 * w + lr) * C::RS + 2 * s + g], S, 0, 0, 0);
           dP = __builtin_amdgcn_mfma_f32_32x32x2f32(dOs[(ro + lr) * C::RS + 2 * s + g], vf[s], dP, 0, 0, 0);
         }
       });
@@ -314,6 +328,9 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
         });
       }
     });
+    __syncthreads();                        // every wave is done with this fill
+    if (qf + 1 < nfill) store_fill();
+    __syncthreads();
   }
   if (kw0 < a.Tp) {
     static_for<DP / 32>([&](auto db) {
