@@ -48,10 +48,12 @@ int check_common(int B, int64_t T, int H, int d) {
   return HOLO_OK;
 }
 
-// Backward workspace, each region 256-byte aligned: doh, doh_t, qh_t, kh_t,
-// vh (io dtype, B*H*Tp*Dp each), delta (fp32, B*H*Tp), dqh, dkh, dvh (fp32,
-// B*H*Tp*Dp each), the chained suffix sums (fp32, B*H*nch*nb*4) and the
-// ticket counter / time-out flag. Returns the total; fills `a` when given.
+// Backward workspace, each region 256-byte aligned: doh, vh and, for fp32
+// only, doh_t, qh_t, kh_t (io dtype, B*H*Tp*Dp each; the bf16 kernels read
+// the transposed operands from row-major LDS tiles), delta (fp32, B*H*Tp),
+// dqh, dkh, dvh (fp32, B*H*Tp*Dp each), the chained suffix sums (fp32,
+// B*H*nch*nb*4) and the ticket counter / time-out flag. Returns the total;
+// fills `a` when given.
 size_t bwd_layout(int B, int64_t T, int H, int d, size_t es, void* base, holo::BwdArgs* a) {
   const int64_t Tp = holo::padded_seq(T), nch = Tp / holo::kChunk;
   const size_t n = (size_t)B * H * Tp * holo::padded_head_dim(d);
@@ -62,7 +64,7 @@ size_t bwd_layout(int B, int64_t T, int H, int d, size_t es, void* base, holo::B
     return base ? static_cast<char*>(base) + at : nullptr;
   };
   void* r[5];
-  for (auto& p : r) p = take(n * es);
+  for (int i = 0; i < 5; ++i) r[i] = (es == 2 && i >= 1 && i <= 3) ? nullptr : take(n * es);
   float* delta = reinterpret_cast<float*>(take((size_t)B * H * Tp * 4));
   float* g[3];
   for (auto& p : g) p = reinterpret_cast<float*>(take(n * 4));

@@ -17,9 +17,11 @@
 //      The closing edge only enters the holonomy (zero gradient).
 //
 // Kernels, in launch order:
-//   bwd_prep      one workgroup per (b, h, 64 tokens): doh (row-major and
-//                 tile-transposed), delta, and the other operand layouts the
-//                 MFMA kernels read (qh_t, kh_t, vh row-major)
+//   bwd_prep      one workgroup per (b, h, 64 tokens): doh, delta, vh
+//                 row-major and, for fp32 only, the transposed operand
+//                 layouts doh_t, qh_t, kh_t (the bf16 MFMA kernels read their
+//                 transposed operands from row-major LDS tiles with
+//                 ds_read_b64_tr_b16)
 //   attn_bwd_dkdv one workgroup per (b, h, 128 keys); each wave keeps its 32
 //                 keys' V rows as MFMA operands in registers (the K rows of
 //                 the workgroup's keys sit in LDS) and sweeps the causal query
@@ -58,6 +60,26 @@ template <typename T> struct frag;
 template <> struct frag<bf16> { typedef bf16x8 type; };
 template <> struct frag<float> { typedef float type; };
 
+// A 32x32x16 bf16 MFMA operand whose k index runs over the rows of a row-major
+// LDS tile (row stride RS): lane l gets column col0 + l % 32 at rows
+// row0 + 4 (l / 32) + {0..3} and row0 + 8 + 4 (l / 32) + {0..3}, the k order
+// of an accumulator used as the other operand. ds_read_b64_tr_b16 hands lane i
+// of each 16-lane group element i % 4 of the 4-element reads of lanes
+// i / 4 + {0, 4, 8, 12}; source lane r of group G reads row
+// row0 + 4 (G / 2) + r / 4, columns col0 + 16 (G % 2) + 4 (r % 4) + {0..3}, so
+// lane i receives column col0 + 16 (G % 2) + i at four consecutive rows.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+template <int RS>
+__device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int row0, int col0, int lane) {
+  const int G = lane >> 4, r = lane & 15;
+  const int row = row0 + 4 * (G >> 1) + (r >> 2), col = col0 + 16 * (G & 1) + 4 * (r & 3);
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + row * RS + col));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + (row + 8) * RS + col));
+  const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo), h4 = __builtin_bit_cast(bf16x4, hi);
+  return bf16x8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+}
+
 // Cooperative copies of ROWS-row / ROWS-column tiles into LDS. All of a
 // thread's global loads are issued before its LDS stores (one memory round
 // trip per tile, not one per chunk).
@@ -71,7 +93,7 @@ template <typename T, int DP, int ROWS = kFill> struct TileCopy {
   struct Multi {
     static constexpr int N = NR * RN + NT * TN;
     static constexpr int IT = (N + kBwdThreads - 1) / kBwdThreads;
-    static __device__ __forceinline__ void load(u32x4 (&r)[IT], const T* const (&rows)[NR], const T* const (&cols)[NT],
+    static __device__ __forceinline__ void load(u32x4 (&r)[IT], const T* const (&rows)[NR], const T* const* cols,
                                                 int j0, int tid) {
       static_for<IT>([&](auto it) {
         const int f = tid + kBwdThreads * it;
@@ -173,7 +195,6 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_prep(BwdArgs a) {
   __syncthreads();
   // doh rows and doh transposed tile
   T* dohr = reinterpret_cast<T*>(a.doh) + (bh * a.Tp + c * kChunk) * DP;
-  T* doht = reinterpret_cast<T*>(a.doh_t) + (bh * a.nch + c) * DP * kChunk;
   for (int i = tid; i < kChunk * (DP / E); i += kBwdThreads) {
     const int r = i / (DP / E), cc = i % (DP / E);
     u32x4 raw;
@@ -181,17 +202,22 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_prep(BwdArgs a) {
     static_for<E>([&](auto k) { e[k] = from_f32<T>(Ds[r][cc * E + k]); });
     *reinterpret_cast<u32x4*>(&dohr[(int64_t)r * DP + cc * E]) = raw;
   }
-  for (int i = tid; i < DP * (kChunk / E); i += kBwdThreads) {
-    const int r = i / (kChunk / E), cc = i % (kChunk / E);
-    u32x4 raw;
-    T* e = reinterpret_cast<T*>(&raw);
-    static_for<E>([&](auto k) { e[k] = from_f32<T>(Ds[cc * E + k][r]); });
-    *reinterpret_cast<u32x4*>(&doht[(int64_t)r * kChunk + cc * E]) = raw;
-  }
-  // the other operand layouts
   const int64_t row0 = (bh * a.Tp + c * kChunk) * DP, tile0 = (bh * a.nch + c) * DP * kChunk;
-  transpose_tile<T, DP, false>(Ts, reinterpret_cast<const T*>(a.qh) + row0, reinterpret_cast<T*>(a.qh_t) + tile0, tid);
-  transpose_tile<T, DP, false>(Ts, reinterpret_cast<const T*>(a.kh) + row0, reinterpret_cast<T*>(a.kh_t) + tile0, tid);
+  if constexpr (sizeof(T) == 4) {
+    // fp32 MFMA operands read the transposed layouts doh_t, qh_t, kh_t (bf16
+    // reads them from the row-major tiles with transposing LDS reads)
+    T* doht = reinterpret_cast<T*>(a.doh_t) + (bh * a.nch + c) * DP * kChunk;
+    for (int i = tid; i < DP * (kChunk / E); i += kBwdThreads) {
+      const int r = i / (kChunk / E), cc = i % (kChunk / E);
+      u32x4 raw;
+      T* e = reinterpret_cast<T*>(&raw);
+      static_for<E>([&](auto k) { e[k] = from_f32<T>(Ds[cc * E + k][r]); });
+      *reinterpret_cast<u32x4*>(&doht[(int64_t)r * kChunk + cc * E]) = raw;
+    }
+    transpose_tile<T, DP, false>(Ts, reinterpret_cast<const T*>(a.qh) + row0, reinterpret_cast<T*>(a.qh_t) + tile0, tid);
+    transpose_tile<T, DP, false>(Ts, reinterpret_cast<const T*>(a.kh) + row0, reinterpret_cast<T*>(a.kh_t) + tile0, tid);
+  }
+  // vh row-major from the forward's transposed tiles
   transpose_tile<T, DP, true>(Ts, reinterpret_cast<const T*>(a.vh_t) + tile0, reinterpret_cast<T*>(a.vh) + row0, tid);
 }
 
@@ -209,8 +235,10 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
   using C = BwdCfg<T, DP, kFillKV>;
   typedef typename frag<T>::type frag_t;
   constexpr bool kBF = sizeof(T) == 2;
-  using M = typename TileCopy<T, DP, kFillKV>::template Multi<2, 2>;
-  __shared__ __align__(16) T tiles[M::kElems];   // Q, dO (row-major), Q^T, dO^T
+  // Q and dO row-major; fp32 also loads the transposed tiles Q^T, dO^T (bf16
+  // reads the transposed operands from the row-major tiles, tr_operand)
+  using M = typename TileCopy<T, DP, kFillKV>::template Multi<2, kBF ? 0 : 2>;
+  __shared__ __align__(16) T tiles[M::kElems];
   __shared__ float lse_s[kFillKV], del_s[kFillKV];
   __shared__ __align__(16) T Kw[128 * C::RS];      // the workgroup's 128 key rows (B operand of S = Q K^T)
   const T* const Qs = tiles;
@@ -257,7 +285,8 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
     const int64_t tile = (bh * a.nch + q0 / kChunk) * DP * kChunk;
     const T* const rows[2] = {reinterpret_cast<const T*>(a.qh) + (bh * a.Tp + q0) * DP,
                               reinterpret_cast<const T*>(a.doh) + (bh * a.Tp + q0) * DP};
-    const T* const cols[2] = {reinterpret_cast<const T*>(a.qh_t) + tile, reinterpret_cast<const T*>(a.doh_t) + tile};
+    const T* const cols[2] = {kBF ? nullptr : reinterpret_cast<const T*>(a.qh_t) + tile,
+                              kBF ? nullptr : reinterpret_cast<const T*>(a.doh_t) + tile};
     M::load(r, rows, cols, (int)(q0 % kChunk), tid);
     const bool qin = tid < kFillKV && q0 + tid < a.T;
     ls = qin ? a.lse[bh * a.Tp + q0 + tid] : INFINITY;
@@ -308,12 +337,8 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
         });
         static_for<2>([&](auto hh) {
           static_for<DP / 32>([&](auto db) {
-            const T* dr = &dOTs[(32 * db + lr) * C::TS + ro + 16 * hh + 4 * g];
-            const T* qr = &QTs[(32 * db + lr) * C::TS + ro + 16 * hh + 4 * g];
-            const bf16x4 dlo = *reinterpret_cast<const bf16x4*>(dr), dhi = *reinterpret_cast<const bf16x4*>(dr + 8);
-            const bf16x4 qlo = *reinterpret_cast<const bf16x4*>(qr), qhi = *reinterpret_cast<const bf16x4*>(qr + 8);
-            const bf16x8 bo = {dlo[0], dlo[1], dlo[2], dlo[3], dhi[0], dhi[1], dhi[2], dhi[3]};
-            const bf16x8 bq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
+            const bf16x8 bo = tr_operand<C::RS>(dOs, ro + 16 * hh, 32 * db, lane);
+            const bf16x8 bq = tr_operand<C::RS>(Qs, ro + 16 * hh, 32 * db, lane);
             dV[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pb[hh], bo, dV[db], 0, 0, 0);
             dK[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(sb[hh], bq, dK[db], 0, 0, 0);
           });
@@ -351,8 +376,9 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
   using C = BwdCfg<T, DP>;
   typedef typename frag<T>::type frag_t;
   constexpr bool kBF = sizeof(T) == 2;
-  using M = typename TileCopy<T, DP>::template Multi<2, 1>;
-  __shared__ __align__(16) T tiles[M::kElems];   // K, V (row-major), K^T
+  // K and V row-major; fp32 also loads K^T (bf16 reads it from K, tr_operand)
+  using M = typename TileCopy<T, DP>::template Multi<2, kBF ? 0 : 1>;
+  __shared__ __align__(16) T tiles[M::kElems];
   const T* const Ks = tiles;
   const T* const Vs = tiles + M::kRowTile;
   const T* const KTs = tiles + 2 * M::kRowTile;
@@ -394,7 +420,7 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
       u32x4 r[M::IT];
       const T* const rows[2] = {reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + k0) * DP,
                                 reinterpret_cast<const T*>(a.vh) + (bh * a.Tp + k0) * DP};
-      const T* const cols[1] = {reinterpret_cast<const T*>(a.kh_t) + (bh * a.nch + k0 / kChunk) * DP * kChunk};
+      const T* const cols[1] = {kBF ? nullptr : reinterpret_cast<const T*>(a.kh_t) + (bh * a.nch + k0 / kChunk) * DP * kChunk};
       M::load(r, rows, cols, 0, tid);
       __syncthreads();                      // the previous fill is consumed
       M::store(tiles, r, tid);
@@ -430,9 +456,7 @@ __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_e
         static_for<2>([&](auto hh) { static_for<8>([&](auto e) { sb[hh][(int)e] = (bf16)dP[8 * hh + e]; }); });
         static_for<2>([&](auto hh) {
           static_for<DP / 32>([&](auto db) {
-            const T* kr = &KTs[(32 * db + lr) * C::TS + ro + 16 * hh + 4 * g];
-            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kr), hi = *reinterpret_cast<const bf16x4*>(kr + 8);
-            const bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const bf16x8 av = tr_operand<C::RS>(Ks, ro + 16 * hh, 32 * db, lane);
             dQ[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, sb[hh], dQ[db], 0, 0, 0);
           });
         });

@@ -63,7 +63,7 @@ struct BwdArgs {
   // incoming gradient of o
   const void* dout; int64_t do_rs, do_hs;
   // workspace
-  void* doh; void* doh_t; void* qh_t; void* kh_t; void* vh;   // io dtype
+  void* doh; void* doh_t; void* qh_t; void* kh_t; void* vh;   // io dtype; the _t layouts fp32 only
   float* delta;                                               // (B, H, Tp): rowsum(do * o)
   float* dqh; float* dkh; float* dvh;                         // fp32, path frame
   float* carry;                                               // (B, H, nch, nb, 4) chained suffix sums

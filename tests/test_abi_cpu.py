@@ -114,12 +114,14 @@ def _bwd(lib, **kw):
 
 
 def test_backward_argument_validation(lib):
-    # workspace: five io-dtype path-frame arrays, delta, three fp32 arrays,
-    # the chained suffix sums and the ticket block, each rounded to 256 bytes
+    # workspace: io-dtype path-frame arrays (doh, vh; fp32 also doh_t, qh_t,
+    # kh_t), delta, three fp32 arrays, the chained suffix sums and the ticket
+    # block, each rounded to 256 bytes
     n = 2 * 3 * 2048 * 96
     r = lambda x: (x + 255) // 256 * 256
-    assert lib.holo_attn_bwd_workspace_size(2, 2048, 3, 96, _lib.HOLO_BF16) == \
-        5 * r(2 * n) + r(2 * 3 * 2048 * 4) + 3 * r(4 * n) + r(2 * 3 * 32 * 32 * 16) + 256
+    rest = r(2 * 3 * 2048 * 4) + 3 * r(4 * n) + r(2 * 3 * 32 * 32 * 16) + 256
+    assert lib.holo_attn_bwd_workspace_size(2, 2048, 3, 96, _lib.HOLO_BF16) == 2 * r(2 * n) + rest
+    assert lib.holo_attn_bwd_workspace_size(2, 2048, 3, 96, _lib.HOLO_F32) == 5 * r(4 * n) + rest
     assert lib.holo_attn_bwd_workspace_size(2, 2048, 3, 96, 9) == 0
     assert _bwd(lib, B=0) == _lib.HOLO_ERR_BAD_SHAPE
     assert _bwd(lib, d=200) == _lib.HOLO_ERR_UNSUPPORTED
