@@ -328,8 +328,8 @@ attn_fwd(AttnArgs a) {
 template <typename T, int DP, bool PQ16>
 static hipError_t launch_attn_dp(const AttnArgs& a, hipStream_t s) {
   using C = AttnCfg<T, DP>;
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&attn_fwd<T, DP, PQ16>), hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::lds);
+  static_assert(C::lds <= kMaxDynamicLds, "tile configuration exceeds the LDS of a workgroup");
+  const hipError_t attr = allow_dynamic_lds<&attn_fwd<T, DP, PQ16>>();
   if (attr != hipSuccess) return attr;
   const int64_t nfold = ((a.T + kBM - 1) / kBM + 1) / 2;
   hipLaunchKernelGGL((attn_fwd<T, DP, PQ16>), dim3((unsigned)(a.B * a.H * nfold)), dim3(kThreads),

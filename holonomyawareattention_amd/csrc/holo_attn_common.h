@@ -1,6 +1,8 @@
 // Tile shapes and wave-level helpers shared by the attention kernels (gfx950).
 #pragma once
 
+#include <atomic>
+
 #include "holo_kernels.h"
 
 namespace holo {
@@ -62,5 +64,27 @@ template <typename T, int DP> struct AttnCfg {
   static_assert(VCH * E * kThreads == kBN * DP, "V tile must split evenly over the threads");
   static_assert((kStage * sizeof(T)) % 16 == 0, "stages must stay 16-byte aligned");
 };
+
+// Largest dynamic LDS a workgroup may use on gfx950, and the device ids the
+// opt-in below tracks.
+constexpr int kMaxDynamicLds = 160 * 1024;
+constexpr int kMaxDevices = 64;
+
+// Opts `Kernel` into kMaxDynamicLds of dynamic LDS on the current device. The
+// attribute belongs to the (kernel, device) pair, so it is set once per device
+// that launches the kernel; launches then pass their own LDS size.
+template <auto Kernel>
+hipError_t allow_dynamic_lds() {
+  static std::atomic<bool> done[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  if (done[dev].load(std::memory_order_acquire)) return hipSuccess;
+  e = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kMaxDynamicLds);
+  if (e == hipSuccess) done[dev].store(true, std::memory_order_release);
+  return e;
+}
 
 }  // namespace holo

@@ -434,10 +434,8 @@ template <typename T, int DP, bool PQ16, bool WRAP>
 static hipError_t launch_masked_dp(const MaskedArgs& a, hipStream_t s) {
   using M = MaskedCfg<T, DP>;
   const size_t lds = M::lds(a.Tp / kBN);
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
-  const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&attn_masked<T, DP, PQ16, WRAP>), hipFuncAttributeMaxDynamicSharedMemorySize,
-      (int)lds);
+  if (lds > (size_t)kMaxDynamicLds) return hipErrorInvalidValue;
+  const hipError_t attr = allow_dynamic_lds<&attn_masked<T, DP, PQ16, WRAP>>();
   if (attr != hipSuccess) return attr;
   const int64_t ntile = (a.T + kBM - 1) / kBM;
   hipLaunchKernelGGL((attn_masked<T, DP, PQ16, WRAP>), dim3((unsigned)(a.B * a.H * ntile)), dim3(kThreads),
