@@ -171,7 +171,29 @@ __global__ void __launch_bounds__(kBwdThreads) bwd_prep(BwdArgs a) {
   float dot = 0.f;
   const T* orow = reinterpret_cast<const T*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs;
   const T* drow = reinterpret_cast<const T*>(a.dout) + (b * a.T + t) * a.do_rs + h * a.do_hs;
-  if (in) {
+  // d = 96 with 16-byte aligned rows: thread p owns dims [24p, 24p + 24) (8
+  // whole blocks), read as 16-byte vectors, and its 8 quaternions (contiguous)
+  const bool wide = DP == 96 && a.d == 96 &&
+                    ((reinterpret_cast<uintptr_t>(drow) | reinterpret_cast<uintptr_t>(orow)) & 15) == 0;
+  if (in && wide) {
+    constexpr int E = 16 / sizeof(T);
+    float u[24], v[24];
+    static_for<24 / E>([&](auto cc) {
+      const u32x4 ru = reinterpret_cast<const u32x4*>(drow + 24 * p)[cc];
+      const u32x4 rv = reinterpret_cast<const u32x4*>(orow + 24 * p)[cc];
+      const T* eu = reinterpret_cast<const T*>(&ru);
+      const T* ev = reinterpret_cast<const T*>(&rv);
+      static_for<E>([&](auto j) { u[cc * E + j] = to_f32(eu[j]); v[cc * E + j] = to_f32(ev[j]); });
+    });
+    const float* pq = a.P + ((bh * a.T + t) * a.nb + 8 * p) * 4;
+    static_for<8>([&](auto jb) {
+      const rot3 R = qmat(load_quat(pq + 4 * jb));
+      dot += u[3 * jb] * v[3 * jb] + u[3 * jb + 1] * v[3 * jb + 1] + u[3 * jb + 2] * v[3 * jb + 2];
+      float y0, y1, y2;
+      rot_t_apply(R, u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
+      Ds[tl][24 * p + 3 * jb] = y0; Ds[tl][24 * p + 3 * jb + 1] = y1; Ds[tl][24 * p + 3 * jb + 2] = y2;
+    });
+  } else if (in) {
     for (int blk = p; blk < a.nb; blk += 4) {
       const rot3 R = qmat(load_quat(a.P + ((bh * a.T + t) * a.nb + blk) * 4));
       float u[3], v[3];
