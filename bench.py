@@ -400,7 +400,7 @@ def decoder_bench(args, torch, F, kernels):
                                   "attention_layers_attention_core": stage_ms[2],
                                   "attention_layers_out_projection": stage_ms[3],
                                   "rest (embedding, LayerNorms, MLPs, residuals, LM head)": ms - stage_ms.sum()},
-           "roofline": {"kernel": "attn_fwd (holo_attn_fwd), 12 launches per step", "bound": "mfma",
+           "roofline": {"kernel": "attn_fwd_bf16 (holo_attn_fwd), 12 launches per step", "bound": "mfma",
                         "achieved": core_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                         "frac": core_tflops / PEAK_BF16_TFLOPS, "traffic": None,
                         "work_per_launch": f"{fl_core:.4e} FLOP = 2*d*T*(T+1)*B*H"}}
@@ -605,10 +605,11 @@ def main():
                       "attention_core": stage_ms[2], "out_projection": stage_ms[3],
                       "sum": float(stage_ms.sum())},
         "roofline": {"kernel": ("attn_masked + wrap_queries + pack_mask (holo_attn_masked_fwd)" if exact
-                                else "attn_fwd (holo_attn_fwd)"), "bound": "mfma",
+                                else ("attn_fwd_bf16 (holo_attn_fwd)" if dt == torch.bfloat16
+                                      else "attn_fwd (holo_attn_fwd)")), "bound": "mfma",
                      "achieved": core_tflops, "peak": core_peak, "unit": "TFLOP/s",
                      "frac": core_tflops / core_peak,
-                     "traffic": None if exact else traffic_from_profile(args.config, ["attn_fwd"]),
+                     "traffic": None if exact else traffic_from_profile(args.config, ["attn_fwd_bf16" if dt == torch.bfloat16 else "attn_fwdIf"]),
                      "work_per_launch": f"{fl_core:.4e} FLOP = 4*d*(allowed pairs {pairs})*B*H"},
         "roofline_scan": {"kernels": "scan_reset + chunk_apply (holo_geom_scan_fwd)",
                           "bound": "hbm", "achieved": scan_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",

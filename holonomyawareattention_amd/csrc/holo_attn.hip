@@ -23,20 +23,97 @@
 // The queries arrive already transported (qh from the scan); the back-rotation
 // o_i = P_i oh_i is fused into the epilogue, which stages the tile's outputs
 // through LDS and rotates each 3-dim block by its stored quaternion.
+// Two kernels share this decomposition and the epilogue: attn_fwd_bf16 (bf16
+// MFMA, three waves per SIMD, direct global->LDS tile loads) and attn_fwd
+// (fp32 MFMA, two waves per SIMD, register-staged tile loads).
 #include <type_traits>
 
 #include "holo_attn_common.h"
 
 namespace holo {
 
-// Pipeline over key tiles j = 0, 1, ...: three LDS stages hold tiles j, j+1
-// and j+2; registers hold tile j+3 in flight. Iteration j issues the QK MFMAs
+// Epilogue of a 128-query tile: normalise the wave's O^T accumulator (dims on
+// the MFMA rows, its 32 queries on the lanes) by the row sums, stage it in LDS
+// (fp32 rows of OS), then back-rotate o = P oh per 3-dim block with the stored
+// quaternions (int16 or fp32) and write 16-byte rows. Os may alias the
+// key/value ring: every read of the ring must be complete.
+template <typename T, int DP, bool PQ16>
+__device__ __forceinline__ void store_tile_output(const AttnArgs& a, float* Os, const f32x16 (&O)[DP / 32],
+                                                  float m_run, float l_run, int64_t q0, int64_t qw, int bh,
+                                                  int b, int h, int tid, int w, int lr, int g) {
+  using C = AttnCfg<T, DP>;
+  const float lt = pair_sum(l_run);
+  const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
+  if (a.lse && g == 0 && qw + lr < a.T) a.lse[(int64_t)bh * a.Tp + qw + lr] = m_run + __log2f(lt);
+  static_for<DP / 32>([&](auto db) {
+    static_for<16>([&](auto r) {
+      Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][(int)r] * inv;
+    });
+  });
+  __syncthreads();
+  // items (row, 8 consecutive 3-dim groups = 24 dims); a row's 8 quaternions
+  // are 128 contiguous bytes in fp32, 64 in int16
+  typedef typename std::conditional<PQ16, u32x2, f32x4>::type pq_t;
+  const pq_t pq_ident = [] {
+    if constexpr (PQ16) return u32x2{1u, 0u};            // (1, 0, 0, 0)
+    else return f32x4{1.f, 0.f, 0.f, 0.f};
+  }();
+  pq_t pq[C::EPI][8];
+  static_for<C::EPI>([&](auto it) {
+    const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
+    const int64_t t = q0 + r;
+    const bool row_ok = idx < kBM * C::NG8 && t < a.T;
+    const pq_t* base = reinterpret_cast<const pq_t*>(
+        reinterpret_cast<const char*>(a.P) + ((bh * a.T + t) * a.nb + 8 * gi) * (int64_t)sizeof(pq_t));
+    if (row_ok && 8 * gi + 8 <= a.nb) {
+      static_for<8>([&](auto jb) { pq[it][jb] = base[jb]; });
+    } else {
+      static_for<8>([&](auto jb) { pq[it][jb] = (row_ok && 8 * gi + jb < a.nb) ? base[jb] : pq_ident; });
+    }
+  });
+  // item = (row, 8 consecutive 3-dim groups = 24 dims), quaternions in pq
+  static_for<C::EPI>([&](auto it) {
+    const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
+    const int64_t t = q0 + r;
+    if (idx >= kBM * C::NG8 || t >= a.T || 24 * gi >= a.d) return;
+    float u[24];
+    static_for<24>([&](auto j) { u[j] = (24 * gi + j < DP) ? Os[r * C::OS + 24 * gi + j] : 0.f; });
+    static_for<8>([&](auto jb) {
+      if (8 * gi + jb < a.nb) {
+        float y0, y1, y2;
+        quat qr;
+        if constexpr (PQ16) qr = unpack_quat_snorm16(pq[it][jb]);
+        else qr = quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]};
+        quat_rotate(qr, u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
+        u[3 * jb] = y0; u[3 * jb + 1] = y1; u[3 * jb + 2] = y2;
+      }
+    });
+    T* orow = reinterpret_cast<T*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs + 24 * gi;
+    if (24 * gi + 24 <= a.d && (reinterpret_cast<uintptr_t>(orow) & 15) == 0) {
+      constexpr int E = 16 / sizeof(T);
+      static_for<24 / E>([&](auto cc) {
+        u32x4 raw;
+        T* e = reinterpret_cast<T*>(&raw);
+        static_for<E>([&](auto j) { e[j] = from_f32<T>(u[cc * E + j]); });
+        reinterpret_cast<u32x4*>(orow)[cc] = raw;
+      });
+    } else {
+      static_for<24>([&](auto j) {
+        if (24 * gi + j < a.d) orow[j] = from_f32<T>(u[j]);
+      });
+    }
+  });
+}
+
+// fp32 kernel (mfma_f32_32x32x2f32). Pipeline over key tiles j = 0, 1, ...:
+// three LDS stages hold tiles j, j+1 and j+2; registers hold tile j+3 in flight. Iteration j issues the QK MFMAs
 // of tile j+1, then runs the softmax and PV MFMAs of tile j (so the VALU work
 // overlaps the matrix core), stores tile j+2 into the free stage, issues the
 // loads of tile j+3 and ends with the tile's only barrier.
 template <typename T, int DP, bool PQ16>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 attn_fwd(AttnArgs a) {
+  static_assert(sizeof(T) == 4, "bf16 runs attn_fwd_bf16");
   using C = AttnCfg<T, DP>;
   extern __shared__ __align__(16) unsigned char smem[];
   T* const kv = reinterpret_cast<T*>(smem);
@@ -72,18 +149,13 @@ attn_fwd(AttnArgs a) {
     const int64_t qw = q0 + 32 * w;                       // first query of this wave
 
     // ---- Q^T operand straight from qh (the scan's transported queries) ----
-    constexpr bool kBF = sizeof(T) == 2;
-    constexpr int QF = kBF ? DP / 16 : DP / 2;            // Q^T operand steps
-    typedef typename std::conditional<kBF, bf16x8, float>::type qfrag_t;
-    qfrag_t qf[QF];
+    constexpr int QF = DP / 2;                            // Q^T operand steps
+    float qf[QF];
     {
       const int64_t qrow_t = qw + lr;                     // rows past Tp read as zero
       const T* qrow = reinterpret_cast<const T*>(a.qh) + ((int64_t)bh * a.Tp + qrow_t) * DP;
       const bool in = qrow_t < a.Tp;
-      static_for<QF>([&](auto s) {
-        if constexpr (kBF) qf[s] = in ? *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * g) : bf16x8{};
-        else qf[s] = in ? qrow[2 * s + g] : 0.f;
-      });
+      static_for<QF>([&](auto s) { qf[s] = in ? qrow[2 * s + g] : 0.f; });
     }
 
     f32x16 O[DP / 32];
@@ -138,13 +210,8 @@ attn_fwd(AttnArgs a) {
       S[0] = f32x16{}; S[1] = f32x16{};
       static_for<QF>([&](auto s) {
         static_for<2>([&](auto kb) {
-          if constexpr (kBF) {
-            bf16x8 av = *reinterpret_cast<const bf16x8*>(&Ks[(32 * kb + lr) * C::KS + 16 * s + 8 * g]);
-            S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, qf[s], S[kb], 0, 0, 0);
-          } else {
-            float av = Ks[(32 * kb + lr) * C::KS + 2 * s + g];
-            S[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, qf[s], S[kb], 0, 0, 0);
-          }
+          const float av = Ks[(32 * kb + lr) * C::KS + 2 * s + g];
+          S[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, qf[s], S[kb], 0, 0, 0);
         });
       });
     };
@@ -178,77 +245,19 @@ attn_fwd(AttnArgs a) {
       static_for<2>([&](auto kb) {
         static_for<16>([&](auto r) { S[kb][(int)r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][(int)r], c, nm)); });
       });
-      if constexpr (kBF) {
-        // P^T operand in bf16; the row sum is taken over the same rounded
-        // values (two per v_dot2), so numerator and denominator agree.
-        bf16x8 pb[2][2];
-        static_for<2>([&](auto kb) {
-          static_for<2>([&](auto hh) {
-            static_for<8>([&](auto e) { pb[kb][hh][(int)e] = (bf16)S[kb][8 * hh + e]; });
+      float t[16];
+      static_for<16>([&](auto r) { t[r] = S[0][(int)r] + S[1][(int)r]; });
+      static_for<8>([&](auto r) { t[r] += t[r + 8]; });
+      static_for<4>([&](auto r) { t[r] += t[r + 4]; });
+      static_for<2>([&](auto r) { t[r] += t[r + 2]; });
+      l_run += t[0] + t[1];
+      static_for<2>([&](auto kb) {
+        static_for<16>([&](auto r) {
+          static_for<DP / 32>([&](auto db) {
+            float av = Vs[(32 * db + lr) * C::VS + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3)];
+            O[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, S[kb][(int)r], O[db], 0, 0, 0);
           });
         });
-        // four independent partial sums (one per P^T operand), then a tree
-        float ls[2][2];
-        const bf16x2 one2 = {(bf16)1.f, (bf16)1.f};
-        static_for<2>([&](auto kb) {
-          static_for<2>([&](auto hh) {
-            ls[kb][hh] = 0.f;
-            static_for<4>([&](auto e) {
-              bf16x2 pr = {pb[kb][hh][2 * e], pb[kb][hh][2 * e + 1]};
-              ls[kb][hh] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, ls[kb][hh], false);
-            });
-          });
-        });
-        l_run += (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
-        static_for<2>([&](auto kb) {
-          static_for<2>([&](auto hh) {
-            static_for<DP / 32>([&](auto db) {          // independent accumulators back to back
-              const T* vr = &Vs[(32 * db + lr) * C::VS + 32 * kb + 16 * hh + 4 * g];
-              bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr);
-              bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + 8);
-              bf16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-              O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pb[kb][hh], O[db], 0, 0, 0);
-            });
-          });
-        });
-      } else {
-        float t[16];
-        static_for<16>([&](auto r) { t[r] = S[0][(int)r] + S[1][(int)r]; });
-        static_for<8>([&](auto r) { t[r] += t[r + 8]; });
-        static_for<4>([&](auto r) { t[r] += t[r + 4]; });
-        static_for<2>([&](auto r) { t[r] += t[r + 2]; });
-        l_run += t[0] + t[1];
-        static_for<2>([&](auto kb) {
-          static_for<16>([&](auto r) {
-            static_for<DP / 32>([&](auto db) {
-              float av = Vs[(32 * db + lr) * C::VS + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3)];
-              O[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, S[kb][(int)r], O[db], 0, 0, 0);
-            });
-          });
-        });
-      }
-    };
-    // quaternions of the epilogue items (row, 8 consecutive 3-dim groups); a
-    // row's 8 quaternions are 128 contiguous bytes in fp32, 64 in int16
-    typedef typename std::conditional<PQ16, u32x2, f32x4>::type pq_t;
-    const pq_t pq_ident = [] {
-      if constexpr (PQ16) return u32x2{1u, 0u};            // (1, 0, 0, 0)
-      else return f32x4{1.f, 0.f, 0.f, 0.f};
-    }();
-    pq_t pq[C::EPI][8];
-    auto load_epilogue_quats = [&](auto first, auto count) {
-      static_for<decltype(count)::value>([&](auto k) {
-        constexpr int it = decltype(first)::value + decltype(k)::value;
-        const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
-        const int64_t t = q0 + r;
-        const bool row_ok = idx < kBM * C::NG8 && t < a.T;
-        const pq_t* base = reinterpret_cast<const pq_t*>(
-            reinterpret_cast<const char*>(a.P) + ((bh * a.T + t) * a.nb + 8 * gi) * (int64_t)sizeof(pq_t));
-        if (row_ok && 8 * gi + 8 <= a.nb) {
-          static_for<8>([&](auto jb) { pq[it][jb] = base[jb]; });
-        } else {
-          static_for<8>([&](auto jb) { pq[it][jb] = (row_ok && 8 * gi + jb < a.nb) ? base[jb] : pq_ident; });
-        }
       });
     };
     // one pipeline step: tile j in S, tile j+1 into Sn
@@ -273,50 +282,7 @@ attn_fwd(AttnArgs a) {
       step(j, SA, SB);
       if (j + 1 < nkv) step(j + 1, SB, SA);
     }
-    load_epilogue_quats(std::integral_constant<int, 0>{}, std::integral_constant<int, C::EPI>{});
-
-    // ---- epilogue: normalise, stage O^T, back-rotate o = P oh, store ----
-    float lt = pair_sum(l_run);
-    const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
-    if (a.lse && g == 0 && qw + lr < a.T) a.lse[(int64_t)bh * a.Tp + qw + lr] = m_run + __log2f(lt);
-    static_for<DP / 32>([&](auto db) {
-      static_for<16>([&](auto r) {
-        Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][(int)r] * inv;
-      });
-    });
-    __syncthreads();
-    // item = (row, 8 consecutive 3-dim groups = 24 dims), quaternions in pq
-    static_for<C::EPI>([&](auto it) {
-      const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
-      const int64_t t = q0 + r;
-      if (idx >= kBM * C::NG8 || t >= a.T || 24 * gi >= a.d) return;
-      float u[24];
-      static_for<24>([&](auto j) { u[j] = (24 * gi + j < DP) ? Os[r * C::OS + 24 * gi + j] : 0.f; });
-      static_for<8>([&](auto jb) {
-        if (8 * gi + jb < a.nb) {
-          float y0, y1, y2;
-          quat qr;
-          if constexpr (PQ16) qr = unpack_quat_snorm16(pq[it][jb]);
-          else qr = quat{pq[it][jb][0], pq[it][jb][1], pq[it][jb][2], pq[it][jb][3]};
-          quat_rotate(qr, u[3 * jb], u[3 * jb + 1], u[3 * jb + 2], y0, y1, y2);
-          u[3 * jb] = y0; u[3 * jb + 1] = y1; u[3 * jb + 2] = y2;
-        }
-      });
-      T* orow = reinterpret_cast<T*>(a.o) + (b * a.T + t) * a.o_rs + h * a.o_hs + 24 * gi;
-      if (24 * gi + 24 <= a.d && (reinterpret_cast<uintptr_t>(orow) & 15) == 0) {
-        constexpr int E = 16 / sizeof(T);
-        static_for<24 / E>([&](auto cc) {
-          u32x4 raw;
-          T* e = reinterpret_cast<T*>(&raw);
-          static_for<E>([&](auto j) { e[j] = from_f32<T>(u[cc * E + j]); });
-          reinterpret_cast<u32x4*>(orow)[cc] = raw;
-        });
-      } else {
-        static_for<24>([&](auto j) {
-          if (24 * gi + j < a.d) orow[j] = from_f32<T>(u[j]);
-        });
-      }
-    });
+    store_tile_output<T, DP, PQ16>(a, Os, O, m_run, l_run, q0, qw, bh, b, h, tid, w, lr, g);
   };
   run_tile(ntile - 1 - f);
   if (f != ntile - 1 - f) {
@@ -325,15 +291,245 @@ attn_fwd(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 kernel: three waves per SIMD. The same work decomposition (folded pairs
+// of 128-query tiles, 4 waves x 32 queries, 64-key tiles), built to fit three
+// workgroups per CU so that a third wave per SIMD hides the latency that two
+// leave exposed (dependent MFMA results, LDS reads, barriers):
+//   - key/value tiles reach LDS by direct global->LDS loads
+//     (global_load_lds_dwordx4) into a 2-stage ring: no staging registers and
+//     no ds_write; tiles are stored unpadded with an XOR swizzle of their
+//     16-byte chunks (k_swz, v_swz) under which the fragment reads are free of
+//     bank conflicts; LDS 51.2 KB per workgroup (the epilogue's fp32 staging);
+//   - one S buffer: the QK of tile j+1 is issued after the tile barrier and
+//     the other waves on the SIMD overlap their softmax with it (<= 168 VGPRs;
+//     the few values kept across the loop spill outside it).
+// Key order inside S^T: lane lr reads K row pi(lr) of each 32-key block (pi
+// swaps the 4-row groups 1 and 2 of every 16), so register r of the S^T
+// accumulator of lane (lr, g) holds key 16(r>>3) + 8g + (r&7): the P^T operand
+// of one PV MFMA covers 8 consecutive keys, which is one 16-byte V^T chunk.
+// Step j (stage j&1 holds tile j; tile j+1 is in flight to the other stage):
+// softmax and PV of tile j; wait for this thread's loads; barrier; loads of
+// tile j+2 into stage j&1; QK of tile j+1.
+template <int DP> struct RingCfg {
+  static constexpr int NCK = DP / 8;                        // 16-byte chunks per K row
+  static constexpr int QF = DP / 16, NDB = DP / 32;
+  static constexpr int KT = kBN * DP;                       // elements per K (= V^T) tile
+  static constexpr int kTileBytes = KT * 2;
+  static constexpr int kVRegion = 2 * kTileBytes;           // LDS: [K stage 0, 1][V stage 0, 1]
+  static constexpr int NKB = NCK % 8 == 0 ? NCK / 2 : 2;    // per-lane K read bases
+  static constexpr int NI = KT / 8 / kThreads;              // 16-byte loads per thread per K (V) tile
+  static constexpr size_t kv_bytes = (size_t)4 * kTileBytes;
+  static constexpr size_t lds = kv_bytes > AttnCfg<bf16, DP>::o_bytes ? kv_bytes : AttnCfg<bf16, DP>::o_bytes;
+  static_assert(NI * 8 * kThreads == KT, "tile split");
+};
+
+// chunk XOR of K row r (NCK chunks per row); only the low four bits of r
+// enter, so a lane's XOR is the same in every 32-row block
+template <int NCK> __device__ __forceinline__ int k_swz(int r) {
+  if constexpr (NCK % 8 == 0) return ((r >> 1) ^ ((r & 1) << 1)) & 7;
+  else return ((r >> 2) ^ ((r >> 1) & 1)) & 3;
+}
+// chunk XOR of V^T row r (8 chunks per row); low five bits only
+__device__ __forceinline__ int v_swz(int r) { return ((r & 7) ^ ((r >> 3) & 3)) & 7; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int N> __device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void ring_barrier() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int DP, bool PQ16>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+attn_fwd_bf16(AttnArgs a) {
+  using C = RingCfg<DP>;
+  using T = bf16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* const Os = reinterpret_cast<float*>(smem);
+
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ntile = (int)((a.T + kBM - 1) / kBM);
+  const int nfold = (ntile + 1) / 2;
+  const int L = blockIdx.x;
+  int bh, f;                                  // folded pairs and XCD mapping as attn_fwd
+  if ((a.B * a.H) % 8 == 0) {
+    const int j = L >> 3;
+    bh = 8 * (j / nfold) + (L & 7);
+    f = j % nfold;
+  } else {
+    bh = L % (a.B * a.H);
+    f = L / (a.B * a.H);
+  }
+  const int b = bh / a.H, h = bh % a.H;
+  const T* kbase = reinterpret_cast<const T*>(a.kh) + (int64_t)bh * a.Tp * DP;
+  const T* vbase = reinterpret_cast<const T*>(a.vh_t) + (int64_t)bh * a.nch * DP * kBN;
+
+  // direct loads: 16-byte chunk p = i*256 + tid of a tile lands at LDS chunk p;
+  // the lane fetches the (row, chunk) that the swizzle stores there
+  int koff[C::NI], voff[C::NI];
+  static_for<C::NI>([&](auto i) {
+    const int p = i * kThreads + tid;
+    const int rk = p / C::NCK, ck = (p % C::NCK) ^ k_swz<C::NCK>(rk);
+    koff[i] = rk * DP + ck * 8;
+    const int rv = p >> 3, cv = (p & 7) ^ v_swz(rv);
+    voff[i] = rv * kBN + cv * 8;
+  });
+  auto issue_tile = [&](int kt, auto st) {
+    const unsigned char* kg = reinterpret_cast<const unsigned char*>(kbase + (int64_t)kt * C::KT);
+    const unsigned char* vg = reinterpret_cast<const unsigned char*>(vbase + (int64_t)kt * C::KT);
+    unsigned char* ks = smem + decltype(st)::value * C::kTileBytes;
+    unsigned char* vs = smem + C::kVRegion + decltype(st)::value * C::kTileBytes;
+    static_for<C::NI>([&](auto i) {
+      __builtin_amdgcn_global_load_lds(kg + (uint32_t)(koff[i] * 2), (lds_void*)(ks + (i * kThreads + 64 * w) * 16), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vg + (uint32_t)(voff[i] * 2), (lds_void*)(vs + (i * kThreads + 64 * w) * 16), 16, 0, 0);
+    });
+  };
+  // fragment reads: a few per-lane base offsets plus compile-time offsets. K
+  // chunk (2s+g)^kx: with a 2-bit XOR it is 4(s>>1) + ((2(s&1)+g)^kx), so two
+  // bases cover every s; with a 3-bit XOR there is one base per s. V chunk
+  // (4kb+2hh+g)^vx: one base per (kb, hh); db adds 32 rows.
+  const int pr = (lr & ~12) | ((lr & 4) << 1) | ((lr & 8) >> 1);     // pi(lr)
+  const int kx = k_swz<C::NCK>(pr), vx = v_swz(lr);
+  int kb_off[C::NKB], vb_off[4];
+  static_for<C::NKB>([&](auto i) { kb_off[i] = (pr * C::NCK + ((2 * i + g) ^ kx)) * 16; });
+  static_for<4>([&](auto i) { vb_off[i] = C::kVRegion + (lr * 8 + ((2 * i + g) ^ vx)) * 16; });
+  auto k_frag = [&](auto st, auto kb, auto s) -> bf16x8 {
+    constexpr int sv = decltype(s)::value;
+    constexpr int bi = C::NCK % 8 == 0 ? sv : (sv & 1);
+    constexpr int imm = decltype(st)::value * C::kTileBytes + decltype(kb)::value * 32 * C::NCK * 16 +
+                        (C::NCK % 8 == 0 ? 0 : (sv >> 1) * 64);
+    return *reinterpret_cast<const bf16x8*>(smem + kb_off[bi] + imm);
+  };
+  auto v_frag = [&](auto st, auto kb, auto hh, auto db) -> bf16x8 {
+    constexpr int bi = 2 * decltype(kb)::value + decltype(hh)::value;
+    constexpr int imm = decltype(st)::value * C::kTileBytes + decltype(db)::value * 32 * 8 * 16;
+    return *reinterpret_cast<const bf16x8*>(smem + vb_off[bi] + imm);
+  };
+
+  auto run_tile = [&](const int qt) {
+    const int64_t q0 = (int64_t)qt * kBM;
+    const int64_t qw = q0 + 32 * w;
+    bf16x8 qf[C::QF];                         // Q^T operand straight from qh
+    {
+      const int64_t qrow_t = qw + lr;         // rows past Tp read as zero
+      const T* qrow = reinterpret_cast<const T*>(a.qh) + ((int64_t)bh * a.Tp + qrow_t) * DP;
+      const bool in = qrow_t < a.Tp;
+      static_for<C::QF>([&](auto s) { qf[s] = in ? *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * g) : bf16x8{}; });
+    }
+    f32x16 O[C::NDB];
+    static_for<C::NDB>([&](auto i) { O[i] = f32x16{}; });
+    float m_run = -1e30f, l_run = 0.f;
+    const float c = a.scale_log2;
+    int64_t kend = q0 + kBM; if (kend > a.T) kend = a.T;
+    const int nkv = (int)((kend + kBN - 1) / kBN);
+    const int nact = qw >= a.T ? 0 : (int)((qw + 31) / kBN) + 1 < nkv ? (int)((qw + 31) / kBN) + 1 : nkv;
+
+    f32x16 S[2];
+    auto qk = [&](auto st) {
+      S[0] = f32x16{}; S[1] = f32x16{};
+      static_for<C::QF>([&](auto s) {
+        static_for<2>([&](auto kb) {
+          S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(st, kb, s), qf[s], S[kb], 0, 0, 0);
+        });
+      });
+    };
+    // online softmax (log2 units, one lane pair per query) and O^T += V^T P^T
+    auto softmax_pv = [&](int kt, auto st) {
+      const int64_t k0 = (int64_t)kt * kBN;
+      if (k0 + kBN - 1 > qw) {                // tile reaches past this wave's first query
+        const int rel = (int)(qw - k0) + lr - 8 * g;
+        static_for<2>([&](auto kb) {
+          static_for<16>([&](auto r) {
+            if (32 * kb + 16 * (r >> 3) + (r & 7) > rel) S[kb][(int)r] = -INFINITY;
+          });
+        });
+      }
+      const float mx = pair_max(tile_max(S)) * c;
+      const bool need = mx > m_run + kRescaleThreshold;     // per row; the branch only skips work
+      if (__any(need)) {
+        const float m_new = need ? mx : m_run;
+        const float corr = exp2f(m_run - m_new);
+        m_run = m_new;
+        l_run *= corr;
+        static_for<C::NDB>([&](auto i) { O[i] *= corr; });
+      }
+      const float nm = -m_run;
+      // P^T operands in bf16; the row sum is taken over the same rounded values
+      bf16x8 pb[2][2];
+      const bf16x2 one2 = {(bf16)1.f, (bf16)1.f};
+      float ls[2][2];
+      static_for<2>([&](auto kb) {
+        static_for<2>([&](auto hh) {
+          static_for<8>([&](auto e) {
+            pb[kb][hh][(int)e] = (bf16)__builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][8 * hh + e], c, nm));
+          });
+          ls[kb][hh] = 0.f;
+          static_for<4>([&](auto e) {
+            bf16x2 pr2 = {pb[kb][hh][2 * e], pb[kb][hh][2 * e + 1]};
+            ls[kb][hh] = __builtin_amdgcn_fdot2_f32_bf16(pr2, one2, ls[kb][hh], false);
+          });
+        });
+      });
+      l_run += (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
+      static_for<2>([&](auto kb) {
+        static_for<2>([&](auto hh) {
+          static_for<C::NDB>([&](auto db) {
+            O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(st, kb, hh, db), pb[kb][hh], O[db], 0, 0, 0);
+          });
+        });
+      });
+    };
+    auto step = [&](int j, auto st) {
+      using SN = std::integral_constant<int, 1 - decltype(st)::value>;
+      if (j < nact) softmax_pv(j, st);
+      wait_vmem<0>();                         // this thread's loads of tile j+1
+      ring_barrier();                         // every wave's loads landed, tile j read
+      if (j + 2 < nkv) issue_tile(j + 2, st);
+      if (j + 1 < nact) qk(SN{});
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    issue_tile(0, S0{});
+    if (nkv > 1) { issue_tile(1, S1{}); wait_vmem<2 * C::NI>(); } else { wait_vmem<0>(); }
+    ring_barrier();
+    if (nact > 0) qk(S0{});
+    for (int j = 0; j < nkv; j += 2) {
+      step(j, S0{});
+      if (j + 1 < nkv) step(j + 1, S1{});
+    }
+    // the last step's barrier follows every read of the ring and no load is
+    // in flight, so the staging may overwrite it
+    store_tile_output<T, DP, PQ16>(a, Os, O, m_run, l_run, q0, qw, bh, b, h, tid, w, lr, g);
+  };
+  run_tile(ntile - 1 - f);
+  if (f != ntile - 1 - f) {
+    __syncthreads();                          // the first tile's epilogue is done with the LDS
+    run_tile(f);
+  }
+}
+
 template <typename T, int DP, bool PQ16>
 static hipError_t launch_attn_dp(const AttnArgs& a, hipStream_t s) {
-  using C = AttnCfg<T, DP>;
-  static_assert(C::lds <= kMaxDynamicLds, "tile configuration exceeds the LDS of a workgroup");
-  const hipError_t attr = allow_dynamic_lds<&attn_fwd<T, DP, PQ16>>();
-  if (attr != hipSuccess) return attr;
   const int64_t nfold = ((a.T + kBM - 1) / kBM + 1) / 2;
-  hipLaunchKernelGGL((attn_fwd<T, DP, PQ16>), dim3((unsigned)(a.B * a.H * nfold)), dim3(kThreads),
-                     C::lds, s, a);
+  const dim3 grid((unsigned)(a.B * a.H * nfold));
+  if constexpr (sizeof(T) == 2) {
+    using C = RingCfg<DP>;
+    static_assert(C::lds <= kMaxDynamicLds, "tile configuration exceeds the LDS of a workgroup");
+    const hipError_t attr = allow_dynamic_lds<&attn_fwd_bf16<DP, PQ16>>();
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((attn_fwd_bf16<DP, PQ16>), grid, dim3(kThreads), C::lds, s, a);
+  } else {
+    using C = AttnCfg<T, DP>;
+    static_assert(C::lds <= kMaxDynamicLds, "tile configuration exceeds the LDS of a workgroup");
+    const hipError_t attr = allow_dynamic_lds<&attn_fwd<T, DP, PQ16>>();
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((attn_fwd<T, DP, PQ16>), grid, dim3(kThreads), C::lds, s, a);
+  }
   return hipGetLastError();
 }
 
