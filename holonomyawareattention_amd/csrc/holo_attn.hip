@@ -24,7 +24,7 @@
 // o_i = P_i oh_i is fused into the epilogue, which stages the tile's outputs
 // through LDS and rotates each 3-dim block by its stored quaternion.
 // Two kernels share this decomposition and the epilogue: attn_fwd_bf16 (bf16
-// MFMA, three waves per SIMD, direct global->LDS tile loads) and attn_fwd
+// MFMA, three waves per SIMD, tile loads that write LDS directly) and attn_fwd
 // (fp32 MFMA, two waves per SIMD, register-staged tile loads).
 #include <type_traits>
 
@@ -296,14 +296,14 @@ attn_fwd(AttnArgs a) {
 // of 128-query tiles, 4 waves x 32 queries, 64-key tiles), built to fit three
 // workgroups per CU so that a third wave per SIMD hides the latency that two
 // leave exposed (dependent MFMA results, LDS reads, barriers):
-//   - key/value tiles reach LDS by direct global->LDS loads
-//     (global_load_lds_dwordx4) into a 2-stage ring: no staging registers and
-//     no ds_write; tiles are stored unpadded with an XOR swizzle of their
+//   - key/value tiles reach LDS by buffer loads that write LDS directly
+//     (buffer_load_dwordx4 ... lds) into a 2-stage ring: no staging registers
+//     and no ds_write; tiles are stored unpadded with an XOR swizzle of their
 //     16-byte chunks (k_swz, v_swz) under which the fragment reads are free of
 //     bank conflicts; LDS 51.2 KB per workgroup (the epilogue's fp32 staging);
 //   - one S buffer: the QK of tile j+1 is issued after the tile barrier and
-//     the other waves on the SIMD overlap their softmax with it (<= 168 VGPRs;
-//     the few values kept across the loop spill outside it).
+//     the other waves on the SIMD overlap their softmax with it (<= 168 VGPRs:
+//     160 at d = 96, no spills).
 // Key order inside S^T: lane lr reads K row pi(lr) of each 32-key block (pi
 // swaps the 4-row groups 1 and 2 of every 16), so register r of the S^T
 // accumulator of lane (lr, g) holds key 16(r>>3) + 8g + (r&7): the P^T operand
@@ -369,24 +369,30 @@ attn_fwd_bf16(AttnArgs a) {
   const T* kbase = reinterpret_cast<const T*>(a.kh) + (int64_t)bh * a.Tp * DP;
   const T* vbase = reinterpret_cast<const T*>(a.vh_t) + (int64_t)bh * a.nch * DP * kBN;
 
-  // direct loads: 16-byte chunk p = i*256 + tid of a tile lands at LDS chunk p;
+  // loads to LDS: 16-byte chunk p = i*256 + tid of a tile lands at LDS chunk p;
   // the lane fetches the (row, chunk) that the swizzle stores there
   int koff[C::NI], voff[C::NI];
   static_for<C::NI>([&](auto i) {
     const int p = i * kThreads + tid;
     const int rk = p / C::NCK, ck = (p % C::NCK) ^ k_swz<C::NCK>(rk);
-    koff[i] = rk * DP + ck * 8;
+    koff[i] = (rk * DP + ck * 8) * (int)sizeof(T);           // bytes
     const int rv = p >> 3, cv = (p & 7) ^ v_swz(rv);
-    voff[i] = rv * kBN + cv * 8;
+    voff[i] = (rv * kBN + cv * 8) * (int)sizeof(T);
   });
+  // buffer loads to LDS: the (b, h) slice in a buffer resource (reads past it
+  // return zero), the tile offset in a scalar register and one 32-bit byte
+  // offset per lane and load (a 64-bit global address per load would hold
+  // twice the registers)
+  const int kv_bytes = (int)((int64_t)a.Tp * DP * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kbase), 0, kv_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vbase), 0, kv_bytes, kBufferWord3);
   auto issue_tile = [&](int kt, auto st) {
-    const unsigned char* kg = reinterpret_cast<const unsigned char*>(kbase + (int64_t)kt * C::KT);
-    const unsigned char* vg = reinterpret_cast<const unsigned char*>(vbase + (int64_t)kt * C::KT);
+    const int toff = kt * C::kTileBytes;
     unsigned char* ks = smem + decltype(st)::value * C::kTileBytes;
     unsigned char* vs = smem + C::kVRegion + decltype(st)::value * C::kTileBytes;
     static_for<C::NI>([&](auto i) {
-      __builtin_amdgcn_global_load_lds(kg + (uint32_t)(koff[i] * 2), (lds_void*)(ks + (i * kThreads + 64 * w) * 16), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vg + (uint32_t)(voff[i] * 2), (lds_void*)(vs + (i * kThreads + 64 * w) * 16), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(ks + (i * kThreads + 64 * w) * 16), 16, koff[i], toff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(vs + (i * kThreads + 64 * w) * 16), 16, voff[i], toff, 0, 0);
     });
   };
   // fragment reads: a few per-lane base offsets plus compile-time offsets. K
