@@ -60,3 +60,24 @@ def test_shape_sweep_bf16_tril(d):
     y = y.double().cpu().numpy()
     ref = R.forward_blocks(x, W, H, 0.7)
     assert np.abs(y - ref).max() <= 2.5e-2 * max(1.0, np.abs(ref).max() / 4)
+
+
+@pytest.mark.parametrize("T", [1, 64, 65, 257])
+@pytest.mark.parametrize("d", [32, 64, 96])
+def test_shape_sweep_bf16_tril_xcd_grid(d, T):
+    """B*H = 8: the bf16 causal kernel's XCD-mapped grid of folded query-tile
+    pairs (one fold at T <= 128, three at T = 257 with a ragged last tile),
+    at each padded head width; same bar as the sweep above."""
+    B, H = 2, 4
+    D = H * d
+    print(f"bf16 xcd grid d={d} T={T}", flush=True)
+    x, W = layer(97 + d + T, B, T, D, H, "additive", dtype=torch.bfloat16)
+    m = make_module(W, D, H, 0.7, "additive", torch.bfloat16, DEV)
+    mask = torch.ones(T, T, dtype=torch.bool, device=DEV).tril()
+    with torch.no_grad():
+        y, _ = m(torch.as_tensor(x, device=DEV, dtype=torch.bfloat16), attn_mask=mask)
+    torch.cuda.synchronize()
+    y = y.double().cpu().numpy()
+    ref = R.forward_blocks(x, W, H, 0.7)
+    assert np.isfinite(y).all()
+    assert np.abs(y - ref).max() <= 2.5e-2 * max(1.0, np.abs(ref).max() / 4)
