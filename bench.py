@@ -84,6 +84,7 @@ def cpu_baseline(cfg, x_np, W, min_seconds=10.0, link_mode="additive"):
                                                "attention cost per token grows with T, so the full "
                                                "sequence runs slower per token)")
     return {"value": rows * Ts / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "host_cpu_count": os.cpu_count(),
             "kind": "port", "seconds": round(dt, 3),
             "sample": f"batch rows 0..{rows - 1} of the same workload, {span} "
                       f"(H={H}, d_head={cfg['D'] // H}, fp32, the reference's dense SO(d) "
@@ -400,7 +401,7 @@ def decoder_bench(args, torch, F, kernels):
                                   "attention_layers_attention_core": stage_ms[2],
                                   "attention_layers_out_projection": stage_ms[3],
                                   "rest (embedding, LayerNorms, MLPs, residuals, LM head)": ms - stage_ms.sum()},
-           "roofline": {"kernel": "attn_fwd_bf16 (holo_attn_fwd), 12 launches per step", "bound": "mfma",
+           "roofline": {"kernel": "attn_fwd_h16 (holo_attn_fwd; fp16 operands), 12 launches per step", "bound": "mfma",
                         "achieved": core_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                         "frac": core_tflops / PEAK_BF16_TFLOPS, "traffic": None,
                         "work_per_launch": f"{fl_core:.4e} FLOP = 2*d*T*(T+1)*B*H"}}
@@ -439,7 +440,8 @@ def decoder_cpu_baseline(m, tok, c, Ts=512):
             h = h + torch.nn.functional.linear(torch.nn.functional.gelu(torch.nn.functional.linear(a, w0, b0)), w2, b2)
         h @ lm.T
         dt = time.perf_counter() - t0
-    return {"value": Ts / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+    return {"value": Ts / dt, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "host_cpu_count": os.cpu_count(), "kind": "port",
             "seconds": round(dt, 3),
             "sample": f"batch row 0, the first {Ts} of T={c['T']} tokens, all {c['NL']} layers and the LM "
                       f"head (fp32; attention = the reference's dense SO(d) layout and chunked algorithm step "
@@ -599,17 +601,18 @@ def main():
                    "global_batch": B, "seq_len": T, "n_heads": H, "d_head": d, "d_model": D,
                    "rotation": f"{d // 3} SO(3) blocks per head", "link_mode": args.link,
                    "mode": args.mode, "mask": args.mask,
+                   "attention_operands": ("bf16" if exact else "fp16") if dt == torch.bfloat16 else "fp32",
                    "edge_scale": es, "parallelism": "single GPU"},
         "layer_tflops": (fl_core + fl_proj) / (ms_per_step * 1e-3) / 1e12,
         "stages_ms": {"projections": stage_ms[0], "geom_scan": stage_ms[1],
                       "attention_core": stage_ms[2], "out_projection": stage_ms[3],
                       "sum": float(stage_ms.sum())},
         "roofline": {"kernel": ("attn_masked + wrap_queries + pack_mask (holo_attn_masked_fwd)" if exact
-                                else ("attn_fwd_bf16 (holo_attn_fwd)" if dt == torch.bfloat16
-                                      else "attn_fwd (holo_attn_fwd)")), "bound": "mfma",
+                                else ("attn_fwd_h16 (holo_attn_fwd; fp16 operands, fp32 accumulation)"
+                                      if dt == torch.bfloat16 else "attn_fwd (holo_attn_fwd)")), "bound": "mfma",
                      "achieved": core_tflops, "peak": core_peak, "unit": "TFLOP/s",
                      "frac": core_tflops / core_peak,
-                     "traffic": None if exact else traffic_from_profile(args.config, ["attn_fwd_bf16" if dt == torch.bfloat16 else "attn_fwdIf"]),
+                     "traffic": None if exact else traffic_from_profile(args.config, ["attn_fwd_h16" if dt == torch.bfloat16 else "attn_fwdIf"]),
                      "work_per_launch": f"{fl_core:.4e} FLOP = 4*d*(allowed pairs {pairs})*B*H"},
         "roofline_scan": {"kernels": "scan_reset + chunk_apply (holo_geom_scan_fwd)",
                           "bound": "hbm", "achieved": scan_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",

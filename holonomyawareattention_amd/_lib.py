@@ -21,6 +21,10 @@ HOLO_ERR_LAUNCH = 5
 
 HOLO_F32 = 0
 HOLO_BF16 = 1
+HOLO_F16 = 2
+
+HOLO_WS_TIMEOUT = 1
+HOLO_WS_OVERFLOW = 2
 
 HOLO_GEN_ADDITIVE = 0
 HOLO_GEN_DIRECT = 1
@@ -43,10 +47,11 @@ SIGNATURES = [
     ("holo_padded_head_dim", _I, [_I]),
     ("holo_padded_seq_len", _L, [_L]),
     ("holo_geom_scan_workspace_size", _S, [_I, _L, _I, _I]),
-    ("holo_geom_scan_fwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I, _I,
+    ("holo_workspace_status", _I, [_P, _S, _P, _P]),
+    ("holo_geom_scan_fwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I, _I, _I,
                                 _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L,
                                 _P, _P, _P, _P, _P, _P, _S, _P]),
-    ("holo_attn_fwd", _I, [_I, _L, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _L, _L, _P, _P]),
+    ("holo_attn_fwd", _I, [_I, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _L, _L, _P, _P]),
     ("holo_attn_masked_workspace_size", _S, [_I, _L, _I, _I, _I, _I, _I]),
     ("holo_attn_masked_fwd", _I, [_I, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _L,
                                   _P, _L, _L, _P, _S, _P]),

@@ -36,6 +36,7 @@ output is not differentiable (return_geometry under autograd raises).
 from __future__ import annotations
 
 import math
+import weakref
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -43,6 +44,22 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import kernels
+
+
+class _Verified:
+    """Remembers that a tensor passed a check, without keeping it alive: a
+    weak reference plus its address and version counter. A later tensor
+    matches only if it is the same live object, unmodified since (so a new
+    tensor placed at a freed tensor's address never matches)."""
+
+    __slots__ = ("ref", "key")
+
+    def __init__(self, t: torch.Tensor, extra=()):
+        self.ref = weakref.ref(t)
+        self.key = (t.data_ptr(), t._version, *extra)
+
+    def matches(self, t: torch.Tensor, extra=()) -> bool:
+        return self.ref() is t and self.key == (t.data_ptr(), t._version, *extra)
 
 
 def _is_exact_tril(mask: Optional[torch.Tensor], L: int) -> bool:
@@ -139,9 +156,9 @@ class PathOrderedGeometricMHA(nn.Module):
             nn.Linear(4 * d_model, self.m_dim * n_heads),
         )
         self.link_mode = "interaction"
-        self._wcat_key = None
+        self._wcat_src = None          # _Verified of each weight behind _wcat
         self._wcat = None
-        self._mask_ok = None
+        self._mask_ok = None           # _Verified of the last mask found to be tril(L)
         # profiling hook: when set to a sequence of 5 torch.cuda.Event, forward
         # records them on the launch stream around its four stages (link
         # inputs, geometry scan, attention, out-projection); no host sync
@@ -167,15 +184,16 @@ class PathOrderedGeometricMHA(nn.Module):
     def _tril_path(self, attn_mask, L: int) -> bool:
         """causal mode with attn_mask exactly tril(L): the reference's kernel
         path (kernel/attention_kernel.py:203-208), here the causal kernels
-        with their fused backward. The check runs once per mask tensor."""
+        with their fused backward. The check runs once per mask tensor: the
+        verdict is kept for the same live tensor object while it is unmodified
+        (a weak reference plus its version counter, never its address alone)."""
         if self.mode != "causal" or attn_mask is None:
             return False
-        key = (attn_mask.data_ptr(), attn_mask._version, tuple(attn_mask.shape), attn_mask.device)
-        if key == self._mask_ok:
+        if self._mask_ok is not None and self._mask_ok.matches(attn_mask, (tuple(attn_mask.shape),)):
             return True
         if not _is_exact_tril(attn_mask, L):
             return False
-        self._mask_ok = key
+        self._mask_ok = _Verified(attn_mask, (tuple(attn_mask.shape),))
         return True
 
     def _kernel_supported(self, x, attn_mask, return_geometry=False) -> bool:
@@ -185,14 +203,15 @@ class PathOrderedGeometricMHA(nn.Module):
         return self._unsupported_reason(x, attn_mask) is None and self._tril_path(attn_mask, x.shape[1])
 
     def _cat_weight(self, mods) -> torch.Tensor:
-        """Row-concatenated weights of `mods` for one GEMM, rebuilt only when a
-        weight changes."""
+        """Row-concatenated weights of `mods` for one GEMM, rebuilt unless every
+        weight is the same live tensor, unmodified, as at the last build."""
         ws = tuple(mod.weight for mod in mods)
-        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
-        if key != self._wcat_key:
+        src = self._wcat_src
+        if src is None or len(src) != len(ws) or not all(v.matches(w, (w.dtype, w.device, tuple(w.shape)))
+                                                         for v, w in zip(src, ws)):
             with torch.no_grad():
                 self._wcat = torch.cat([w.detach() for w in ws], dim=0)
-            self._wcat_key = key
+            self._wcat_src = tuple(_Verified(w, (w.dtype, w.device, tuple(w.shape))) for w in ws)
         return self._wcat
 
     def _link_inputs(self, x: torch.Tensor):
@@ -271,6 +290,13 @@ class PathOrderedGeometricMHA(nn.Module):
         return F.linear(o.reshape(B, L, D), self.out.weight)
 
     @staticmethod
+    def _op_dtype(x: torch.Tensor) -> torch.dtype:
+        """Operand type of the transported q, k, v on the causal inference
+        path: fp16 for bf16 activations (11-bit significands on the matrix
+        cores at the bf16 rate; the parity bar needs them), fp32 otherwise."""
+        return torch.float16 if x.dtype == torch.bfloat16 else x.dtype
+
+    @staticmethod
     def _p_format(x: torch.Tensor, return_geometry: bool) -> str:
         """Storage of the prefix rotations between the scan and the attention
         epilogue: int16 quaternions (half the bytes, quantisation ~6e-5 of a
@@ -310,10 +336,11 @@ class PathOrderedGeometricMHA(nn.Module):
                 ev[1].record()
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
                                                      want_hol=return_geometry,
-                                                     p_format=self._p_format(x, return_geometry))
+                                                     p_format=self._p_format(x, return_geometry),
+                                                     op_dtype=self._op_dtype(x))
             if ev is not None:
                 ev[2].record()
-            o = kernels.attention(qh, kh, vh_t, P, self.d, self.scale)
+            o = kernels.attention(qh, kh, vh_t, P, self.d, self.scale, out_dtype=x.dtype)
             if ev is not None:
                 ev[3].record()
             y = F.linear(o.view(B, L, D), self.out.weight)

@@ -48,11 +48,12 @@ int check_common(int B, int64_t T, int H, int d) {
   return HOLO_OK;
 }
 
-// Backward workspace, each region 256-byte aligned: doh, vh and, for fp32
+// Backward workspace, each region 256-byte aligned: the ticket counter and
+// status word, doh, vh and, for fp32
 // only, doh_t, qh_t, kh_t (io dtype, B*H*Tp*Dp each; the bf16 kernels read
 // the transposed operands from row-major LDS tiles), delta (fp32, B*H*Tp),
 // dqh, dkh, dvh (fp32, B*H*Tp*Dp each), the chained suffix sums (fp32,
-// B*H*nch*nb*4) and the ticket counter / time-out flag. Returns the total;
+// B*H*nch*nb*4). Returns the total;
 // fills `a` when given.
 size_t bwd_layout(int B, int64_t T, int H, int d, size_t es, void* base, holo::BwdArgs* a) {
   const int64_t Tp = holo::padded_seq(T), nch = Tp / holo::kChunk;
@@ -63,13 +64,14 @@ size_t bwd_layout(int B, int64_t T, int H, int d, size_t es, void* base, holo::B
     off += (bytes + 255) / 256 * 256;
     return base ? static_cast<char*>(base) + at : nullptr;
   };
+  // ticket counter and status word first (holo_workspace_status reads word 1)
+  unsigned* ticket = reinterpret_cast<unsigned*>(take(256));
   void* r[5];
   for (int i = 0; i < 5; ++i) r[i] = (es == 2 && i >= 1 && i <= 3) ? nullptr : take(n * es);
   float* delta = reinterpret_cast<float*>(take((size_t)B * H * Tp * 4));
   float* g[3];
   for (auto& p : g) p = reinterpret_cast<float*>(take(n * 4));
   float* carry = reinterpret_cast<float*>(take((size_t)B * H * nch * (d / 3) * 16));
-  unsigned* ticket = reinterpret_cast<unsigned*>(take(256));
   if (a) {
     a->doh = r[0]; a->doh_t = r[1]; a->qh_t = r[2]; a->kh_t = r[3]; a->vh = r[4];
     a->delta = delta; a->dqh = g[0]; a->dkh = g[1]; a->dvh = g[2]; a->carry = carry; a->ticket = ticket;
@@ -83,7 +85,7 @@ extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (5 << 16) | 0; }
+int holo_abi_version(void) { return (6 << 16) | 0; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -94,8 +96,19 @@ size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d) {
   return holo::scan_state_bytes(B, T, H, d);
 }
 
+int holo_workspace_status(const void* workspace, size_t workspace_bytes, unsigned* status, void* stream) {
+  g_last_error.clear();
+  if (!workspace || !status) return fail(HOLO_ERR_INVALID_ARG, "null workspace or status pointer");
+  if (workspace_bytes < 8) return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes holds no status word", workspace_bytes);
+  const hipError_t e = hipMemcpyAsync(status, static_cast<const unsigned*>(workspace) + 1, sizeof(unsigned),
+                                      hipMemcpyDefault, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "status copy: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
 int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
-                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype, int p_format, int mode,
+                       int gen_mode, float edge_scale, int io_dtype, int op_dtype, int gen_dtype,
+                       int p_format, int mode,
                        const void* gq, int64_t gq_rs, int64_t gq_hs,
                        const void* gk, int64_t gk_rs, int64_t gk_hs,
                        const void* q, int64_t q_rs, int64_t q_hs,
@@ -112,6 +125,9 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
     return fail(HOLO_ERR_INVALID_ARG, "gen_dtype %d is not HOLO_F32 or HOLO_BF16", gen_dtype);
   if (io_dtype == HOLO_F32 && gen_dtype != HOLO_F32)
     return fail(HOLO_ERR_UNSUPPORTED, "fp32 keys/values need an fp32 generator");
+  if (io_dtype == HOLO_F32 ? op_dtype != HOLO_F32 : (op_dtype != HOLO_BF16 && op_dtype != HOLO_F16))
+    return fail(HOLO_ERR_INVALID_ARG, "op_dtype %d with io_dtype %d (fp32 inputs: HOLO_F32; bf16 inputs: "
+                "HOLO_BF16 or HOLO_F16)", op_dtype, io_dtype);
   if (gen_mode != HOLO_GEN_ADDITIVE && gen_mode != HOLO_GEN_DIRECT)
     return fail(HOLO_ERR_INVALID_ARG, "gen_mode %d unknown", gen_mode);
   if (p_format != HOLO_QUAT_F32 && p_format != HOLO_QUAT_SNORM16)
@@ -163,29 +179,36 @@ int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
     a.wide = (d == 48 || d == 72 || d == 96) && al(gq, gq_rs, gq_hs, ge) && al(gk, gk_rs, gk_hs, ge) &&
              al(q, q_rs, q_hs, ie) && al(k, k_rs, k_hs, ie) && al(v, v_rs, v_hs, ie);
   }
-  {
-    // chained-scan state: chunk products and inclusive prefixes, then the
-    // ticket counter and time-out flag (cleared by the scan's own reset launch)
-    const size_t nq = (size_t)B * H * 2 * a.nch * nb * 4;
-    a.incl = static_cast<float*>(workspace);
-    a.ticket = reinterpret_cast<unsigned*>(a.incl + nq);
-  }
+  // chained-scan workspace: the ticket counter and status word (256 bytes),
+  // then the chunk products and inclusive prefixes (cleared by the scan's own
+  // reset launch)
+  a.ticket = static_cast<unsigned*>(workspace);
+  a.incl = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = io_dtype == HOLO_F32 ? holo::launch_scan<float, float>(a, s)
-                 : gen_dtype == HOLO_F32 ? holo::launch_scan<holo::bf16, float>(a, s)
-                                         : holo::launch_scan<holo::bf16, holo::bf16>(a, s);
+  using holo::bf16;
+  using holo::f16;
+  hipError_t e;
+  if (io_dtype == HOLO_F32) e = holo::launch_scan<float, float, float>(a, s);
+  else if (op_dtype == HOLO_F16)
+    e = gen_dtype == HOLO_F32 ? holo::launch_scan<bf16, f16, float>(a, s) : holo::launch_scan<bf16, f16, bf16>(a, s);
+  else
+    e = gen_dtype == HOLO_F32 ? holo::launch_scan<bf16, bf16, float>(a, s) : holo::launch_scan<bf16, bf16, bf16>(a, s);
   if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "scan launch: %s", hipGetErrorString(e));
   return HOLO_OK;
 }
 
-int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float scale,
+int holo_attn_fwd(int B, int64_t T, int H, int d, int op_dtype, int out_dtype, int p_format, float scale,
                   const void* qh, const void* kh, const void* vh_t, const void* P,
                   void* o, int64_t o_rs, int64_t o_hs, float* lse, void* stream) {
   g_last_error.clear();
   int rc = check_common(B, T, H, d);
   if (rc) return rc;
-  if (dtype != HOLO_F32 && dtype != HOLO_BF16)
-    return fail(HOLO_ERR_INVALID_ARG, "dtype %d is not HOLO_F32 or HOLO_BF16", dtype);
+  if (op_dtype != HOLO_F32 && op_dtype != HOLO_BF16 && op_dtype != HOLO_F16)
+    return fail(HOLO_ERR_INVALID_ARG, "op_dtype %d is not HOLO_F32, HOLO_BF16 or HOLO_F16", op_dtype);
+  if (out_dtype != HOLO_F32 && !(out_dtype == HOLO_BF16 && op_dtype != HOLO_F32))
+    return fail(HOLO_ERR_INVALID_ARG, "out_dtype %d with op_dtype %d (HOLO_F32, or HOLO_BF16 with 16-bit operands)",
+                out_dtype, op_dtype);
+  const int dtype = op_dtype;
   if (p_format != HOLO_QUAT_F32 && p_format != HOLO_QUAT_SNORM16)
     return fail(HOLO_ERR_INVALID_ARG, "p_format %d is not HOLO_QUAT_F32 or HOLO_QUAT_SNORM16", p_format);
   const int nb = d / 3;
@@ -209,8 +232,12 @@ int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float
   a.p_format = p_format;
   a.lse = lse;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = dtype == HOLO_F32 ? holo::launch_attn<float>(a, s)
-                                   : holo::launch_attn<holo::bf16>(a, s);
+  using holo::bf16;
+  using holo::f16;
+  const bool of = out_dtype == HOLO_F32;
+  hipError_t e = op_dtype == HOLO_F32    ? holo::launch_attn<float, float>(a, s)
+                 : op_dtype == HOLO_BF16 ? (of ? holo::launch_attn<bf16, float>(a, s) : holo::launch_attn<bf16, bf16>(a, s))
+                                         : (of ? holo::launch_attn<f16, float>(a, s) : holo::launch_attn<f16, bf16>(a, s));
   if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "attention launch: %s", hipGetErrorString(e));
   return HOLO_OK;
 }

@@ -23,9 +23,11 @@
 // The queries arrive already transported (qh from the scan); the back-rotation
 // o_i = P_i oh_i is fused into the epilogue, which stages the tile's outputs
 // through LDS and rotates each 3-dim block by its stored quaternion.
-// Two kernels share this decomposition and the epilogue: attn_fwd_bf16 (bf16
-// MFMA, three waves per SIMD, tile loads that write LDS directly) and attn_fwd
-// (fp32 MFMA, two waves per SIMD, register-staged tile loads).
+// Two kernels share this decomposition and the epilogue: attn_fwd_h16 (16-bit
+// operands, bf16 or fp16, on the MFMA; three waves per SIMD, tile loads that
+// write LDS directly) and attn_fwd (fp32 MFMA, two waves per SIMD,
+// register-staged tile loads). The output o is written in its own type OT:
+// the operand type's companion (bf16 for the bf16 path) or fp32.
 #include <type_traits>
 
 #include "holo_attn_common.h"
@@ -35,13 +37,13 @@ namespace holo {
 // Epilogue of a 128-query tile: normalise the wave's O^T accumulator (dims on
 // the MFMA rows, its 32 queries on the lanes) by the row sums, stage it in LDS
 // (fp32 rows of OS), then back-rotate o = P oh per 3-dim block with the stored
-// quaternions (int16 or fp32) and write 16-byte rows. Os may alias the
-// key/value ring: every read of the ring must be complete.
+// quaternions (int16 or fp32) and write 16-byte rows of o in type T. Os may
+// alias the key/value ring: every read of the ring must be complete.
 template <typename T, int DP, bool PQ16>
 __device__ __forceinline__ void store_tile_output(const AttnArgs& a, float* Os, const f32x16 (&O)[DP / 32],
                                                   float m_run, float l_run, int64_t q0, int64_t qw, int bh,
                                                   int b, int h, int tid, int w, int lr, int g) {
-  using C = AttnCfg<T, DP>;
+  using C = AttnCfg<float, DP>;                  // staging layout (fp32 rows of OS)
   const float lt = pair_sum(l_run);
   const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
   if (a.lse && g == 0 && qw + lr < a.T) a.lse[(int64_t)bh * a.Tp + qw + lr] = m_run + __log2f(lt);
@@ -113,7 +115,7 @@ __device__ __forceinline__ void store_tile_output(const AttnArgs& a, float* Os, 
 template <typename T, int DP, bool PQ16>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 attn_fwd(AttnArgs a) {
-  static_assert(sizeof(T) == 4, "bf16 runs attn_fwd_bf16");
+  static_assert(sizeof(T) == 4, "16-bit operands run attn_fwd_h16");
   using C = AttnCfg<T, DP>;
   extern __shared__ __align__(16) unsigned char smem[];
   T* const kv = reinterpret_cast<T*>(smem);
@@ -292,7 +294,8 @@ attn_fwd(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// bf16 kernel: three waves per SIMD. The same work decomposition (folded pairs
+// 16-bit kernel (operands OPT = bf16 or fp16, output OT): three waves per
+// SIMD. The same work decomposition (folded pairs
 // of 128-query tiles, 4 waves x 32 queries, 64-key tiles), built to fit three
 // workgroups per CU so that a third wave per SIMD hides the latency that two
 // leave exposed (dependent MFMA results, LDS reads, barriers):
@@ -343,11 +346,14 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int DP, bool PQ16>
+template <typename OPT, typename OT, int DP, bool PQ16>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
-attn_fwd_bf16(AttnArgs a) {
+attn_fwd_h16(AttnArgs a) {
   using C = RingCfg<DP>;
-  using T = bf16;
+  using T = OPT;
+  using Op = Op16<OPT>;
+  using v8 = typename Op::v8;
+  using v2 = typename Op::v2;
   extern __shared__ __align__(16) unsigned char smem[];
   float* const Os = reinterpret_cast<float*>(smem);
 
@@ -404,28 +410,28 @@ attn_fwd_bf16(AttnArgs a) {
   int kb_off[C::NKB], vb_off[4];
   static_for<C::NKB>([&](auto i) { kb_off[i] = (pr * C::NCK + ((2 * i + g) ^ kx)) * 16; });
   static_for<4>([&](auto i) { vb_off[i] = C::kVRegion + (lr * 8 + ((2 * i + g) ^ vx)) * 16; });
-  auto k_frag = [&](auto st, auto kb, auto s) -> bf16x8 {
+  auto k_frag = [&](auto st, auto kb, auto s) -> v8 {
     constexpr int sv = decltype(s)::value;
     constexpr int bi = C::NCK % 8 == 0 ? sv : (sv & 1);
     constexpr int imm = decltype(st)::value * C::kTileBytes + decltype(kb)::value * 32 * C::NCK * 16 +
                         (C::NCK % 8 == 0 ? 0 : (sv >> 1) * 64);
-    return *reinterpret_cast<const bf16x8*>(smem + kb_off[bi] + imm);
+    return *reinterpret_cast<const v8*>(smem + kb_off[bi] + imm);
   };
-  auto v_frag = [&](auto st, auto kb, auto hh, auto db) -> bf16x8 {
+  auto v_frag = [&](auto st, auto kb, auto hh, auto db) -> v8 {
     constexpr int bi = 2 * decltype(kb)::value + decltype(hh)::value;
     constexpr int imm = decltype(st)::value * C::kTileBytes + decltype(db)::value * 32 * 8 * 16;
-    return *reinterpret_cast<const bf16x8*>(smem + vb_off[bi] + imm);
+    return *reinterpret_cast<const v8*>(smem + vb_off[bi] + imm);
   };
 
   auto run_tile = [&](const int qt) {
     const int64_t q0 = (int64_t)qt * kBM;
     const int64_t qw = q0 + 32 * w;
-    bf16x8 qf[C::QF];                         // Q^T operand straight from qh
+    v8 qf[C::QF];                             // Q^T operand straight from qh
     {
       const int64_t qrow_t = qw + lr;         // rows past Tp read as zero
       const T* qrow = reinterpret_cast<const T*>(a.qh) + ((int64_t)bh * a.Tp + qrow_t) * DP;
       const bool in = qrow_t < a.Tp;
-      static_for<C::QF>([&](auto s) { qf[s] = in ? *reinterpret_cast<const bf16x8*>(qrow + 16 * s + 8 * g) : bf16x8{}; });
+      static_for<C::QF>([&](auto s) { qf[s] = in ? *reinterpret_cast<const v8*>(qrow + 16 * s + 8 * g) : v8{}; });
     }
     f32x16 O[C::NDB];
     static_for<C::NDB>([&](auto i) { O[i] = f32x16{}; });
@@ -440,7 +446,7 @@ attn_fwd_bf16(AttnArgs a) {
       S[0] = f32x16{}; S[1] = f32x16{};
       static_for<C::QF>([&](auto s) {
         static_for<2>([&](auto kb) {
-          S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_frag(st, kb, s), qf[s], S[kb], 0, 0, 0);
+          S[kb] = Op::mfma(k_frag(st, kb, s), qf[s], S[kb]);
         });
       });
     };
@@ -465,19 +471,20 @@ attn_fwd_bf16(AttnArgs a) {
         static_for<C::NDB>([&](auto i) { O[i] *= corr; });
       }
       const float nm = -m_run;
-      // P^T operands in bf16; the row sum is taken over the same rounded values
-      bf16x8 pb[2][2];
-      const bf16x2 one2 = {(bf16)1.f, (bf16)1.f};
+      // P^T operands in the operand type; the row sum is taken over the same
+      // rounded values
+      v8 pb[2][2];
+      const v2 one2 = {(T)1.f, (T)1.f};
       float ls[2][2];
       static_for<2>([&](auto kb) {
         static_for<2>([&](auto hh) {
           static_for<8>([&](auto e) {
-            pb[kb][hh][(int)e] = (bf16)__builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][8 * hh + e], c, nm));
+            pb[kb][hh][(int)e] = (T)__builtin_amdgcn_exp2f(__builtin_fmaf(S[kb][8 * hh + e], c, nm));
           });
           ls[kb][hh] = 0.f;
           static_for<4>([&](auto e) {
-            bf16x2 pr2 = {pb[kb][hh][2 * e], pb[kb][hh][2 * e + 1]};
-            ls[kb][hh] = __builtin_amdgcn_fdot2_f32_bf16(pr2, one2, ls[kb][hh], false);
+            v2 pr2 = {pb[kb][hh][2 * e], pb[kb][hh][2 * e + 1]};
+            ls[kb][hh] = Op::dot2(pr2, one2, ls[kb][hh]);
           });
         });
       });
@@ -485,7 +492,7 @@ attn_fwd_bf16(AttnArgs a) {
       static_for<2>([&](auto kb) {
         static_for<2>([&](auto hh) {
           static_for<C::NDB>([&](auto db) {
-            O[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_frag(st, kb, hh, db), pb[kb][hh], O[db], 0, 0, 0);
+            O[db] = Op::mfma(v_frag(st, kb, hh, db), pb[kb][hh], O[db]);
           });
         });
       });
@@ -510,7 +517,7 @@ attn_fwd_bf16(AttnArgs a) {
     }
     // the last step's barrier follows every read of the ring and no load is
     // in flight, so the staging may overwrite it
-    store_tile_output<T, DP, PQ16>(a, Os, O, m_run, l_run, q0, qw, bh, b, h, tid, w, lr, g);
+    store_tile_output<OT, DP, PQ16>(a, Os, O, m_run, l_run, q0, qw, bh, b, h, tid, w, lr, g);
   };
   run_tile(ntile - 1 - f);
   if (f != ntile - 1 - f) {
@@ -519,17 +526,18 @@ attn_fwd_bf16(AttnArgs a) {
   }
 }
 
-template <typename T, int DP, bool PQ16>
+template <typename T, typename OT, int DP, bool PQ16>
 static hipError_t launch_attn_dp(const AttnArgs& a, hipStream_t s) {
   const int64_t nfold = ((a.T + kBM - 1) / kBM + 1) / 2;
   const dim3 grid((unsigned)(a.B * a.H * nfold));
   if constexpr (sizeof(T) == 2) {
     using C = RingCfg<DP>;
     static_assert(C::lds <= kMaxDynamicLds, "tile configuration exceeds the LDS of a workgroup");
-    const hipError_t attr = allow_dynamic_lds<&attn_fwd_bf16<DP, PQ16>>();
+    const hipError_t attr = allow_dynamic_lds<&attn_fwd_h16<T, OT, DP, PQ16>>();
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((attn_fwd_bf16<DP, PQ16>), grid, dim3(kThreads), C::lds, s, a);
+    hipLaunchKernelGGL((attn_fwd_h16<T, OT, DP, PQ16>), grid, dim3(kThreads), C::lds, s, a);
   } else {
+    static_assert(std::is_same<OT, float>::value, "the fp32 kernel writes fp32");
     using C = AttnCfg<T, DP>;
     static_assert(C::lds <= kMaxDynamicLds, "tile configuration exceeds the LDS of a workgroup");
     const hipError_t attr = allow_dynamic_lds<&attn_fwd<T, DP, PQ16>>();
@@ -539,23 +547,26 @@ static hipError_t launch_attn_dp(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <typename T, bool PQ16>
+template <typename T, typename OT, bool PQ16>
 static hipError_t launch_attn_pf(const AttnArgs& a, hipStream_t s) {
   switch (a.Dp) {
-    case 32: return launch_attn_dp<T, 32, PQ16>(a, s);
-    case 64: return launch_attn_dp<T, 64, PQ16>(a, s);
-    case 96: return launch_attn_dp<T, 96, PQ16>(a, s);
+    case 32: return launch_attn_dp<T, OT, 32, PQ16>(a, s);
+    case 64: return launch_attn_dp<T, OT, 64, PQ16>(a, s);
+    case 96: return launch_attn_dp<T, OT, 96, PQ16>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
 
-template <typename T>
+template <typename OPT, typename OT>
 hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
-  return a.p_format ? launch_attn_pf<T, true>(a, s) : launch_attn_pf<T, false>(a, s);
+  return a.p_format ? launch_attn_pf<OPT, OT, true>(a, s) : launch_attn_pf<OPT, OT, false>(a, s);
 }
 
-template hipError_t launch_attn<float>(const AttnArgs&, hipStream_t);
-template hipError_t launch_attn<bf16>(const AttnArgs&, hipStream_t);
+template hipError_t launch_attn<float, float>(const AttnArgs&, hipStream_t);
+template hipError_t launch_attn<bf16, bf16>(const AttnArgs&, hipStream_t);
+template hipError_t launch_attn<bf16, float>(const AttnArgs&, hipStream_t);
+template hipError_t launch_attn<f16, bf16>(const AttnArgs&, hipStream_t);
+template hipError_t launch_attn<f16, float>(const AttnArgs&, hipStream_t);
 
 // ---- quaternion -> dense rotation matrices (geometry output) ----
 __global__ void __launch_bounds__(256) quat_to_dense(int64_t n, int d, int nb, const float* q, float* out) {

@@ -42,6 +42,28 @@ __device__ __forceinline__ float tile_max(const f32x16 (&S)[2]) {
   return fmaxf(max3(m[0], m[1], m[2]), m[3]);
 }
 
+// Matrix-core operations of a 16-bit operand type on gfx950: the 32x32x16
+// MFMA (fp32 accumulation) and the two-element dot product into fp32.
+template <typename T> struct Op16;
+template <> struct Op16<bf16> {
+  typedef bf16x8 v8;
+  typedef bf16x2 v2;
+  static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+};
+template <> struct Op16<f16> {
+  typedef f16x8 v8;
+  typedef f16x2 v2;
+  static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float dot2(v2 a, v2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+};
+
 template <typename T, int DP> struct AttnCfg {
   static constexpr int E = 16 / sizeof(T);             // elements per 16 B
   // LDS row strides chosen so the MFMA operand reads hit distinct banks:

@@ -659,7 +659,7 @@ __global__ void __launch_bounds__(kBwdThreads) link_bwd(BwdArgs a) {
         __builtin_amdgcn_s_sleep(1);
       }
       if (!ok) {
-        __hip_atomic_store(a.ticket + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(a.ticket + 1, kStatusTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const float nan = __uint_as_float(kCanonNan);
         nxt = quat{nan, nan, nan, nan};
       }

@@ -16,6 +16,10 @@ namespace holo {
 constexpr unsigned kUnset = 0xffffffffu;
 constexpr unsigned kCanonNan = 0x7fc00000u;
 constexpr int kMaxPolls = 1 << 18;   // ~0.3 s of polling
+// Bits of the status word that follows the ticket counter in a chained
+// workspace (cleared by the reset launch at the start of every call).
+constexpr unsigned kStatusTimeout = 1u;    // a carry wait ran out of polls (outputs NaN)
+constexpr unsigned kStatusOverflow = 2u;   // a transported value exceeded the operand type's range
 
 __device__ __forceinline__ void put_quat(float* slot, const quat& q) {
   unsigned* u = reinterpret_cast<unsigned*>(slot);

@@ -12,6 +12,11 @@ typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// fp16: the attention operands of the bf16 inference path (11-bit significand
+// against bf16's 8, same matrix-core rate)
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 // 16-byte and 8-byte raw moves: native vector types (HIP's uint4 is a union
@@ -38,9 +43,16 @@ __host__ __device__ inline int64_t padded_seq(int64_t T) { return (T + kChunk - 
 
 __device__ inline float to_f32(float x) { return x; }
 __device__ inline float to_f32(bf16 x) { return (float)x; }
+__device__ inline float to_f32(f16 x) { return (float)x; }
 template <typename T> __device__ inline T from_f32(float x);
 template <> __device__ inline float from_f32<float>(float x) { return x; }
 template <> __device__ inline bf16 from_f32<bf16>(float x) { return (bf16)x; }
+template <> __device__ inline f16 from_f32<f16>(float x) { return (f16)x; }
+
+// Largest finite magnitude of a storage type (fp16 operands overflow to inf
+// beyond it; the scan reports that in its status word).
+template <typename T> constexpr float max_finite() { return 3.0e38f; }
+template <> constexpr float max_finite<f16>() { return 65504.f; }
 
 // Quaternion (w, x, y, z); R(a (x) b) = R(a) R(b).
 struct quat { float w, x, y, z; };

@@ -19,7 +19,7 @@ struct ScanArgs {
   int wide;        // 16-byte row path of the scan (d in {48, 72, 96}, aligned rows)
   int inert;       // transport u' = P u (inert mode) instead of u^ = P^T u
   float* incl;     // chained-scan state: chunk products (B, H, nch, nb, 4), then inclusive prefixes (same shape)
-  unsigned* ticket;  // [0]: chunk ticket counter, [1]: carry-wait time-out flag
+  unsigned* ticket;  // [0]: chunk ticket counter, [1]: status word (kStatusTimeout, kStatusOverflow)
 };
 size_t scan_state_bytes(int B, int64_t T, int H, int d);
 constexpr int kScanGroup = 8;    // chunks per carry-chain hop of the scan when the chain lags
@@ -109,7 +109,7 @@ struct AddNormArgs {
   void* y; int64_t y_rs;
 };
 
-template <typename IO, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
+template <typename IO, typename OP, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_add_layernorm(const AddNormArgs& a, hipStream_t s);
 hipError_t launch_pack_mask(const uint8_t* mask, int64_t mask_rs, int64_t T, int64_t Tp, uint64_t* bits,
                             uint8_t* tile_act, hipStream_t s);
@@ -117,7 +117,8 @@ template <typename T> hipError_t launch_attn_masked(const MaskedArgs& a, hipStre
 template <typename IO, typename GT> hipError_t launch_decode_geom(const DecodeGeomArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_decode_attn(const DecodeAttnArgs& a, hipStream_t s);
 int64_t decode_splits(int64_t t);
-template <typename T> hipError_t launch_attn(const AttnArgs& a, hipStream_t s);
+// OPT: operand type of qh, kh, vh_t (fp32, bf16, fp16); OT: type of o (fp32, bf16)
+template <typename OPT, typename OT> hipError_t launch_attn(const AttnArgs& a, hipStream_t s);
 hipError_t launch_quat_to_dense(int64_t n, int d, const float* q, float* out, hipStream_t s);
 hipError_t launch_chain_reset(void* state, int64_t n_pairs, unsigned* ticket, hipStream_t s);
 template <typename IO, typename GT> hipError_t launch_bwd(const BwdArgs& a, hipStream_t s);

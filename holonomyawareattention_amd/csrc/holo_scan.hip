@@ -8,6 +8,11 @@
 //   P_0 = I, P_{t+1} = G_t P_t ; Hol = G_{T-1} P_{T-1}     :89-95
 //   qh_t  = P_t^T q_t, kh_t = P_t^T k_t, vh_t = P_t^T v_t   :108-110
 //
+// q, k, v are read in their storage type IO; the transported qh, kh, vh are
+// written in the operand type OP of the attention that consumes them (fp32,
+// bf16, or fp16 on the bf16 inference path: 11-bit significands for the
+// matrix-core operands). A value beyond OP's finite range sets bit 1 of the
+// status word in the workspace (bit 0: carry-wait time-out).
 // Each 3x3 block of every (b, h) is an independent scan over t. The scan is
 // one pass over the inputs in chunks of 64 links, one workgroup per
 // (b, h, chunk):
@@ -86,7 +91,7 @@ __device__ inline quat wait_slot(const ScanArgs& a, const float* slot) {
     if (get_quat(slot, x)) return x;
     __builtin_amdgcn_s_sleep(1);
   }
-  __hip_atomic_store(a.ticket + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_or(a.ticket + 1, kStatusTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const float nan = __uint_as_float(kCanonNan);
   return quat{nan, nan, nan, nan};
 }
@@ -187,9 +192,19 @@ __device__ inline void chunk_prefix(const ScanArgs& a, float* gs, float* ss, flo
 //      LDS (zero padding);
 //   4. the tiles leave with 16-byte stores of whole rows (each tile is one
 //      contiguous block in global memory).
-template <typename IO, typename GT, int DP>
+// Sets the overflow bit of the status word when |x| exceeds OP's finite range
+// for any value x this thread converts (mx: the largest magnitude seen).
+template <typename OP>
+__device__ __forceinline__ void note_range(const ScanArgs& a, float mx) {
+  if constexpr (sizeof(OP) == 2 && !std::is_same<OP, bf16>::value) {
+    if (mx > max_finite<OP>())
+      __hip_atomic_fetch_or(a.ticket + 1, kStatusOverflow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <typename IO, typename OP, typename GT, int DP>
 __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
-  constexpr int E = 16 / sizeof(IO);
+  constexpr int E = 16 / sizeof(OP);
   constexpr int KS = DP + E;            // LDS row strides (16 B multiples)
   constexpr int VS = kChunk + E;
   constexpr int NBM = DP / 3;           // blocks held in LDS (nb <= NBM)
@@ -197,9 +212,9 @@ __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
   __shared__ __align__(16) float gs[kChunk * NBM * 4];
   __shared__ __align__(16) float ss[8 * NBM * 4];
   __shared__ __align__(16) float cs[NBM * 4];
-  __shared__ __align__(16) IO qhs[kChunk * KS];
-  __shared__ __align__(16) IO khs[kChunk * KS];
-  __shared__ __align__(16) IO vts[DP * VS];
+  __shared__ __align__(16) OP qhs[kChunk * KS];
+  __shared__ __align__(16) OP khs[kChunk * KS];
+  __shared__ __align__(16) OP vts[DP * VS];
 
   const int tid = threadIdx.x;
   int64_t bh, c;
@@ -220,6 +235,7 @@ __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
   const IO* qin = reinterpret_cast<const IO*>(a.q) + h * a.q_hs;
   const IO* kin = reinterpret_cast<const IO*>(a.k) + h * a.k_hs;
   const IO* vin = reinterpret_cast<const IO*>(a.v) + h * a.v_hs;
+  float mx = 0.f;
   for (int idx = tid; idx < kChunk * NBX; idx += 256) {
     int i = idx / NBX, blk = idx % NBX, c0 = 3 * blk;
     int64_t t = t0 + i;
@@ -242,17 +258,20 @@ __global__ void __launch_bounds__(256) chunk_apply(ScanArgs a) {
         v3[0] = y0; v3[1] = y1; v3[2] = y2;
       }
     }
-    for (int j = 0; j < 3; ++j)
+    for (int j = 0; j < 3; ++j) {
+      mx = fmaxf(mx, fmaxf(fabsf(q3[j]), fmaxf(fabsf(k3[j]), fabsf(v3[j]))));
       if (c0 + j < DP) {
-        qhs[i * KS + c0 + j] = from_f32<IO>(q3[j]);
-        khs[i * KS + c0 + j] = from_f32<IO>(k3[j]);
-        vts[(c0 + j) * VS + i] = from_f32<IO>(v3[j]);
+        qhs[i * KS + c0 + j] = from_f32<OP>(q3[j]);
+        khs[i * KS + c0 + j] = from_f32<OP>(k3[j]);
+        vts[(c0 + j) * VS + i] = from_f32<OP>(v3[j]);
       }
+    }
   }
+  note_range<OP>(a, mx);
   __syncthreads();
-  u32x4* qdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.qh) + (bh * a.Tp + t0) * DP);
-  u32x4* kdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.kh) + (bh * a.Tp + t0) * DP);
-  u32x4* vdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.vh_t) + (bh * a.nch + c) * DP * kChunk);
+  u32x4* qdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.qh) + (bh * a.Tp + t0) * DP);
+  u32x4* kdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.kh) + (bh * a.Tp + t0) * DP);
+  u32x4* vdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.vh_t) + (bh * a.nch + c) * DP * kChunk);
   constexpr int KR = DP / E, VR = kChunk / E;      // 16 B chunks per row
   for (int i = tid; i < kChunk * KR; i += 256) {
     qdst[i] = *reinterpret_cast<const u32x4*>(&qhs[(i / KR) * KS + (i % KR) * E]);
@@ -290,20 +309,20 @@ __device__ __forceinline__ void store_row(T* p, const float* in) {
   });
 }
 
-template <typename IO, typename GT, int NG, int DP>
+template <typename IO, typename OP, typename GT, int NG, int DP>
 __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   constexpr int NT = 64 * NG;           // threads
   constexpr int NB = 8 * NG;            // blocks per head (nb)
   constexpr int D = 24 * NG;            // head dimension
-  constexpr int E = 16 / sizeof(IO);
+  constexpr int E = 16 / sizeof(OP);
   constexpr int VS = kChunk + E;
   constexpr int KS = DP + E;             // row stride of the staged qh / kh tiles
-  constexpr int GS_BYTES = kChunk * NB * 16, QK_BYTES = 2 * kChunk * KS * (int)sizeof(IO);
+  constexpr int GS_BYTES = kChunk * NB * 16, QK_BYTES = 2 * kChunk * KS * (int)sizeof(OP);
   // link quaternions / P, later reused for the transported qh and kh tiles
   __shared__ __align__(16) float gs[(GS_BYTES > QK_BYTES ? GS_BYTES : QK_BYTES) / 4];
   __shared__ __align__(16) float ss[8 * NB * 4];
   __shared__ __align__(16) float cs[NB * 4];
-  __shared__ __align__(16) IO vts[DP * VS];
+  __shared__ __align__(16) OP vts[DP * VS];
 
   const int tid = threadIdx.x;
   const int i = tid / NG, g = tid % NG;
@@ -334,7 +353,7 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   }
   // zero the padded rows of the value tile
   for (int idx = tid; idx < (DP - D) * kChunk; idx += NT)
-    vts[(D + idx / kChunk) * VS + idx % kChunk] = from_f32<IO>(0.f);
+    vts[(D + idx / kChunk) * VS + idx % kChunk] = from_f32<OP>(0.f);
 
   // ---- link quaternions of link t -> LDS ----
   static_for<8>([&](auto j) {
@@ -361,32 +380,37 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
     rot_t_apply(R, vv[3 * j], vv[3 * j + 1], vv[3 * j + 2], y0, y1, y2);
     vv[3 * j] = y0; vv[3 * j + 1] = y1; vv[3 * j + 2] = y2;
   });
+  if constexpr (sizeof(OP) == 2 && !std::is_same<OP, bf16>::value) {
+    float mx = 0.f;
+    static_for<24>([&](auto j) { mx = fmaxf(mx, fmaxf(fabsf(qv[j]), fmaxf(fabsf(kv[j]), fabsf(vv[j])))); });
+    note_range<OP>(a, mx);
+  }
   // ---- stage the three transported tiles in LDS (the P slots are free once
   // every thread has read its own), then write each with whole 16-byte rows
   // per lane: the qh and kh tiles of a chunk are contiguous 64 x DP blocks ----
   __syncthreads();
-  IO* qts = reinterpret_cast<IO*>(gs);
-  IO* kts = qts + kChunk * KS;
-  store_row<IO, 24>(qts + i * KS + 24 * g, qv);
-  store_row<IO, 24>(kts + i * KS + 24 * g, kv);
+  OP* qts = reinterpret_cast<OP*>(gs);
+  OP* kts = qts + kChunk * KS;
+  store_row<OP, 24>(qts + i * KS + 24 * g, qv);
+  store_row<OP, 24>(kts + i * KS + 24 * g, kv);
   if (DP > D && g == NG - 1) {
     float z[DP > D ? DP - D : E];
     static_for<(DP > D ? DP - D : E)>([&](auto j) { z[j] = 0.f; });
     if constexpr (DP > D) {
-      store_row<IO, DP - D>(qts + i * KS + D, z);
-      store_row<IO, DP - D>(kts + i * KS + D, z);
+      store_row<OP, DP - D>(qts + i * KS + D, z);
+      store_row<OP, DP - D>(kts + i * KS + D, z);
     }
   }
-  static_for<24>([&](auto j) { vts[(24 * g + j) * VS + i] = from_f32<IO>(vv[j]); });
+  static_for<24>([&](auto j) { vts[(24 * g + j) * VS + i] = from_f32<OP>(vv[j]); });
   __syncthreads();
-  u32x4* qdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.qh) + (bh * a.Tp + t0) * DP);
-  u32x4* kdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.kh) + (bh * a.Tp + t0) * DP);
+  u32x4* qdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.qh) + (bh * a.Tp + t0) * DP);
+  u32x4* kdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.kh) + (bh * a.Tp + t0) * DP);
   constexpr int KR = DP / E;
   for (int idx = tid; idx < kChunk * KR; idx += NT) {
     qdst[idx] = *reinterpret_cast<const u32x4*>(&qts[(idx / KR) * KS + (idx % KR) * E]);
     kdst[idx] = *reinterpret_cast<const u32x4*>(&kts[(idx / KR) * KS + (idx % KR) * E]);
   }
-  u32x4* vdst = reinterpret_cast<u32x4*>(reinterpret_cast<IO*>(a.vh_t) + (bh * a.nch + c) * DP * kChunk);
+  u32x4* vdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.vh_t) + (bh * a.nch + c) * DP * kChunk);
   constexpr int VR = kChunk / E;
   for (int idx = tid; idx < DP * VR; idx += NT)
     vdst[idx] = *reinterpret_cast<const u32x4*>(&vts[(idx / VR) * VS + (idx % VR) * E]);
@@ -399,7 +423,7 @@ hipError_t launch_chain_reset(void* state, int64_t n_pairs, unsigned* ticket, hi
   return hipGetLastError();
 }
 
-template <typename IO, typename GT>
+template <typename IO, typename OP, typename GT>
 hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
   const int tpb = 256;
   const int64_t n_pairs = (int64_t)a.B * a.H * 2 * a.nch * a.nb * 2;    // 64-bit words of the state
@@ -408,24 +432,26 @@ hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)((int64_t)a.B * a.H * a.nch));
   if (a.wide) {
     switch (a.d) {
-      case 48: hipLaunchKernelGGL((chunk_apply_wide<IO, GT, 2, 64>), grid, dim3(128), 0, s, a); break;
-      case 72: hipLaunchKernelGGL((chunk_apply_wide<IO, GT, 3, 96>), grid, dim3(192), 0, s, a); break;
-      case 96: hipLaunchKernelGGL((chunk_apply_wide<IO, GT, 4, 96>), grid, dim3(256), 0, s, a); break;
+      case 48: hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 2, 64>), grid, dim3(128), 0, s, a); break;
+      case 72: hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 3, 96>), grid, dim3(192), 0, s, a); break;
+      case 96: hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 4, 96>), grid, dim3(256), 0, s, a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
   }
   switch (a.Dp) {
-    case 32: hipLaunchKernelGGL((chunk_apply<IO, GT, 32>), grid, dim3(tpb), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((chunk_apply<IO, GT, 64>), grid, dim3(tpb), 0, s, a); break;
-    case 96: hipLaunchKernelGGL((chunk_apply<IO, GT, 96>), grid, dim3(tpb), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((chunk_apply<IO, OP, GT, 32>), grid, dim3(tpb), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((chunk_apply<IO, OP, GT, 64>), grid, dim3(tpb), 0, s, a); break;
+    case 96: hipLaunchKernelGGL((chunk_apply<IO, OP, GT, 96>), grid, dim3(tpb), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-template hipError_t launch_scan<float, float>(const ScanArgs&, hipStream_t);
-template hipError_t launch_scan<bf16, float>(const ScanArgs&, hipStream_t);
-template hipError_t launch_scan<bf16, bf16>(const ScanArgs&, hipStream_t);
+template hipError_t launch_scan<float, float, float>(const ScanArgs&, hipStream_t);
+template hipError_t launch_scan<bf16, bf16, float>(const ScanArgs&, hipStream_t);
+template hipError_t launch_scan<bf16, bf16, bf16>(const ScanArgs&, hipStream_t);
+template hipError_t launch_scan<bf16, f16, float>(const ScanArgs&, hipStream_t);
+template hipError_t launch_scan<bf16, f16, bf16>(const ScanArgs&, hipStream_t);
 
 }  // namespace holo

@@ -20,6 +20,8 @@ import torch
 from . import _lib
 
 _DT = {torch.float32: _lib.HOLO_F32, torch.bfloat16: _lib.HOLO_BF16}
+# operand types of the transported qh / kh / vh_t (fp16 only between the scan and holo_attn_fwd)
+_OPDT = {**_DT, torch.float16: _lib.HOLO_F16}
 # storage of P: name -> (holo_quat_format, torch dtype of the (B, H, T, nb, 4) tensor)
 _PFMT = {"f32": (_lib.HOLO_QUAT_F32, torch.float32), "snorm16": (_lib.HOLO_QUAT_SNORM16, torch.int16)}
 _MODE = {"causal": _lib.HOLO_MODE_CAUSAL, "inert": _lib.HOLO_MODE_INERT}
@@ -64,7 +66,8 @@ def padded_seq_len(T: int) -> int:
 
 def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor,
               gk: Optional[torch.Tensor], edge_scale: float, want_hol: bool = False,
-              p_format: str = "f32", mode: str = "causal"
+              p_format: str = "f32", mode: str = "causal", op_dtype: Optional[torch.dtype] = None,
+              status: Optional[torch.Tensor] = None
               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """q, k, v: (B,T,H,d) views; gq, gk: (B,T,H,3*nb) views (gk None: gq is the
     full link parameter g and a_t = edge_scale * g_t; gk with strides
@@ -74,7 +77,11 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     Hol (B,H,nb,4) fp32 or None. P is fp32 quaternions (p_format "f32") or
     round(32767 q/|q|) as int16 ("snorm16", half the bytes; the attention
     epilogue uses either, quat_to_dense takes fp32). mode "causal" transports
-    u^ = P^T u, "inert" u' = P u (for attention_masked in inert mode)."""
+    u^ = P^T u, "inert" u' = P u (for attention_masked in inert mode).
+    op_dtype: type of qh/kh/vh_t (default q's dtype; float16 with bfloat16
+    inputs for `attention`'s fp16 operands). status: an int32 device tensor
+    of one element that receives the workspace status word (HOLO_WS_* bits,
+    0 = clean) on the current stream."""
     lib = _lib.load()
     B, T, H, d = k.shape
     nb = d // 3
@@ -93,6 +100,9 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     for name, t in (("gq", gq), ("gk", gk)):
         if t is not None and (t.dtype != gdt or t.device != dev):
             raise ValueError(f"geom_scan: {name} must be {gdt} on {dev}")
+    opdt = dt if op_dtype is None else op_dtype
+    if opdt not in _OPDT or (dt == torch.float32) != (opdt == torch.float32):
+        raise ValueError(f"geom_scan: operand dtype {opdt} with {dt} inputs is not supported")
     q_rs, q_hs = _token_view(q, B, T, H, d, "q")
     k_rs, k_hs = _token_view(k, B, T, H, d, "k")
     v_rs, v_hs = _token_view(v, B, T, H, d, "v")
@@ -101,9 +111,9 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
         raise ValueError("geom_scan: gq must have one row per token")
     gk_rs, gk_hs = (0, 0) if gk is None else _token_view(gk, B, T, H, 3 * nb, "gk")
     Dp, Tp = padded_head_dim(d), padded_seq_len(T)
-    qh = torch.empty((B, H, Tp, Dp), dtype=dt, device=dev)
-    kh = torch.empty((B, H, Tp, Dp), dtype=dt, device=dev)
-    vh_t = torch.empty((B, H, Tp // 64, Dp, 64), dtype=dt, device=dev)
+    qh = torch.empty((B, H, Tp, Dp), dtype=opdt, device=dev)
+    kh = torch.empty((B, H, Tp, Dp), dtype=opdt, device=dev)
+    vh_t = torch.empty((B, H, Tp // 64, Dp, 64), dtype=opdt, device=dev)
     if p_format not in _PFMT:
         raise ValueError(f"geom_scan: p_format must be one of {sorted(_PFMT)}")
     if mode not in _MODE:
@@ -114,31 +124,44 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     rc = lib.holo_geom_scan_fwd(
         B, T, H, d, _lib.HOLO_GEN_DIRECT if gk is None else _lib.HOLO_GEN_ADDITIVE,
-        float(edge_scale), _DT[dt], _DT[gdt], _PFMT[p_format][0], _MODE[mode],
+        float(edge_scale), _DT[dt], _OPDT[opdt], _DT[gdt], _PFMT[p_format][0], _MODE[mode],
         _ptr(gq), gq_rs, gq_hs, _ptr(gk), gk_rs, gk_hs,
         _ptr(q), q_rs, q_hs, _ptr(k), k_rs, k_hs, _ptr(v), v_rs, v_hs,
         _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(hol),
         _ptr(ws), ws_bytes, _stream(dev))
     _lib.check(rc, "holo_geom_scan_fwd")
+    if status is not None:
+        workspace_status(ws, status)
     return qh, kh, vh_t, P, hol
+
+
+def workspace_status(ws: torch.Tensor, status: torch.Tensor) -> None:
+    """Copy the status word of a chained workspace (HOLO_WS_* bits) into
+    `status`, an int32 device tensor of one element, on the current stream."""
+    if status.dtype != torch.int32 or status.numel() != 1 or status.device != ws.device:
+        raise ValueError("workspace_status: status must be a one-element int32 tensor on the workspace's device")
+    rc = _lib.load().holo_workspace_status(_ptr(ws), ws.numel() * ws.element_size(), _ptr(status),
+                                           _stream(ws.device))
+    _lib.check(rc, "holo_workspace_status")
 
 
 def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
               d: int, scale: float, out: Optional[torch.Tensor] = None,
-              lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+              lse: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """qh, kh, vh_t, P from geom_scan for head dimension d.
     Returns o as a (B,T,H,d) tensor (contiguous (B,T,H*d) storage unless
-    `out`, a (B,T,H,d) view, is given). `lse`, a (B, H, Tp) fp32 tensor,
-    receives each query's log2 softmax normaliser (what `attention_backward`
-    needs)."""
+    `out`, a (B,T,H,d) view, is given) of type out_dtype (default: fp32 for
+    fp32 operands, bf16 for 16-bit ones; float32 is allowed with any
+    operands). `lse`, a (B, H, Tp) fp32 tensor, receives each query's log2
+    softmax normaliser (what `attention_backward` needs)."""
     lib = _lib.load()
     if P.dim() != 5:
         raise ValueError("attention: P must be (B, H, T, nb, 4)")
     B, H, T = (int(n) for n in P.shape[:3])
     nb = d // 3
     dev, dt = qh.device, qh.dtype
-    if dev.type != "cuda" or dt not in _DT:
-        raise ValueError(f"attention: qh must be a float32/bfloat16 GPU tensor (got {dt} on {dev})")
+    if dev.type != "cuda" or dt not in _OPDT:
+        raise ValueError(f"attention: qh must be a float32/bfloat16/float16 GPU tensor (got {dt} on {dev})")
     Dp, Tp = padded_head_dim(d), padded_seq_len(T)
     if tuple(qh.shape) != (B, H, Tp, Dp) or not qh.is_contiguous():
         raise ValueError("attention: qh does not match the geom_scan layout")
@@ -152,15 +175,19 @@ def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.T
     for t in (kh, vh_t, P):
         if t.device != dev:
             raise ValueError("attention: all tensors must be on one device")
+    odt = out.dtype if out is not None else out_dtype if out_dtype is not None else \
+        (torch.float32 if dt == torch.float32 else torch.bfloat16)
+    if odt not in _DT or (dt == torch.float32 and odt != torch.float32):
+        raise ValueError(f"attention: output dtype {odt} with {dt} operands is not supported")
     if out is None:
-        out = torch.empty((B, T, H, d), dtype=dt, device=dev)
-    elif out.dtype != dt or out.device != dev:
-        raise ValueError("attention: out must match q's dtype and device")
+        out = torch.empty((B, T, H, d), dtype=odt, device=dev)
+    elif out.device != dev or (out_dtype is not None and out_dtype != out.dtype):
+        raise ValueError("attention: out must be on qh's device (and of out_dtype when both are given)")
     o_rs, o_hs = _token_view(out, B, T, H, d, "out")
     if lse is not None and (tuple(lse.shape) != (B, H, Tp) or lse.dtype != torch.float32
                             or not lse.is_contiguous() or lse.device != dev):
         raise ValueError(f"attention: lse must be a contiguous fp32 {(B, H, Tp)} tensor on {dev}")
-    rc = lib.holo_attn_fwd(B, T, H, d, _DT[dt], pf, float(scale),
+    rc = lib.holo_attn_fwd(B, T, H, d, _OPDT[dt], _DT[odt], pf, float(scale),
                            _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
                            _ptr(out), o_rs, o_hs, _ptr(lse), _stream(dev))
     _lib.check(rc, "holo_attn_fwd")

@@ -69,8 +69,22 @@ typedef enum holo_status {
 
 typedef enum holo_dtype {
   HOLO_F32 = 0,
-  HOLO_BF16 = 1
+  HOLO_BF16 = 1,
+  /* fp16: only as the operand type of the transported qh / kh / vh_t between
+     holo_geom_scan_fwd and holo_attn_fwd on the bf16 path (11-bit
+     significands at the bf16 matrix-core rate; finite range +-65504)       */
+  HOLO_F16 = 2
 } holo_dtype;
+
+/* Bits of a chained workspace's status word (holo_workspace_status).       */
+typedef enum holo_ws_status {
+  /* a chained carry wait ran out of polls (impossible in a conforming
+     launch); the affected outputs were written as NaN                      */
+  HOLO_WS_TIMEOUT = 1,
+  /* holo_geom_scan_fwd: a transported value exceeded the finite range of
+     op_dtype (fp16); it was stored as +-inf                                 */
+  HOLO_WS_OVERFLOW = 2
+} holo_ws_status;
 
 /* Storage of the prefix rotations P (one quaternion per block and token). */
 typedef enum holo_quat_format {
@@ -115,6 +129,16 @@ HOLO_API int64_t holo_padded_seq_len(int64_t T);
 HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
 
 /*
+ * Status word of the last call that used a chained workspace (a
+ * holo_geom_scan_fwd or holo_attn_bwd workspace; its first 256 bytes hold the
+ * ticket counter and this word): copies the 32-bit word, a set of
+ * holo_ws_status bits (0 = clean), into *status, which may be device memory
+ * or pinned host memory, with an asynchronous copy on `stream` (the caller
+ * synchronises before reading a host copy). Diagnostics, not the hot path.
+ */
+HOLO_API int holo_workspace_status(const void* workspace, size_t workspace_bytes, unsigned* status, void* stream);
+
+/*
  * Link rotations, chunked prefix-product scan and key/value transport.
  *
  * Inputs (token-major as the projections produce them):
@@ -126,17 +150,18 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  *            HOLO_GEN_ADDITIVE that gives a_t = edge_scale * (gq_t + c) for a
  *            per-head constant c (e.g. the interaction edge MLP's output bias,
  *            with gq its unbiased output).
- *   q, k, v: dtype `io_dtype`.
- *   q      : like k, v.
+ *   q, k, v: dtype `io_dtype` (HOLO_F32 or HOLO_BF16),
  *            element (b, t, h, c) at ptr[(b*T + t)*row_stride + h*head_stride + c], c < d.
  *   mode   : HOLO_MODE_CAUSAL transports u^ = P^T u (the written formulas);
  *            HOLO_MODE_INERT transports u' = P u instead (the endpoint
  *            transport of inert mode, kernel/attention_fast.py:142-144), for
  *            holo_attn_masked_fwd in that mode.
- * Outputs:
- *   qh   (B, H, Tp, Dp)        io_dtype, qh[t] = P_t^T q_t   (Tp = padded T, Dp = padded d)
- *   kh   (B, H, Tp, Dp)        io_dtype, kh[t] = P_t^T k_t
- *   vh_t (B, H, Tp/64, Dp, 64) io_dtype, key tiles of 64 stored transposed:
+ * Outputs, in `op_dtype` (HOLO_F32 with fp32 inputs; HOLO_BF16 or HOLO_F16
+ * with bf16 inputs: the operand type of the attention call that reads them;
+ * an fp16 value beyond +-65504 is stored as inf and sets HOLO_WS_OVERFLOW):
+ *   qh   (B, H, Tp, Dp)        qh[t] = P_t^T q_t   (Tp = padded T, Dp = padded d)
+ *   kh   (B, H, Tp, Dp)        kh[t] = P_t^T k_t
+ *   vh_t (B, H, Tp/64, Dp, 64) key tiles of 64 stored transposed:
  *                               vh_t[b][h][t/64][c][t%64] = (P_t^T v_t)[c]
  *        Padding (t >= T or c >= d) is written as zero.
  *   P    (B, H, T, nb, 4)      quaternions of the prefix products in `p_format`
@@ -147,10 +172,12 @@ HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
  * product of all earlier chunks, which each chunk's workgroup publishes for
  * the next one in `workspace` (a chained scan): the inputs are read once. The
  * workspace is cleared by the call itself (a fill kernel on `stream`); two
- * calls that share one workspace must not run concurrently.
+ * calls that share one workspace must not run concurrently. Its status word
+ * (holo_workspace_status) reports a carry time-out or an fp16 overflow.
  */
 HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
-                       int gen_mode, float edge_scale, int io_dtype, int gen_dtype, int p_format, int mode,
+                       int gen_mode, float edge_scale, int io_dtype, int op_dtype, int gen_dtype,
+                       int p_format, int mode,
                        const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
                        const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
                        const void* q, int64_t q_row_stride, int64_t q_head_stride,
@@ -161,17 +188,20 @@ HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
 
 /*
  * Causal path-ordered attention on transported queries/keys/values.
- *   qh, kh, vh_t, P : as written by holo_geom_scan_fwd (same B, T, H, d, dtype,
- *                     p_format)
- *   o    : output, element (b, t, h, c) at o[(b*T + t)*o_row_stride + h*o_head_stride + c]
+ *   qh, kh, vh_t, P : as written by holo_geom_scan_fwd (same B, T, H, d,
+ *                     op_dtype, p_format)
+ *   o    : output in `out_dtype`, element (b, t, h, c) at
+ *          o[(b*T + t)*o_row_stride + h*o_head_stride + c]
  *          o_i = P_i * sum_{j<=i} softmax_j(scale * qh_i . kh_j) * vh_j
  *   lse  : optional (null to skip), (B, H, Tp) fp32: per query, log2 of the
  *          softmax normaliser in units of scale*log2(e) times the score (what
  *          holo_attn_bwd recomputes the probabilities from)
- * dtype is the dtype of q, kh, vh_t and o (HOLO_BF16: bf16 MFMA with fp32
- * accumulation and softmax; HOLO_F32: fp32 MFMA throughout).
+ * op_dtype is the type of qh, kh, vh_t and of the softmax weights on the
+ * matrix core: HOLO_BF16 or HOLO_F16 (16-bit MFMA with fp32 accumulation and
+ * softmax) or HOLO_F32 (fp32 MFMA throughout). out_dtype: HOLO_F32, or
+ * HOLO_BF16 with 16-bit operands.
  */
-HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, float scale,
+HOLO_API int holo_attn_fwd(int B, int64_t T, int H, int d, int op_dtype, int out_dtype, int p_format, float scale,
                   const void* qh, const void* kh, const void* vh_t, const void* P,
                   void* o, int64_t o_row_stride, int64_t o_head_stride,
                   float* lse, void* stream);

@@ -300,14 +300,28 @@ def causal_attention64(qh: np.ndarray, kh: np.ndarray, vh: np.ndarray, scale: fl
     out = np.empty_like(qh)
     for i0 in range(0, T, q_block):
         i1 = min(T, i0 + q_block)
-        s = np.einsum("...id,...jd->...ij", qh[..., i0:i1, :], kh[..., :i1, :]) * scale
+        s = np.matmul(qh[..., i0:i1, :], np.swapaxes(kh[..., :i1, :], -1, -2)) * scale
         mask = np.arange(i0, i1)[:, None] >= np.arange(i1)[None, :]
         s = np.where(mask, s, -np.inf)
         s = s - s.max(axis=-1, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=-1, keepdims=True)
-        out[..., i0:i1, :] = np.einsum("...ij,...jd->...id", p, vh[..., :i1, :])
+        out[..., i0:i1, :] = np.matmul(p, vh[..., :i1, :])
     return out
+
+
+def attention_rows64(qh: np.ndarray, kh: np.ndarray, vh: np.ndarray, scale: float,
+                     rows: np.ndarray) -> np.ndarray:
+    """Rows `rows` (query positions) of causal_attention64: query i attends to
+    keys 0..i. qh, kh, vh (..., T, d) float64 -> (..., len(rows), d)."""
+    rows = np.asarray(rows)
+    i1 = int(rows.max()) + 1
+    s = np.matmul(qh[..., rows, :], np.swapaxes(kh[..., :i1, :], -1, -2)) * scale
+    s = np.where(rows[:, None] >= np.arange(i1)[None, :], s, -np.inf)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.matmul(p, vh[..., :i1, :])
 
 
 def ring_mask(T: int) -> np.ndarray:

@@ -23,6 +23,8 @@ import importlib.util
 import os
 import sys
 
+sys.dont_write_bytecode = True      # write nothing into the read-only reference tree
+
 import numpy as np
 import torch
 

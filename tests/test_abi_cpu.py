@@ -45,24 +45,26 @@ def test_exported_symbols_are_exactly_the_abi():
 
 
 def test_version_and_layout_queries(lib):
-    assert lib.holo_abi_version() >> 16 >= 2
+    assert lib.holo_abi_version() >> 16 >= 6
     assert [lib.holo_padded_head_dim(d) for d in (1, 12, 32, 33, 48, 96)] == [32, 32, 32, 64, 64, 96]
     assert [lib.holo_padded_seq_len(t) for t in (1, 64, 65, 2048)] == [64, 64, 128, 2048]
-    # chained-scan state: fp32 quaternions for every chunk product and every
-    # chunk inclusive prefix per (b, h, block), then 256 bytes for the ticket
-    # counter and flag
+    # chained-scan workspace: 256 bytes for the ticket counter and status word,
+    # then fp32 quaternions for every chunk product and every chunk inclusive
+    # prefix per (b, h, block)
     assert lib.holo_geom_scan_workspace_size(16, 2048, 16, 96) == 16 * 16 * 2 * 32 * 32 * 16 + 256
     assert lib.holo_geom_scan_workspace_size(1, 1, 1, 2) == 256
     assert lib.holo_geom_scan_workspace_size(0, 2048, 16, 96) == 0
 
 
 def _scan(lib, **kw):
-    args = dict(B=1, T=8, H=2, d=12, gen=0, es=0.1, io=_lib.HOLO_F32, gdt=_lib.HOLO_F32, pf=_lib.HOLO_QUAT_F32,
+    args = dict(B=1, T=8, H=2, d=12, gen=0, es=0.1, io=_lib.HOLO_F32, op=_lib.HOLO_F32, gdt=_lib.HOLO_F32,
+                pf=_lib.HOLO_QUAT_F32,
                 mode=_lib.HOLO_MODE_CAUSAL, gq=16, gk=16, q=16, k=16, v=16, qh=16, kh=16, vh=16, P=16, hol=None, ws=16, wsb=1 << 20,
                 rs=64, hs=24)
     args.update(kw)
     a = args
-    return lib.holo_geom_scan_fwd(a["B"], a["T"], a["H"], a["d"], a["gen"], a["es"], a["io"], a["gdt"], a["pf"],
+    return lib.holo_geom_scan_fwd(a["B"], a["T"], a["H"], a["d"], a["gen"], a["es"], a["io"], a["op"], a["gdt"],
+                                  a["pf"],
                                   a["mode"], a["gq"], a["rs"], a["hs"], a["gk"], a["rs"], a["hs"],
                                   a["q"], a["rs"], a["hs"], a["k"], a["rs"], a["hs"], a["v"], a["rs"], a["hs"],
                                   a["qh"], a["kh"], a["vh"], a["P"], a["hol"], a["ws"], a["wsb"], None)
@@ -76,6 +78,9 @@ def test_scan_argument_validation(lib):
     assert _scan(lib, pf=2) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, mode=2) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, io=_lib.HOLO_F32, gdt=_lib.HOLO_BF16) == _lib.HOLO_ERR_UNSUPPORTED
+    assert _scan(lib, op=_lib.HOLO_F16) == _lib.HOLO_ERR_INVALID_ARG            # fp32 inputs: fp32 operands
+    assert _scan(lib, io=_lib.HOLO_BF16, op=_lib.HOLO_F32) == _lib.HOLO_ERR_INVALID_ARG
+    assert _scan(lib, io=_lib.HOLO_BF16, op=9) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, k=None) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, gen=_lib.HOLO_GEN_ADDITIVE, gk=None) == _lib.HOLO_ERR_INVALID_ARG
     assert _scan(lib, gen=_lib.HOLO_GEN_DIRECT) == _lib.HOLO_ERR_INVALID_ARG      # gk given
@@ -86,17 +91,27 @@ def test_scan_argument_validation(lib):
 
 
 def test_attention_argument_validation(lib):
-    f = lib.holo_attn_fwd
-    assert f(1, 0, 1, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_BAD_SHAPE
-    assert f(1, 8, 1, 120, 0, 0, 0.3, 16, 16, 16, 16, 16, 120, 120, None, None) == _lib.HOLO_ERR_UNSUPPORTED
-    assert f(1, 8, 1, 12, 0, 0, 0.0, 16, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 1, 12, 0, 0, 0.3, None, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 2, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 4, None, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 1, 12, 5, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_INVALID_ARG
-    assert f(1, 8, 1, 12, 0, 3, 0.3, 16, 16, 16, 16, 16, 12, 12, None, None) == _lib.HOLO_ERR_INVALID_ARG
+    F32, BF16, F16 = _lib.HOLO_F32, _lib.HOLO_BF16, _lib.HOLO_F16
+
+    def f(B, T, H, d, op, out, pf, sc, qh, kh, vh, P, o, rs, hs, lse):
+        return lib.holo_attn_fwd(B, T, H, d, op, out, pf, sc, qh, kh, vh, P, o, rs, hs, lse, None)
+    assert f(1, 0, 1, 12, F32, F32, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_BAD_SHAPE
+    assert f(1, 8, 1, 120, F32, F32, 0, 0.3, 16, 16, 16, 16, 16, 120, 120, None) == _lib.HOLO_ERR_UNSUPPORTED
+    assert f(1, 8, 1, 12, F32, F32, 0, 0.0, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, F32, F32, 0, 0.3, None, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 2, 12, F32, F32, 0, 0.3, 16, 16, 16, 16, 16, 12, 4, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, 5, F32, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, F32, BF16, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, F16, F16, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, F32, F32, 3, 0.3, 16, 16, 16, 16, 16, 12, 12, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(1, 8, 1, 12, F32, F32, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, 8) == _lib.HOLO_ERR_INVALID_ARG   # lse misaligned
 
 
-    assert f(1, 8, 1, 12, 0, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, 8, None) == _lib.HOLO_ERR_INVALID_ARG   # lse misaligned
+def test_workspace_status_validation(lib):
+    st = lib.holo_workspace_status
+    assert st(None, 1024, 16, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert st(16, 1024, None, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert st(16, 4, 16, None) == _lib.HOLO_ERR_WORKSPACE
 
 
 def _bwd(lib, **kw):
@@ -216,6 +231,7 @@ def test_masked_attention_argument_validation(lib):
     assert _masked(lib, d=120) == _lib.HOLO_ERR_UNSUPPORTED
     assert _masked(lib, mode=2) == _lib.HOLO_ERR_INVALID_ARG
     assert _masked(lib, dt=3) == _lib.HOLO_ERR_INVALID_ARG
+    assert _masked(lib, dt=_lib.HOLO_F16) == _lib.HOLO_ERR_INVALID_ARG   # the exact path takes bf16 / fp32
     assert _masked(lib, pf=5) == _lib.HOLO_ERR_INVALID_ARG
     assert _masked(lib, hol=None) == _lib.HOLO_ERR_INVALID_ARG            # causal mode needs the holonomy
     assert _masked(lib, mrs=7) == _lib.HOLO_ERR_INVALID_ARG               # mask rows shorter than T

@@ -4,8 +4,14 @@ holo_attn_fwd (causal, tril) and holo_attn_masked_fwd (ring mask), fp32,
 against the float64 oracle on the same inputs; the driver also checks the
 error path (status code and message of a bad call).
 
+The driver also runs the C binding INTEGRATION.md shows
+(tests/c/integration_example.c: the bf16 path with fp16 operands, o in fp32)
+on the same q, k, v rounded to bf16.
+
 Tolerance (written in the test): fp32 max-abs <= 2e-5 (the fp32 bar; the ring
-mask's wrap branch carries the holonomy, a product of all T links).
+mask's wrap branch carries the holonomy, a product of all T links); the bf16
+path's per-head o max-abs <= 2e-3 against the oracle on the bf16-rounded
+inputs (the bf16 bar).
 """
 from __future__ import annotations
 
@@ -15,6 +21,7 @@ import subprocess
 
 import numpy as np
 import pytest
+import torch
 
 from holonomyawareattention_amd import build as _build
 from oracle import holo_ref as R
@@ -50,5 +57,12 @@ def test_c_caller_matches_oracle(tmp_path):
     ref_ring = R.exact_attention64(qq, kk, vv, P, Hol, scale, R.ring_mask(T), "causal")
     err_tril = np.abs(o_tril - ref_tril.transpose(0, 2, 1, 3)).max()
     err_ring = np.abs(o_ring - ref_ring.transpose(0, 2, 1, 3)).max()
-    print(f"max-abs: tril {err_tril:.3e}, ring {err_ring:.3e}")
+    o_bf16 = np.fromfile(tmp_path / "o_bf16.f32", dtype=np.float32).reshape(B, T, H, d).astype(np.float64)
+    rb = lambda a: torch.as_tensor(a).to(torch.bfloat16).double().numpy()
+    qb, kb, vb = (rb(u) for u in (qq, kk, vv))
+    ref_bf16 = R.apply_blocks(P, R.causal_attention64(R.apply_blocks_T(P, qb), R.apply_blocks_T(P, kb),
+                                                      R.apply_blocks_T(P, vb), scale))
+    err_bf16 = np.abs(o_bf16 - ref_bf16.transpose(0, 2, 1, 3)).max()
+    print(f"max-abs: tril {err_tril:.3e}, ring {err_ring:.3e}, bf16 binding {err_bf16:.3e}")
     assert err_tril <= 2e-5 and err_ring <= 2e-5
+    assert err_bf16 <= 2e-3

@@ -1,20 +1,27 @@
-"""Incremental decode on the GPU against the full-sequence forward.
+"""Incremental decode on the GPU against the fp64 oracle and the
+full-sequence forward.
 
 Row t of the causal forward depends on tokens 0..t only (the edge t-1 -> t
 uses x_{t-1} and x_t; the closing edge only enters the holonomy), so
 prefill(x[:, :T0]) followed by decode_step on tokens T0..T-1 must reproduce
-forward(x)[:, T0:T]. Tolerances (written in each test): fp32 2e-5 max-abs
-(P_t composed step by step instead of in chunks, attention summed per
-256-key segment); bf16 2e-2 max-abs, since the decode attention keeps the
-softmax weights in fp32 where the full-sequence kernel rounds them to bf16
-for its PV MFMA (one bf16 rounding, |y| ~ 1).
+the oracle's forward (oracle.holo_ref.forward_blocks on the same rounded
+inputs) at rows T0..T-1, and the GPU's own full forward there.
+Tolerances (written in each test): fp32 2e-5 max-abs (P_t composed step by
+step instead of in chunks, attention summed per 256-key segment); bf16
+against the oracle the y-level bound of the other bf16 tests (2.5e-2 *
+max(1, max|y|/4)), against the GPU forward 2e-2 (the decode attention keeps
+the softmax weights in fp32 where the full-sequence kernel rounds them to
+16 bits for its PV MFMA).
 """
 from __future__ import annotations
 
 import pytest
 import torch
 
+import numpy as np
+
 from holonomyawareattention_amd import kernels
+from oracle import holo_ref as R
 from tests._util import layer, make_module, run_module
 
 pytestmark = pytest.mark.gpu
@@ -25,6 +32,10 @@ def _tol(dtype):
     return 2e-5 if dtype == torch.float32 else 2e-2
 
 
+def _oracle_tol(dtype, y_ref):
+    return 2e-5 if dtype == torch.float32 else 2.5e-2 * max(1.0, np.abs(y_ref).max() / 4)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("lm", ["additive", "interaction"])
 def test_decode_matches_full_forward(dtype, lm):
@@ -32,16 +43,19 @@ def test_decode_matches_full_forward(dtype, lm):
     x, W = layer(40, B, T, D, H, lm, dtype=dtype)
     m = make_module(W, D, H, es, lm, dtype, DEV)
     y_full, _ = run_module(m, x, DEV, dtype)
+    y_ref = R.forward_blocks(x, W, H, es, lm)
     xt = torch.as_tensor(x).to(DEV, dtype)
     y0, st = m.prefill(xt[:, :T0], capacity=T)
     assert (y0.float() - y_full[:, :T0].float()).abs().max().item() <= _tol(dtype)
-    worst = 0.0
+    worst, worst_ref = 0.0, 0.0
     for t in range(T0, T):
         yt = m.decode_step(xt[:, t:t + 1], st)
         worst = max(worst, (yt[:, 0].float() - y_full[:, t].float()).abs().max().item())
+        worst_ref = max(worst_ref, np.abs(yt[:, 0].double().cpu().numpy() - y_ref[:, t]).max())
     torch.cuda.synchronize()
     assert st.t == T
     assert worst <= _tol(dtype), worst
+    assert worst_ref <= _oracle_tol(dtype, y_ref[:, T0:]), worst_ref
 
 
 def test_decode_cache_matches_scan():
@@ -72,13 +86,16 @@ def test_decode_many_segments_bf16():
     x, W = layer(42, B, T, D, H, "additive", dtype=torch.bfloat16)
     m = make_module(W, D, H, es, "additive", torch.bfloat16, DEV)
     y_full, _ = run_module(m, x, DEV, torch.bfloat16)
+    y_ref = R.forward_blocks(x, W, H, es, "additive")
     xt = torch.as_tensor(x).to(DEV, torch.bfloat16)
     _, st = m.prefill(xt[:, :T0])
-    worst = 0.0
+    worst, worst_ref = 0.0, 0.0
     for t in range(T0, T):
         yt = m.decode_step(xt[:, t:t + 1], st)
         worst = max(worst, (yt[:, 0].float() - y_full[:, t].float()).abs().max().item())
+        worst_ref = max(worst_ref, np.abs(yt[:, 0].double().cpu().numpy() - y_ref[:, t]).max())
     assert worst <= 2e-2, worst
+    assert worst_ref <= _oracle_tol(torch.bfloat16, y_ref[:, T0:]), worst_ref
 
 
 def test_decode_from_one_token_fp32():
@@ -86,12 +103,14 @@ def test_decode_from_one_token_fp32():
     x, W = layer(43, B, T, D, H, "additive", dtype=torch.float32)
     m = make_module(W, D, H, es, "additive", torch.float32, DEV)
     y_full, _ = run_module(m, x, DEV, torch.float32)
+    y_ref = R.forward_blocks(x, W, H, es, "additive")
     xt = torch.as_tensor(x).to(DEV, torch.float32)
     y0, st = m.prefill(xt[:, :1], capacity=64)
     assert (y0[:, 0] - y_full[:, 0]).abs().max().item() <= 2e-5
     for t in range(1, T):
         yt = m.decode_step(xt[:, t:t + 1], st)
         assert (yt[:, 0] - y_full[:, t]).abs().max().item() <= 2e-5, t
+        assert np.abs(yt[:, 0].double().cpu().numpy() - y_ref[:, t]).max() <= 2e-5, t
     with pytest.raises(ValueError):
         st.t = st.capacity
         m.decode_step(xt[:, :1], st)

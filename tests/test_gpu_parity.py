@@ -3,13 +3,14 @@
 Tolerances (written in each test):
   fp32 path   -- end to end <= 1e-5 max-abs against the reference fp32
                  forward at config 1; stage outputs within fp32 rounding.
-  bf16 path   -- the inputs the oracle sees are the bf16-rounded x and weights;
-                 the kernel path additionally rounds q/k/v (projection output),
-                 the transported qh/kh/vh, the softmax weights (PV MFMA operand)
-                 and o (out-projection operand) to bf16. Each of these alone
-                 moves y by up to ~7e-3 where |o| ~ 3.5 (the first positions,
-                 which attend to one or two keys), so the bound is
-                 max-abs <= 2.5e-2, rms <= 1e-3 and relative Frobenius <= 1e-2.
+  bf16 path   -- end-to-end y against the fp64 oracle on the bf16-rounded x
+                 and weights: the path additionally rounds q/k/v (projection
+                 output) and o (out-projection operand) to bf16 and y itself
+                 is stored in bf16 (half an ulp is up to 7.8e-3 at |y| = 4), so
+                 the y-level bound is max-abs <= 2.5e-2, rms <= 1e-3 and
+                 relative Frobenius <= 1e-2. The 2e-3 bar is held where bf16
+                 storage does not mask it: the per-head output o in fp32
+                 (test_gpu_parity_bar.py).
 """
 from __future__ import annotations
 
@@ -91,9 +92,12 @@ def test_scan_stage(dtype, B, T, D, H, es):
             assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-3)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32])
 @pytest.mark.parametrize("B,T,D,H", [(2, 300, 192, 2), (1, 129, 96, 2), (1, 7, 48, 4), (2, 200, 64, 2)])
 def test_attention_stage(dtype, B, T, D, H):
+    """fp32 attention on the exact qh, kh, vh, P it consumed (the 16-bit
+    operand types are held to their derived rounding bound in
+    test_gpu_parity_bar.py)."""
     es = 0.5
     x, W = layer(22, B, T, D, H, dtype=dtype)
     d = D // H
@@ -110,11 +114,7 @@ def test_attention_stage(dtype, B, T, D, H):
     o_ref = np.einsum("bhtij,bhtj->bhti", Pb, oh).transpose(0, 2, 1, 3)
     got = _np(o)
     err = np.abs(got - o_ref)
-    if dtype == torch.float32:
-        assert err.max() < 1e-5 * max(1.0, np.abs(o_ref).max())
-    else:   # softmax weights rounded to bf16 for the PV MFMA and o stored in bf16
-        assert err.max() < 2e-2
-        assert np.sqrt((err ** 2).mean()) < 1e-2 * np.sqrt((o_ref ** 2).mean())
+    assert err.max() < 1e-5 * max(1.0, np.abs(o_ref).max())
 
 
 GOLDEN_CASES = ["tiny_additive_es005_f64", "tiny_additive_es15_f64", "tiny_interaction_es15_f64",
