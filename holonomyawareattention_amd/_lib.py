@@ -26,6 +26,8 @@ HOLO_F16 = 2
 HOLO_WS_TIMEOUT = 1
 HOLO_WS_OVERFLOW = 2
 
+HOLO_SCAN_STATIC_SCRATCH_BYTES = 32 << 20   # holo_geom_scan_fwd_static's per-device state array
+
 HOLO_GEN_ADDITIVE = 0
 HOLO_GEN_DIRECT = 1
 
@@ -51,6 +53,9 @@ SIGNATURES = [
     ("holo_geom_scan_fwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I, _I, _I,
                                 _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L,
                                 _P, _P, _P, _P, _P, _P, _S, _P]),
+    ("holo_geom_scan_fwd_static", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I, _I, _I,
+                                       _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L, _P, _L, _L,
+                                       _P, _P, _P, _P, _P, _P]),
     ("holo_attn_fwd", _I, [_I, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _L, _L, _P, _P]),
     ("holo_attn_masked_workspace_size", _S, [_I, _L, _I, _I, _I, _I, _I]),
     ("holo_attn_masked_fwd", _I, [_I, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _L,

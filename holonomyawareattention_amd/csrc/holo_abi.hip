@@ -3,6 +3,7 @@
 // allocates device memory or synchronises the host.
 #include <cstdio>
 #include <cstdarg>
+#include <mutex>
 #include <string>
 
 #include "holo_kernels.h"
@@ -509,3 +510,66 @@ int holo_decode_attn_fwd(int B, int H, int d, int64_t t, int64_t capacity, int d
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// holo_geom_scan_fwd_static: the scan with its chained state in a static
+// device array instead of a caller workspace, for callers that cannot
+// allocate (graph capture, serving loops). One array per device, held until
+// the process ends; every call on a device shares it, so calls that overlap
+// in time on one device race. The scan's own reset kernel clears the state
+// and the ticket counter at the start of every call.
+namespace {
+
+constexpr size_t kScratchBytes = HOLO_SCAN_STATIC_SCRATCH_BYTES;
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices];   // device address of `scratch`, per device
+
+// Device address of the current device's `scratch` (the host-side symbol is
+// only a stand-in for it), resolved once per device with that device current.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(HOLO_ERR_UNSUPPORTED, "device %d beyond the %d devices the static scratch tracks", dev,
+                kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(HOLO_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HOLO_OK;
+}
+
+}  // namespace
+
+extern "C" int holo_geom_scan_fwd_static(int B, int64_t T, int H, int d,
+                                         int gen_mode, float edge_scale, int io_dtype, int op_dtype, int gen_dtype,
+                                         int p_format, int mode,
+                                         const void* gq, int64_t gq_rs, int64_t gq_hs,
+                                         const void* gk, int64_t gk_rs, int64_t gk_hs,
+                                         const void* q, int64_t q_rs, int64_t q_hs,
+                                         const void* k, int64_t k_rs, int64_t k_hs,
+                                         const void* v, int64_t v_rs, int64_t v_hs,
+                                         void* qh, void* kh, void* vh_t, float* P, float* hol, void* stream) {
+  g_last_error.clear();
+  const size_t need = holo_geom_scan_workspace_size(B, T, H, d);
+  if (need > kScratchBytes)
+    return fail(HOLO_ERR_UNSUPPORTED,
+                "B=%d T=%lld H=%d d=%d needs %zu bytes of chained scan state, above the %zu-byte static scratch "
+                "(holo_geom_scan_fwd takes a caller workspace of any size)",
+                B, (long long)T, H, d, need, kScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return holo_geom_scan_fwd(B, T, H, d, gen_mode, edge_scale, io_dtype, op_dtype, gen_dtype, p_format, mode,
+                            gq, gq_rs, gq_hs, gk, gk_rs, gk_hs, q, q_rs, q_hs, k, k_rs, k_hs, v, v_rs, v_hs,
+                            qh, kh, vh_t, P, hol, ws, kScratchBytes, stream);
+}

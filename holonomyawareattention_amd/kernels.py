@@ -67,7 +67,7 @@ def padded_seq_len(T: int) -> int:
 def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor,
               gk: Optional[torch.Tensor], edge_scale: float, want_hol: bool = False,
               p_format: str = "f32", mode: str = "causal", op_dtype: Optional[torch.dtype] = None,
-              status: Optional[torch.Tensor] = None
+              status: Optional[torch.Tensor] = None, static_scratch: bool = False
               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """q, k, v: (B,T,H,d) views; gq, gk: (B,T,H,3*nb) views (gk None: gq is the
     full link parameter g and a_t = edge_scale * g_t; gk with strides
@@ -81,7 +81,10 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     op_dtype: type of qh/kh/vh_t (default q's dtype; float16 with bfloat16
     inputs for `attention`'s fp16 operands). status: an int32 device tensor
     of one element that receives the workspace status word (HOLO_WS_* bits,
-    0 = clean) on the current stream."""
+    0 = clean) on the current stream. static_scratch: run
+    holo_geom_scan_fwd_static, whose chained state lives in the library's
+    per-device static array (no workspace; inputs whose state exceeds it
+    raise NotImplementedError; calls that overlap on one device race)."""
     lib = _lib.load()
     B, T, H, d = k.shape
     nb = d // 3
@@ -120,6 +123,17 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
         raise ValueError(f"geom_scan: mode must be one of {sorted(_MODE)}")
     P = torch.empty((B, H, T, nb, 4), dtype=_PFMT[p_format][1], device=dev)
     hol = torch.empty((B, H, nb, 4), dtype=torch.float32, device=dev) if want_hol else None
+    if static_scratch:
+        if status is not None:
+            raise ValueError("geom_scan: the static scratch has no status query")
+        rc = lib.holo_geom_scan_fwd_static(
+            B, T, H, d, _lib.HOLO_GEN_DIRECT if gk is None else _lib.HOLO_GEN_ADDITIVE,
+            float(edge_scale), _DT[dt], _OPDT[opdt], _DT[gdt], _PFMT[p_format][0], _MODE[mode],
+            _ptr(gq), gq_rs, gq_hs, _ptr(gk), gk_rs, gk_hs,
+            _ptr(q), q_rs, q_hs, _ptr(k), k_rs, k_hs, _ptr(v), v_rs, v_hs,
+            _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(hol), _stream(dev))
+        _lib.check(rc, "holo_geom_scan_fwd_static")
+        return qh, kh, vh_t, P, hol
     ws_bytes = int(lib.holo_geom_scan_workspace_size(B, T, H, d))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     rc = lib.holo_geom_scan_fwd(

@@ -187,6 +187,30 @@ HOLO_API int holo_geom_scan_fwd(int B, int64_t T, int H, int d,
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * holo_geom_scan_fwd_static: holo_geom_scan_fwd (same arguments, same
+ * results) with its chained scan state in a static device array of
+ * HOLO_SCAN_STATIC_SCRATCH_BYTES per device instead of a caller workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation); it calls no allocating routine. Inputs whose state
+ * (holo_geom_scan_workspace_size) exceeds the array are rejected with
+ * HOLO_ERR_UNSUPPORTED. Every call on a device shares that device's array:
+ * calls that overlap in time on one device race (the state is cleared at the
+ * start of each call, on `stream`). The array's address is resolved on the
+ * first call on each device, with that device current.
+ */
+#define HOLO_SCAN_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
+HOLO_API int holo_geom_scan_fwd_static(int B, int64_t T, int H, int d,
+                       int gen_mode, float edge_scale, int io_dtype, int op_dtype, int gen_dtype,
+                       int p_format, int mode,
+                       const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
+                       const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
+                       const void* q, int64_t q_row_stride, int64_t q_head_stride,
+                       const void* k, int64_t k_row_stride, int64_t k_head_stride,
+                       const void* v, int64_t v_row_stride, int64_t v_head_stride,
+                       void* qh, void* kh, void* vh_t, float* P, float* hol, void* stream);
+
+/*
  * Causal path-ordered attention on transported queries/keys/values.
  *   qh, kh, vh_t, P : as written by holo_geom_scan_fwd (same B, T, H, d,
  *                     op_dtype, p_format)
