@@ -577,7 +577,10 @@ def main():
     else:                                   # qkv + out, and the edge MLP 2D -> 4D -> H*m
         fl_proj = 2.0 * B * T * D * 4 * D + 2.0 * B * T * (2 * D * 4 * D + 4 * D * m_total)
     io_bytes = 2 if dt == torch.bfloat16 else 4
-    greads = 2 if args.link == "additive" else 1
+    # generator bytes the scan reads per token-head: one fp32 row of g when the
+    # fused projection GEMM formed g_t = gq(x_t) + gk(x_{t+1}) (or the edge MLP
+    # wrote it), two (gq and gk) otherwise
+    greads = 1 if (args.link != "additive" or m._fused_projection_ok(x)) else 2
     scan_bytes = scan_bytes_per_token_head(d, io_bytes, quat_bytes=qbytes, gen_reads=greads) * B * T * H
     core_peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
     core_tflops = fl_core / (stage_ms[2] * 1e-3) / 1e12

@@ -214,15 +214,32 @@ class PathOrderedGeometricMHA(nn.Module):
             self._wcat_src = tuple(_Verified(w, (w.dtype, w.device, tuple(w.shape))) for w in ws)
         return self._wcat
 
-    def _link_inputs(self, x: torch.Tensor):
+    def _fused_projection_ok(self, x: torch.Tensor) -> bool:
+        """holo_qkvg_proj_fwd's conditions: bf16, additive generator, K a
+        multiple of 64, output widths multiples of 4, 16-byte aligned rows."""
+        D = x.shape[-1]
+        ws = (self.qkv.weight, self.gqproj.weight, self.gkproj.weight)
+        return (x.dtype == torch.bfloat16 and self.link_mode == "additive" and D % 64 == 0
+                and (self.h * self.m_dim) % 4 == 0 and self.h * self.m_dim > 0 and x.stride(-1) == 1
+                and x.data_ptr() % 16 == 0 and all(w.dtype == torch.bfloat16 and w.is_contiguous()
+                                                   and w.data_ptr() % 16 == 0 for w in ws))
+
+    def _link_inputs(self, x: torch.Tensor, fused: bool = False):
         """q, k, v views (B,L,H,d) and generator views gq, gk (B,L,H,m).
 
         The generator leaves the GEMM in fp32 whatever x's dtype: link angle
         errors accumulate along the path, so the link parameters are never
         rounded to bf16 (additive: one extra GEMM with an fp32 output;
-        interaction: the edge MLP's last layer)."""
+        interaction: the edge MLP's last layer). fused=True (bf16, additive)
+        runs q/k/v and the generator as one hand-written GEMM
+        (holo_qkvg_proj_fwd) that returns gq = g_t = gq(x_t) + gk(x_{t+1})
+        and gk = None: the scan's direct mode, a_t = edge_scale * g_t."""
         B, L, D = x.shape
         H, d, m = self.h, self.d, self.m_dim
+        if fused and self._fused_projection_ok(x):
+            qkv, g = kernels.qkvg_projection(x, self.qkv.weight, self.gqproj.weight, self.gkproj.weight)
+            qkv = qkv.view(B, L, H, 3 * d)
+            return qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], g.view(B, L, H, m), None
         x2 = x.reshape(B * L, D)
         if self.link_mode == "additive":
             if x.dtype == torch.float32:
@@ -331,7 +348,7 @@ class PathOrderedGeometricMHA(nn.Module):
         with torch.no_grad():
             if ev is not None:
                 ev[0].record()
-            q, k, v, gq, gk = self._link_inputs(x)
+            q, k, v, gq, gk = self._link_inputs(x, fused=True)
             if ev is not None:
                 ev[1].record()
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
@@ -367,7 +384,7 @@ class PathOrderedGeometricMHA(nn.Module):
         with torch.no_grad():
             if ev is not None:
                 ev[0].record()
-            q, k, v, gq, gk = self._link_inputs(x)
+            q, k, v, gq, gk = self._link_inputs(x, fused=True)
             if ev is not None:
                 ev[1].record()
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,

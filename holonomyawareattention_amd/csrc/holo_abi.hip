@@ -92,6 +92,43 @@ int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
 int64_t holo_padded_seq_len(int64_t T) { return holo::padded_seq(T); }
 
+int holo_qkvg_proj_fwd(int64_t M, int64_t T, int K, int n_qkv, int n_gen,
+                       const void* x, int64_t x_rs, const void* w_qkv, const void* w_gq, const void* w_gk,
+                       void* qkv, int64_t qkv_rs, float* g, int64_t g_rs, void* stream) {
+  g_last_error.clear();
+  if (M <= 0 || T <= 0 || K <= 0 || n_qkv < 0 || n_gen < 0 || n_qkv + n_gen == 0)
+    return fail(HOLO_ERR_BAD_SHAPE, "M, T, K must be positive, n_qkv, n_gen >= 0, not both 0 (got %lld, %lld, %d, %d, %d)",
+                (long long)M, (long long)T, K, n_qkv, n_gen);
+  if (M % T != 0) return fail(HOLO_ERR_BAD_SHAPE, "M = %lld is not a whole number of sequences of T = %lld",
+                              (long long)M, (long long)T);
+  if (K % 64 != 0 || n_qkv % 4 != 0 || n_gen % 4 != 0)
+    return fail(HOLO_ERR_UNSUPPORTED, "K = %d must be a multiple of 64 and n_qkv = %d, n_gen = %d multiples of 4",
+                K, n_qkv, n_gen);
+  if (!x || (n_qkv > 0 && (!w_qkv || !qkv)) || (n_gen > 0 && (!w_gq || !w_gk || !g)))
+    return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if (!aligned16(x) || (n_qkv > 0 && (!aligned16(w_qkv) || !aligned16(qkv))) ||
+      (n_gen > 0 && (!aligned16(w_gq) || !aligned16(w_gk) || !aligned16(g))))
+    return fail(HOLO_ERR_INVALID_ARG, "x, weights, qkv and g must be 16-byte aligned");
+  if (x_rs < K || x_rs % 8 != 0 || (n_qkv > 0 && (qkv_rs < n_qkv || qkv_rs % 8 != 0)) ||
+      (n_gen > 0 && (g_rs < n_gen || g_rs % 4 != 0)))
+    return fail(HOLO_ERR_INVALID_ARG, "row strides (x %lld, qkv %lld, g %lld) too small or misaligned",
+                (long long)x_rs, (long long)qkv_rs, (long long)g_rs);
+  // buffer loads address each operand with 32-bit byte offsets
+  if (M * x_rs * 2 > 0x7fffffff || (int64_t)(n_qkv > n_gen ? n_qkv : n_gen) * K * 2 > 0x7fffffff)
+    return fail(HOLO_ERR_UNSUPPORTED, "operands above 2 GiB (M = %lld, K = %d)", (long long)M, K);
+  holo::QkvgArgs a;
+  a.M = M; a.T = T; a.K = K; a.n_qkv = n_qkv; a.n_gen = n_gen;
+  a.tm = (int)((M + 255) / 256); a.tnq = (n_qkv + 255) / 256; a.tng = (n_gen + 255) / 256;
+  a.x = static_cast<const holo::bf16*>(x); a.ldx = x_rs;
+  a.wq = static_cast<const holo::bf16*>(w_qkv);
+  a.wg0 = static_cast<const holo::bf16*>(w_gq); a.wg1 = static_cast<const holo::bf16*>(w_gk);
+  a.qkv = static_cast<holo::bf16*>(qkv); a.ldq = qkv_rs;
+  a.g = g; a.ldg = g_rs;
+  const hipError_t e = holo::launch_qkvg(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "projection GEMM launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
 size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d) {
   if (B <= 0 || T <= 0 || H <= 0 || d <= 0) return 0;
   return holo::scan_state_bytes(B, T, H, d);

@@ -336,16 +336,6 @@ template <int NCK> __device__ __forceinline__ int k_swz(int r) {
 // chunk XOR of V^T row r (8 chunks per row); low five bits only
 __device__ __forceinline__ int v_swz(int r) { return ((r & 7) ^ ((r >> 3) & 3)) & 7; }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-template <int N> __device__ __forceinline__ void wait_vmem() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void ring_barrier() {
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 template <typename OPT, typename OT, int DP, bool PQ16>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
 attn_fwd_h16(AttnArgs a) {

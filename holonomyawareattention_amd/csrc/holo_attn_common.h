@@ -87,6 +87,19 @@ template <typename T, int DP> struct AttnCfg {
   static_assert((kStage * sizeof(T)) % 16 == 0, "stages must stay 16-byte aligned");
 };
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Wait until at most N of this wave's vector memory operations (including
+// buffer loads that write LDS) are outstanding.
+template <int N> __device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Workgroup barrier that also orders the LDS accesses around it for the compiler.
+__device__ __forceinline__ void ring_barrier() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Largest dynamic LDS a workgroup may use on gfx950, and the device ids the
 // opt-in below tracks.
 constexpr int kMaxDynamicLds = 160 * 1024;

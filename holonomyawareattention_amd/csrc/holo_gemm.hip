@@ -1,0 +1,274 @@
+// Projections of the layer on gfx950 MFMA: one GEMM for the per-head
+// interleaved q/k/v columns and the additive link generator.
+//
+// Reference behaviour (core/attention_fast_chunked.py):
+//   qkv = x W_qkv^T                                   :69-71 (bf16 out here)
+//   g_t = gq(x_t) + gk(x_{(t+1) mod T})               :80-84 (before edge_scale)
+// The generator output never exists in two halves: its tiles run a second
+// K segment over the token rows shifted by one position (wrapping inside each
+// sequence of T tokens), so one accumulator holds x_t W_gq^T + x_{t+1} W_gk^T
+// and the epilogue writes g_t in fp32 (384 bytes per token and head at
+// d = 96, read once by the scan).
+//
+// Tiling: 256 x 256 outputs per workgroup, 4 waves of 128 x 128 on
+// v_mfma_f32_32x32x16_bf16 (the weights on the MFMA rows, the tokens on the
+// lanes, so a lane holds 4 consecutive features of one token per register
+// quad: 8- or 16-byte stores). K advances in steps of 32 through a 4-stage LDS
+// ring filled by buffer loads that write LDS directly (no staging
+// registers); tiles are stored unpadded with the 16-byte chunk c of row r at
+// c ^ f(r), f(r) = ((r >> 1) ^ (r >> 3)) & 3, under which the fragment reads
+// of a wave are free of bank conflicts (for 32 or 64 banks of 4 bytes). Step
+// i waits for its own tile, meets the barrier (every wave has then finished
+// step i-1, so its stage is free) and issues the loads of step i+3 into that
+// stage before its 32 MFMAs per wave.
+// Generator tiles do twice the work of q/k/v tiles and come first in the
+// grid; each XCD takes a contiguous range of tiles in M-block-major order, so
+// the tiles running together on one XCD share their token rows in its L2.
+#include "holo_attn_common.h"
+
+namespace holo {
+
+namespace {
+
+// physical 16-byte chunk of logical chunk c in tile row r (rows of BK bf16):
+// XOR with bits of r chosen so that each ds_read_b128 of a fragment (32 rows,
+// two chunks) is free of bank conflicts (measured on gfx950), and so that the
+// XOR of row r and row r + 32 agree (one per-lane offset per 32-row block)
+template <int BK> __device__ __forceinline__ int gemm_swz(int r) {
+  if constexpr (BK == 32) return (r >> 2) & 3;
+  else return (r ^ (r >> 3)) & 7;
+}
+
+// Maps workgroup L of the tiles of one kind (tm M-blocks x tn N-blocks) to
+// (mb, nb): XCD L % 8 takes a contiguous range of tiles, N-block-major within
+// the range, so the tiles running together on one XCD share a few weight
+// blocks (resident in its L2) across many token blocks.
+__device__ __forceinline__ void xcd_tile(int L, int tm, int tn, int& mb, int& nb, int gm) {
+  const int count = tm * tn;
+  if (count % 8 != 0 || tm % 8 != 0) { mb = L / tn; nb = L % tn; return; }
+  const int per = tm >> 3;                           // M-blocks per XCD
+  const int x = L & 7, j = L >> 3;                   // XCD, index within its range
+  if (gm <= 0 || per % gm != 0) { nb = j / per; mb = x * per + j % per; return; }
+  // groups of gm M-blocks: within a group the N-blocks advance slowest, so
+  // the gm token blocks stay in L2 across the whole weight sweep
+  const int grp = j / (gm * tn), r = j - grp * gm * tn;
+  nb = r / gm;
+  mb = x * per + grp * gm + r % gm;
+}
+
+}  // namespace
+
+// FT features x TT tokens per workgroup, WF x WT waves (each FT/WF x TT/WT),
+// NST pipeline stages of BK.
+template <int FT, int TT, int WF, int WT, int BK, int NST> struct GemmCfg {
+  static constexpr int kThreadsG = 64 * WF * WT;
+  static constexpr int kCPR = BK / 8;                           // 16-byte chunks per tile row
+  static constexpr int kWBytes = FT * BK * 2, kXBytes = TT * BK * 2;
+  static constexpr int kStageBytes = kWBytes + kXBytes;
+  static constexpr int kLds = NST * kStageBytes;
+  static constexpr int kWLoads = kWBytes / 16 / kThreadsG, kXLoads = kXBytes / 16 / kThreadsG;
+  static constexpr int kLoads = kWLoads + kXLoads;
+  static constexpr int MI = FT / WF / 32, NJ = TT / WT / 32;   // MFMA tiles per wave
+  static_assert(kWLoads * 16 * kThreadsG == kWBytes && kXLoads * 16 * kThreadsG == kXBytes, "tile split");
+  static_assert(kLds <= 160 * 1024, "LDS");
+};
+
+template <int FT, int TT, int WF, int WT, int BK, int NST, int WPE>
+__global__ void __launch_bounds__(64 * WF * WT) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+gemm_qkvg(QkvgArgs a) {
+  using C = GemmCfg<FT, TT, WF, WT, BK, NST>;
+  constexpr int NT = C::kThreadsG;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wf = w / WT, wt = w % WT;       // wave: feature slice, token slice
+
+  // ---- tile of this workgroup: generator tiles first (twice the K) ----
+  const int L = blockIdx.x;
+  const int n_gen_tiles = a.tm * a.tng;
+  const bool gen = L < n_gen_tiles;
+  int mb, nb;
+  if (gen) xcd_tile(L, a.tm, a.tng, mb, nb, a.group_m);
+  else xcd_tile(L - n_gen_tiles, a.tm, a.tnq, mb, nb, a.group_m);
+  const int64_t m0 = (int64_t)mb * TT;
+  const int n0 = nb * FT;
+  const int nseg = gen ? 2 : 1;
+  const int nks = a.K / BK;                   // K steps per segment
+  const int nit = nseg * nks;
+
+  // ---- buffer resources: out-of-range rows read as zero ----
+  const int n_rows_w = gen ? a.n_gen : a.n_qkv;
+  const int wbytes = (int)((int64_t)n_rows_w * a.K * 2);
+  const __amdgpu_buffer_rsrc_t wr0 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(gen ? a.wg0 : a.wq), 0, wbytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t wr1 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(gen ? a.wg1 : a.wq), 0, wbytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(a.x), 0, (int)(a.M * a.ldx * 2), kBufferWord3);
+
+  // ---- per-lane byte offsets of this thread's loads: chunk p = i*NT + tid
+  // of a tile lands at LDS chunk p, so the lane fetches (row, logical chunk)
+  // = (p / CPR, (p % CPR) ^ f(row)) ----
+  int wo[C::kWLoads], xo0[C::kXLoads], xo1[C::kXLoads];
+  static_for<C::kWLoads>([&](auto i) {
+    const int p = i * NT + tid, r = p / C::kCPR, c = (p % C::kCPR) ^ gemm_swz<BK>(r);
+    wo[i] = ((n0 + r) * a.K + c * 8) * 2;
+  });
+  static_for<C::kXLoads>([&](auto i) {
+    const int p = i * NT + tid, r = p / C::kCPR, c = (p % C::kCPR) ^ gemm_swz<BK>(r);
+    const int64_t m = m0 + r;
+    xo0[i] = (int)((m * a.ldx + c * 8) * 2);
+    // shifted rows: token t+1 of the same sequence (t = T-1 wraps to 0); rows
+    // past M stay past M (read as zero)
+    const int64_t ms = m >= a.M ? m : ((m + 1) % a.T == 0 ? m + 1 - a.T : m + 1);
+    xo1[i] = (int)((ms * a.ldx + c * 8) * 2);
+  });
+
+  auto issue = [&](int it, auto st) {
+    const int seg = it >= nks, k0 = (it - seg * nks) * BK;
+    unsigned char* ws = smem + decltype(st)::value * C::kStageBytes;
+    unsigned char* xs = ws + C::kWBytes;
+    static_for<C::kWLoads>([&](auto i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(seg ? wr1 : wr0, (lds_void*)(ws + (i * NT + 64 * w) * 16), 16,
+                                               wo[i], k0 * 2, 0, 0);
+    });
+    static_for<C::kXLoads>([&](auto i) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(xs + (i * NT + 64 * w) * 16), 16,
+                                               seg ? xo1[i] : xo0[i], k0 * 2, 0, 0);
+    });
+  };
+
+  // fragment reads: row lr of a 32-row block, logical chunk 2s+g. With
+  // BK = 32 f(row) does not depend on the block; with BK = 64 it alternates
+  // between even and odd 32-row blocks (row bit 5 enters through r >> 3), so
+  // per substep one offset per block parity
+  constexpr int RB = BK * 2;                  // bytes per tile row
+  constexpr int NS = BK / 16;                 // k16 substeps per step
+  int ko[2][NS];
+  static_for<NS>([&](auto s) {
+    ko[0][s] = lr * RB + ((2 * s + g) ^ gemm_swz<BK>(lr)) * 16;
+    ko[1][s] = lr * RB + ((2 * s + g) ^ gemm_swz<BK>(lr + 32)) * 16;
+  });
+  const int wbase = wf * (FT / WF) * RB, xbase = C::kWBytes + wt * (TT / WT) * RB;
+
+  f32x16 acc[C::MI][C::NJ];
+  static_for<C::MI>([&](auto i) { static_for<C::NJ>([&](auto j) { acc[i][j] = f32x16{}; }); });
+
+  auto compute = [&](auto st) {
+    const unsigned char* sb = smem + decltype(st)::value * C::kStageBytes;
+    static_for<NS>([&](auto s) {
+      bf16x8 af[C::MI], bfr[C::NJ];
+      // the wave's first block of each operand is 32-row aligned at an even
+      // block index (FT/WF and TT/WT are multiples of 64)
+      static_for<C::MI>([&](auto i) {
+        af[i] = *reinterpret_cast<const bf16x8*>(sb + wbase + ko[i & 1][s] + i * 32 * RB);
+      });
+      static_for<C::NJ>([&](auto j) {
+        bfr[j] = *reinterpret_cast<const bf16x8*>(sb + xbase + ko[j & 1][s] + j * 32 * RB);
+      });
+      static_for<C::MI>([&](auto i) {
+        static_for<C::NJ>([&](auto j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        });
+      });
+    });
+  };
+
+  // one pipeline step: tile `it` in stage ST; up to NST-2 later tiles in flight
+  auto step = [&](int it, auto st) {
+    if (it >= nit) return;
+    const int ahead = nit - 1 - it < NST - 2 ? nit - 1 - it : NST - 2;   // later tiles already issued
+    if constexpr (NST >= 4) {
+      if (ahead >= 2) wait_vmem<2 * C::kLoads>();
+      else if (ahead == 1) wait_vmem<C::kLoads>();
+      else wait_vmem<0>();
+    } else {
+      if (ahead >= 1) wait_vmem<C::kLoads>();
+      else wait_vmem<0>();
+    }
+    ring_barrier();
+    using SN = std::integral_constant<int, (decltype(st)::value + NST - 1) % NST>;
+    if (it + NST - 1 < nit) issue(it + NST - 1, SN{});
+    compute(st);
+  };
+
+  static_for<NST - 1>([&](auto i) { if (i < nit) issue(i, i); });
+  for (int it = 0; it < nit; it += NST) {
+    static_for<NST>([&](auto i) { step(it + i, i); });
+  }
+
+  // ---- epilogue: the tile goes through LDS (both stages are free once every
+  // wave is past its last compute) so that global stores are whole 16-byte
+  // pieces of token rows: lane = token, register quad q = 4 consecutive
+  // features. Staged rows: token-major, the 16-byte chunk c of row r at
+  // c ^ (r & 31) (conflict-free for the 32 token rows a store covers and for
+  // the row-wise reads). The fp32 generator tile goes in two halves of the
+  // tokens (128 KB each). ----
+  ring_barrier();
+  const int es = gen ? 4 : 2;                         // output bytes per element
+  const int rowb = FT * es;                           // staged row bytes (512 or 1024)
+  const int cpr = rowb / 16;                          // 16-byte chunks per staged row
+  const int passes = gen ? 2 : 1;
+  const int tp = TT / passes;                         // tokens per pass
+  const int n_out = gen ? a.n_gen : a.n_qkv;
+  for (int hp = 0; hp < passes; ++hp) {
+    const int tw0 = wt * (TT / WT);                   // first token of this wave
+    if (tw0 / tp == hp) {
+      static_for<C::NJ>([&](auto j) {
+        const int r = tw0 % tp + j * 32 + lr;         // staged row (token)
+        static_for<C::MI>([&](auto i) {
+          static_for<4>([&](auto q) {
+            const int f = wf * (FT / WF) + i * 32 + 8 * q + 4 * g;   // first of 4 features
+            const f32x16& c = acc[i][j];
+            if (gen) {
+              const int ch = (f >> 2) ^ (r & 31);
+              *reinterpret_cast<f32x4*>(smem + r * rowb + ch * 16) =
+                  f32x4{c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]};
+            } else {
+              const int ch = (f >> 3) ^ (r & 31);
+              *reinterpret_cast<bf16x4*>(smem + r * rowb + ch * 16 + (f & 4) * 2) =
+                  bf16x4{(bf16)c[4 * q], (bf16)c[4 * q + 1], (bf16)c[4 * q + 2], (bf16)c[4 * q + 3]};
+            }
+          });
+        });
+      });
+    }
+    ring_barrier();
+    for (int idx = tid; idx < tp * cpr; idx += NT) {
+      const int r = idx / cpr, c = idx - r * cpr;
+      const int64_t m = m0 + hp * tp + r;
+      const int n = n0 + c * 16 / es;
+      if (m >= a.M || n >= n_out) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * rowb + (c ^ (r & 31)) * 16);
+      char* dst = gen ? reinterpret_cast<char*>(a.g + m * a.ldg + n) : reinterpret_cast<char*>(a.qkv + m * a.ldq + n);
+      if (n + 16 / es <= n_out) *reinterpret_cast<u32x4*>(dst) = v;
+      else *reinterpret_cast<u32x2*>(dst) = v.xy;      // bf16 tail of 4 features
+    }
+    if (hp + 1 < passes) ring_barrier();
+  }
+}
+
+template <int FT, int TT, int WF, int WT, int BK, int NST, int WPE>
+static hipError_t launch_cfg(QkvgArgs a, hipStream_t s) {
+  using C = GemmCfg<FT, TT, WF, WT, BK, NST>;
+  a.tm = (int)((a.M + TT - 1) / TT);
+  a.tnq = (a.n_qkv + FT - 1) / FT;
+  a.tng = (a.n_gen + FT - 1) / FT;
+  const hipError_t attr = allow_dynamic_lds<&gemm_qkvg<FT, TT, WF, WT, BK, NST, WPE>>();
+  if (attr != hipSuccess) return attr;
+  const unsigned grid = (unsigned)(a.tm * (a.tng + a.tnq));
+  if (grid == 0) return hipSuccess;
+  hipLaunchKernelGGL((gemm_qkvg<FT, TT, WF, WT, BK, NST, WPE>), dim3(grid), dim3(C::kThreadsG), C::kLds, s, a);
+  return hipGetLastError();
+}
+
+// 256 features x 256 tokens per workgroup, 8 waves of 128 x 64 (two per
+// SIMD), K steps of 64 through two LDS stages (128 KB), token blocks grouped
+// by 8 per weight sweep within each XCD.
+hipError_t launch_qkvg(const QkvgArgs& a, hipStream_t s) {
+  QkvgArgs b = a;
+  b.group_m = 8;
+  return launch_cfg<256, 256, 2, 4, 64, 2, 2>(b, s);
+}
+
+}  // namespace holo

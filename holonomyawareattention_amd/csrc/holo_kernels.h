@@ -109,6 +109,24 @@ struct AddNormArgs {
   void* y; int64_t y_rs;
 };
 
+// q/k/v projection and additive link generator in one GEMM (bf16 in, fp32
+// accumulation): qkv (M, n_qkv) bf16 = x W_qkv^T and g (M, n_gen) fp32 =
+// x_t W_gq^T + x_{t+1} W_gk^T, t+1 wrapping inside each sequence of T rows.
+struct QkvgArgs {
+  int64_t M;                 // B*T token rows
+  int64_t T;                 // tokens per sequence
+  int K;                     // d_model, a multiple of 64
+  int n_qkv, n_gen;          // output columns (multiples of 4)
+  int tm, tnq, tng;          // tiles: M blocks of 256, q/k/v and generator N blocks of 256
+  const bf16* x; int64_t ldx;                  // (M, K), row stride ldx
+  const bf16* wq;                              // (n_qkv, K) contiguous
+  const bf16* wg0; const bf16* wg1;            // (n_gen, K) contiguous: gq and gk weights
+  bf16* qkv; int64_t ldq;                      // (M, n_qkv)
+  float* g; int64_t ldg;                       // (M, n_gen)
+  int group_m;               // M-blocks per L2 group within an XCD's range of tiles
+};
+hipError_t launch_qkvg(const QkvgArgs& a, hipStream_t s);
+
 template <typename IO, typename OP, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_add_layernorm(const AddNormArgs& a, hipStream_t s);
 hipError_t launch_pack_mask(const uint8_t* mask, int64_t mask_rs, int64_t T, int64_t Tp, uint64_t* bits,

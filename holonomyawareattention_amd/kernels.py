@@ -64,6 +64,35 @@ def padded_seq_len(T: int) -> int:
     return int(_lib.load().holo_padded_seq_len(T))
 
 
+def qkvg_projection(x: torch.Tensor, w_qkv: torch.Tensor, w_gq: Optional[torch.Tensor],
+                    w_gk: Optional[torch.Tensor]) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """holo_qkvg_proj_fwd: x (B, T, K) bf16 -> qkv (B, T, n_qkv) bf16 = x w_qkv^T
+    and g (B, T, n_gen) fp32 = x_t w_gq^T + x_{(t+1) mod T} w_gk^T (None when
+    w_gq is None). Weights (n, K) bf16 (the nn.Linear layout)."""
+    lib = _lib.load()
+    if x.dim() != 3 or x.dtype != torch.bfloat16 or x.device.type != "cuda":
+        raise ValueError("qkvg_projection: x must be a (B, T, K) bfloat16 GPU tensor")
+    B, T, K = (int(n) for n in x.shape)
+    x2 = x.reshape(B * T, K)
+    if x2.stride(1) != 1:
+        raise ValueError("qkvg_projection: x rows must be contiguous")
+    ws = [w_qkv] + ([w_gq, w_gk] if w_gq is not None else [])
+    for w in ws:
+        if w.dtype != torch.bfloat16 or w.dim() != 2 or w.shape[1] != K or not w.is_contiguous() \
+                or w.device != x.device:
+            raise ValueError("qkvg_projection: weights must be contiguous (n, K) bfloat16 tensors on x's device")
+    n_qkv = int(w_qkv.shape[0])
+    n_gen = 0 if w_gq is None else int(w_gq.shape[0])
+    if w_gq is not None and tuple(w_gk.shape) != tuple(w_gq.shape):
+        raise ValueError("qkvg_projection: w_gq and w_gk must have one shape")
+    qkv = torch.empty((B, T, n_qkv), dtype=torch.bfloat16, device=x.device)
+    g = torch.empty((B, T, n_gen), dtype=torch.float32, device=x.device) if n_gen else None
+    rc = lib.holo_qkvg_proj_fwd(B * T, T, K, n_qkv, n_gen, _ptr(x2), x2.stride(0), _ptr(w_qkv), _ptr(w_gq),
+                                _ptr(w_gk), _ptr(qkv), n_qkv, _ptr(g), n_gen, _stream(x.device))
+    _lib.check(rc, "holo_qkvg_proj_fwd")
+    return qkv, g
+
+
 def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor,
               gk: Optional[torch.Tensor], edge_scale: float, want_hol: bool = False,
               p_format: str = "f32", mode: str = "causal", op_dtype: Optional[torch.dtype] = None,

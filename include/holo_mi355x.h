@@ -125,6 +125,26 @@ HOLO_API int holo_padded_head_dim(int d);
 /* Padded sequence length used by the kh / vh_t layouts (T rounded up to 64). */
 HOLO_API int64_t holo_padded_seq_len(int64_t T);
 
+/*
+ * holo_qkvg_proj_fwd: the layer's input projections in one hand-written
+ * gfx950 GEMM (bf16 operands, fp32 accumulation), replacing the q/k/v
+ * projection and the additive link generator
+ * (core/attention_fast_chunked.py:69-71 and :80-84):
+ *   qkv[r][n] = sum_c x[r][c] w_qkv[n][c]                        bf16, n < n_qkv
+ *   g[r][n]   = sum_c x[r][c] w_gq[n][c] + x[r'][c] w_gk[n][c]   fp32, n < n_gen
+ * for token rows r = b*T + t, r' = b*T + (t+1) mod T: g is the generator sum
+ * before edge_scale, the input of holo_geom_scan_fwd in HOLO_GEN_DIRECT mode
+ * (a_t = edge_scale * g_t), so gq and gk are never stored. x is (M, K) with
+ * row stride x_row_stride (M = B*T); weights are row-major (n, K), the
+ * nn.Linear layout. K a multiple of 64; n_qkv, n_gen multiples of 4 (n_gen
+ * may be 0: then w_gq, w_gk and g are unused); pointers 16-byte aligned, row
+ * strides whole 16-byte multiples.
+ */
+HOLO_API int holo_qkvg_proj_fwd(int64_t M, int64_t T, int K, int n_qkv, int n_gen,
+                       const void* x, int64_t x_row_stride,
+                       const void* w_qkv, const void* w_gq, const void* w_gk,
+                       void* qkv, int64_t qkv_row_stride, float* g, int64_t g_row_stride, void* stream);
+
 /* Workspace bytes for holo_geom_scan_fwd. */
 HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
 

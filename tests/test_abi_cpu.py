@@ -107,6 +107,22 @@ def test_attention_argument_validation(lib):
     assert f(1, 8, 1, 12, F32, F32, 0, 0.3, 16, 16, 16, 16, 16, 12, 12, 8) == _lib.HOLO_ERR_INVALID_ARG   # lse misaligned
 
 
+def test_projection_argument_validation(lib):
+    f = lib.holo_qkvg_proj_fwd
+
+    def call(M=512, T=256, K=128, nq=384, ng=96, xs=128, qs=384, gs=96, x=16, wq=16, w0=16, w1=16, q=16, g=16):
+        return f(M, T, K, nq, ng, x, xs, wq, w0, w1, q, qs, g, gs, None)
+    assert call(M=0) == _lib.HOLO_ERR_BAD_SHAPE
+    assert call(T=300) == _lib.HOLO_ERR_BAD_SHAPE                   # M not a whole number of sequences
+    assert call(K=96, xs=96) == _lib.HOLO_ERR_UNSUPPORTED            # K not a multiple of 64
+    assert call(nq=386, qs=392) == _lib.HOLO_ERR_UNSUPPORTED         # output width not a multiple of 4
+    assert call(x=None) == _lib.HOLO_ERR_INVALID_ARG
+    assert call(w0=None) == _lib.HOLO_ERR_INVALID_ARG                # generator weights needed when ng > 0
+    assert call(q=8) == _lib.HOLO_ERR_INVALID_ARG                    # misaligned
+    assert call(qs=388) == _lib.HOLO_ERR_INVALID_ARG                 # qkv row stride not a 16-byte multiple
+    assert call(xs=120) == _lib.HOLO_ERR_INVALID_ARG                 # x row stride below K
+
+
 def test_workspace_status_validation(lib):
     st = lib.holo_workspace_status
     assert st(None, 1024, 16, None) == _lib.HOLO_ERR_INVALID_ARG

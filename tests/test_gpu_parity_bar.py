@@ -35,10 +35,12 @@ def _f64(t):
 
 
 def _product_core(m, x, status=None):
-    """The module's projections, then the causal path as the module runs it
-    (fp16 operands, int16 quaternions), with o written in fp32."""
+    """The module's projections (the fused q/k/v + generator GEMM: gq holds
+    g_t = gq(x_t) + gk(x_{t+1}), gk is None), then the causal path as the
+    module runs it (fp16 operands, int16 quaternions), with o written in fp32."""
     with torch.no_grad():
-        q, k, v, gq, gk = m._link_inputs(x)
+        q, k, v, gq, gk = m._link_inputs(x, fused=True)
+        assert gk is None
         qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, m.edge_scale, p_format="snorm16",
                                                 op_dtype=torch.float16, status=status)
         o = kernels.attention(qh, kh, vh_t, P, m.d, m.scale, out_dtype=torch.float32)
@@ -57,9 +59,12 @@ def _oracle_o(parts, es, rows, bsel=slice(None), tlen=None):
     tsl = slice(0, tlen)
     qq, kk, vv = (_f64(t[bsel, tsl]) for t in (q, k, v))
     gq_ = _f64(gq[bsel, tsl])
-    gk_ = _f64(gk[bsel, :tlen + 1] if tlen < T else gk[bsel])
-    gk_next = gk_[:, :, 1:tlen + 1] if tlen < T else np.roll(gk_, -1, axis=2)
-    a = (gq_ + gk_next) * es
+    if gk is None:                                   # gq is already g_t = gq(x_t) + gk(x_{t+1})
+        a = gq_ * es
+    else:
+        gk_ = _f64(gk[bsel, :tlen + 1] if tlen < T else gk[bsel])
+        gk_next = gk_[:, :, 1:tlen + 1] if tlen < T else np.roll(gk_, -1, axis=2)
+        a = (gq_ + gk_next) * es
     nb = q.shape[-1] // 3
     P, _ = R.geometry_blocks(a[..., :3 * nb])
     qh, kh, vh = (R.apply_blocks_T(P, u) for u in (qq, kk, vv))
@@ -128,7 +133,7 @@ def _unpack_vh(vh_t, T, d):
 def test_attention_stage_rounding_bound(opdt, B, T, D, H):
     """The attention kernel on the exact qh, kh, vh, P it consumed, o in fp32.
     The one rounding left is that of the softmax weights p_j to the operand
-    type (relative u = 2^-9 bf16, 2^-11 fp16); the row sum is taken over the
+    type (unit roundoff u = 2^-8 bf16, 2^-11 fp16: 8 and 11 significant bits); the row sum is taken over the
     same rounded weights, so each normalised weight moves by at most
     a_j * 2u / (1 - u) and, per 3-dim block, ||d oh_i|| <= 2u/(1-u) *
     ||sum_j a_ij |vh_j| ||; the back-rotation keeps the norm. Bound per element:
@@ -152,7 +157,7 @@ def test_attention_stage_rounding_bound(opdt, B, T, D, H):
     scale = 1.0 / math.sqrt(d)
     oh = R.causal_attention64(qhr, khr, vhr, scale)
     o_ref = np.einsum("bhtij,bhtj->bhti", Pb, oh)
-    u = 2.0 ** -9 if opdt == torch.bfloat16 else 2.0 ** -11
+    u = 2.0 ** -8 if opdt == torch.bfloat16 else 2.0 ** -11
     spread = R.causal_attention64(qhr, khr, np.abs(vhr), scale) * (2 * u / (1 - u))
     blk = np.sqrt((spread[..., :3 * nb].reshape(*spread.shape[:-1], nb, 3) ** 2).sum(-1))
     bound = np.concatenate([np.repeat(blk, 3, axis=-1), spread[..., 3 * nb:]], axis=-1)
