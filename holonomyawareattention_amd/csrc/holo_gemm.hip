@@ -10,20 +10,21 @@
 // and the epilogue writes g_t in fp32 (384 bytes per token and head at
 // d = 96, read once by the scan).
 //
-// Tiling: 256 x 256 outputs per workgroup, 4 waves of 128 x 128 on
-// v_mfma_f32_32x32x16_bf16 (the weights on the MFMA rows, the tokens on the
-// lanes, so a lane holds 4 consecutive features of one token per register
-// quad: 8- or 16-byte stores). K advances in steps of 32 through a 4-stage LDS
-// ring filled by buffer loads that write LDS directly (no staging
-// registers); tiles are stored unpadded with the 16-byte chunk c of row r at
-// c ^ f(r), f(r) = ((r >> 1) ^ (r >> 3)) & 3, under which the fragment reads
-// of a wave are free of bank conflicts (for 32 or 64 banks of 4 bytes). Step
-// i waits for its own tile, meets the barrier (every wave has then finished
-// step i-1, so its stage is free) and issues the loads of step i+3 into that
-// stage before its 32 MFMAs per wave.
+// Tiling (the launched form, launch_qkvg): 256 features x 256 tokens per
+// workgroup, 8 waves of 128 x 64 on v_mfma_f32_32x32x16_bf16 (the weights on
+// the MFMA rows, the tokens on the lanes, so a lane holds 4 consecutive
+// features of one token per register quad). K advances in steps of 64
+// through a 2-stage LDS ring (128 KB) filled by buffer loads that write LDS
+// directly (no staging registers); tiles are stored unpadded with the 16-byte
+// chunk c of row r at c ^ gemm_swz(r), under which the fragment reads of a
+// wave are free of bank conflicts on gfx950 (measured). Step i waits for its
+// own tile, meets the barrier (every wave has then finished step i-1, so its
+// stage is free) and issues the loads of step i+1 into that stage before its
+// 32 MFMAs per wave. The epilogue goes through LDS so that global stores are
+// whole 16-byte pieces of token rows.
 // Generator tiles do twice the work of q/k/v tiles and come first in the
-// grid; each XCD takes a contiguous range of tiles in M-block-major order, so
-// the tiles running together on one XCD share their token rows in its L2.
+// grid; each XCD takes a contiguous range of M-blocks, in groups of 8 that
+// stay in its L2 while the N-blocks sweep the weights.
 #include "holo_attn_common.h"
 
 namespace holo {
@@ -32,8 +33,9 @@ namespace {
 
 // physical 16-byte chunk of logical chunk c in tile row r (rows of BK bf16):
 // XOR with bits of r chosen so that each ds_read_b128 of a fragment (32 rows,
-// two chunks) is free of bank conflicts (measured on gfx950), and so that the
-// XOR of row r and row r + 32 agree (one per-lane offset per 32-row block)
+// two chunks) is free of bank conflicts (measured on gfx950); with BK = 32
+// rows r and r + 32 take the same XOR, with BK = 64 it follows the parity of
+// the 32-row block (two per-lane offsets per substep)
 template <int BK> __device__ __forceinline__ int gemm_swz(int r) {
   if constexpr (BK == 32) return (r >> 2) & 3;
   else return (r ^ (r >> 3)) & 7;
