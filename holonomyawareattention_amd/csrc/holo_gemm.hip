@@ -73,6 +73,9 @@ template <int FT, int TT, int WF, int WT, int BK, int NST> struct GemmCfg {
   static constexpr int MI = FT / WF / 32, NJ = TT / WT / 32;   // MFMA tiles per wave
   static_assert(kWLoads * 16 * kThreadsG == kWBytes && kXLoads * 16 * kThreadsG == kXBytes, "tile split");
   static_assert(kLds <= 160 * 1024, "LDS");
+  // the epilogue stages the tile in the ring's LDS: bf16 q/k/v tiles whole,
+  // fp32 generator tiles in two halves of the tokens
+  static_assert(TT * FT * 2 <= kLds && (TT / 2) * FT * 4 <= kLds, "epilogue staging exceeds the ring");
 };
 
 template <int FT, int TT, int WF, int WT, int BK, int NST, int WPE>
@@ -203,13 +206,15 @@ gemm_qkvg(QkvgArgs a) {
   // wave is past its last compute) so that global stores are whole 16-byte
   // pieces of token rows: lane = token, register quad q = 4 consecutive
   // features. Staged rows: token-major, the 16-byte chunk c of row r at
-  // c ^ (r & 31) (conflict-free for the 32 token rows a store covers and for
-  // the row-wise reads). The fp32 generator tile goes in two halves of the
-  // tokens (128 KB each). ----
+  // c ^ (r & xm), xm = min(cpr, 32) - 1 (the XOR stays inside the row;
+  // conflict-free for the 32 token rows a store covers and for the row-wise
+  // reads). The fp32 generator tile goes in two halves of the tokens (128 KB
+  // each). ----
   ring_barrier();
   const int es = gen ? 4 : 2;                         // output bytes per element
   const int rowb = FT * es;                           // staged row bytes (512 or 1024)
   const int cpr = rowb / 16;                          // 16-byte chunks per staged row
+  const int xm = (cpr < 32 ? cpr : 32) - 1;           // XOR mask: stays inside the row
   const int passes = gen ? 2 : 1;
   const int tp = TT / passes;                         // tokens per pass
   const int n_out = gen ? a.n_gen : a.n_qkv;
@@ -223,11 +228,11 @@ gemm_qkvg(QkvgArgs a) {
             const int f = wf * (FT / WF) + i * 32 + 8 * q + 4 * g;   // first of 4 features
             const f32x16& c = acc[i][j];
             if (gen) {
-              const int ch = (f >> 2) ^ (r & 31);
+              const int ch = (f >> 2) ^ (r & xm);
               *reinterpret_cast<f32x4*>(smem + r * rowb + ch * 16) =
                   f32x4{c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]};
             } else {
-              const int ch = (f >> 3) ^ (r & 31);
+              const int ch = (f >> 3) ^ (r & xm);
               *reinterpret_cast<bf16x4*>(smem + r * rowb + ch * 16 + (f & 4) * 2) =
                   bf16x4{(bf16)c[4 * q], (bf16)c[4 * q + 1], (bf16)c[4 * q + 2], (bf16)c[4 * q + 3]};
             }
@@ -241,7 +246,7 @@ gemm_qkvg(QkvgArgs a) {
       const int64_t m = m0 + hp * tp + r;
       const int n = n0 + c * 16 / es;
       if (m >= a.M || n >= n_out) continue;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * rowb + (c ^ (r & 31)) * 16);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * rowb + (c ^ (r & xm)) * 16);
       char* dst = gen ? reinterpret_cast<char*>(a.g + m * a.ldg + n) : reinterpret_cast<char*>(a.qkv + m * a.ldq + n);
       if (n + 16 / es <= n_out) *reinterpret_cast<u32x4*>(dst) = v;
       else *reinterpret_cast<u32x2*>(dst) = v.xy;      // bf16 tail of 4 features
