@@ -11,7 +11,7 @@
 // d = 96, read once by the scan).
 //
 // Tiling (the launched form, launch_qkvg): 256 features x 256 tokens per
-// workgroup, 8 waves of 128 x 64 on v_mfma_f32_32x32x16_bf16 (the weights on
+// workgroup, 8 waves of 64 x 128 on v_mfma_f32_32x32x16_bf16 (the weights on
 // the MFMA rows, the tokens on the lanes, so a lane holds 4 consecutive
 // features of one token per register quad). K advances in steps of 64
 // through a 2-stage LDS ring (128 KB) filled by buffer loads that write LDS
@@ -248,8 +248,10 @@ gemm_qkvg(QkvgArgs a) {
       if (m >= a.M || n >= n_out) continue;
       const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * rowb + (c ^ (r & xm)) * 16);
       char* dst = gen ? reinterpret_cast<char*>(a.g + m * a.ldg + n) : reinterpret_cast<char*>(a.qkv + m * a.ldq + n);
-      if (n + 16 / es <= n_out) *reinterpret_cast<u32x4*>(dst) = v;
-      else *reinterpret_cast<u32x2*>(dst) = v.xy;      // bf16 tail of 4 features
+      // non-temporal: the outputs (503 MB at config 2) stream to HBM instead
+      // of evicting the token rows the other tiles still read (3% measured)
+      if (n + 16 / es <= n_out) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
+      else __builtin_nontemporal_store(v.xy, reinterpret_cast<u32x2*>(dst));   // bf16 tail of 4 features
     }
     if (hp + 1 < passes) ring_barrier();
   }
@@ -269,13 +271,14 @@ static hipError_t launch_cfg(QkvgArgs a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// 256 features x 256 tokens per workgroup, 8 waves of 128 x 64 (two per
-// SIMD), K steps of 64 through two LDS stages (128 KB), token blocks grouped
-// by 8 per weight sweep within each XCD.
+// 256 features x 256 tokens per workgroup, 8 waves of 64 features x 128
+// tokens (two per SIMD), K steps of 64 through two LDS stages (128 KB), token
+// blocks grouped by 8 per weight sweep within each XCD. (Waves of 128 x 64:
+// 1-2% slower.)
 hipError_t launch_qkvg(const QkvgArgs& a, hipStream_t s) {
   QkvgArgs b = a;
   b.group_m = 8;
-  return launch_cfg<256, 256, 2, 4, 64, 2, 2>(b, s);
+  return launch_cfg<256, 256, 4, 2, 64, 2, 2>(b, s);
 }
 
 }  // namespace holo
