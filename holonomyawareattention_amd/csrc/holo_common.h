@@ -95,54 +95,57 @@ __device__ inline quat qexp_skew(float a0, float a1, float a2) {
 }
 
 // Rotation matrix of q scaled by 1/|q|^2 (exactly orthogonal for any q != 0).
+// These helpers spell out every fused multiply-add (fmaf) in a fixed order,
+// so their rounding does not depend on how the compiler contracts the code
+// around each inlined call: every kernel that rotates the same vector by the
+// same quaternion gets the same bits.
 struct rot3 { float m[3][3]; };
 
 __device__ inline rot3 qmat(const quat& q) {
-  float ww = q.w * q.w, xx = q.x * q.x, yy = q.y * q.y, zz = q.z * q.z;
-  float inv = __builtin_amdgcn_rcpf(ww + xx + yy + zz);   // v_rcp_f32, 1 ulp
-  float xy = q.x * q.y, xz = q.x * q.z, yz = q.y * q.z;
-  float wx = q.w * q.x, wy = q.w * q.y, wz = q.w * q.z;
+  const float zz = q.z * q.z;
+  const float inv = __builtin_amdgcn_rcpf(fmaf(q.w, q.w, fmaf(q.x, q.x, fmaf(q.y, q.y, zz))));   // 1 ulp
+  const float i2 = 2.f * inv;
   rot3 r;
-  r.m[0][0] = (ww + xx - yy - zz) * inv;
-  r.m[0][1] = 2.f * (xy - wz) * inv;
-  r.m[0][2] = 2.f * (xz + wy) * inv;
-  r.m[1][0] = 2.f * (xy + wz) * inv;
-  r.m[1][1] = (ww - xx + yy - zz) * inv;
-  r.m[1][2] = 2.f * (yz - wx) * inv;
-  r.m[2][0] = 2.f * (xz - wy) * inv;
-  r.m[2][1] = 2.f * (yz + wx) * inv;
-  r.m[2][2] = (ww - xx - yy + zz) * inv;
+  r.m[0][0] = fmaf(q.w, q.w, fmaf(q.x, q.x, -fmaf(q.y, q.y, zz))) * inv;
+  r.m[0][1] = fmaf(q.x, q.y, -(q.w * q.z)) * i2;
+  r.m[0][2] = fmaf(q.x, q.z, q.w * q.y) * i2;
+  r.m[1][0] = fmaf(q.x, q.y, q.w * q.z) * i2;
+  r.m[1][1] = fmaf(q.w, q.w, fmaf(q.y, q.y, -fmaf(q.x, q.x, zz))) * inv;
+  r.m[1][2] = fmaf(q.y, q.z, -(q.w * q.x)) * i2;
+  r.m[2][0] = fmaf(q.x, q.z, -(q.w * q.y)) * i2;
+  r.m[2][1] = fmaf(q.y, q.z, q.w * q.x) * i2;
+  r.m[2][2] = fmaf(q.w, q.w, fmaf(q.z, q.z, -fmaf(q.x, q.x, q.y * q.y))) * inv;
   return r;
 }
 
 // y = R^T u
 __device__ inline void rot_t_apply(const rot3& R, float u0, float u1, float u2,
                                    float& y0, float& y1, float& y2) {
-  y0 = R.m[0][0] * u0 + R.m[1][0] * u1 + R.m[2][0] * u2;
-  y1 = R.m[0][1] * u0 + R.m[1][1] * u1 + R.m[2][1] * u2;
-  y2 = R.m[0][2] * u0 + R.m[1][2] * u1 + R.m[2][2] * u2;
+  y0 = fmaf(R.m[0][0], u0, fmaf(R.m[1][0], u1, R.m[2][0] * u2));
+  y1 = fmaf(R.m[0][1], u0, fmaf(R.m[1][1], u1, R.m[2][1] * u2));
+  y2 = fmaf(R.m[0][2], u0, fmaf(R.m[1][2], u1, R.m[2][2] * u2));
 }
 
 // y = R u
 __device__ inline void rot_apply(const rot3& R, float u0, float u1, float u2,
                                  float& y0, float& y1, float& y2) {
-  y0 = R.m[0][0] * u0 + R.m[0][1] * u1 + R.m[0][2] * u2;
-  y1 = R.m[1][0] * u0 + R.m[1][1] * u1 + R.m[1][2] * u2;
-  y2 = R.m[2][0] * u0 + R.m[2][1] * u1 + R.m[2][2] * u2;
+  y0 = fmaf(R.m[0][0], u0, fmaf(R.m[0][1], u1, R.m[0][2] * u2));
+  y1 = fmaf(R.m[1][0], u0, fmaf(R.m[1][1], u1, R.m[1][2] * u2));
+  y2 = fmaf(R.m[2][0], u0, fmaf(R.m[2][1], u1, R.m[2][2] * u2));
 }
 
 // y = R(q) u with R the homogeneous rotation of q (same map as qmat):
 // R(q) u = ((w^2 - |v|^2) u + 2 (v.u) v + 2 w (v x u)) / |q|^2,  v = (x, y, z)
 __device__ inline void quat_rotate(const quat& q, float u0, float u1, float u2,
                                    float& y0, float& y1, float& y2) {
-  const float vv = q.x * q.x + q.y * q.y + q.z * q.z;
-  const float inv = __builtin_amdgcn_rcpf(q.w * q.w + vv);
-  const float a = (q.w * q.w - vv) * inv;
-  const float b = 2.f * (q.x * u0 + q.y * u1 + q.z * u2) * inv;
-  const float cw = 2.f * q.w * inv;
-  y0 = a * u0 + b * q.x + cw * (q.y * u2 - q.z * u1);
-  y1 = a * u1 + b * q.y + cw * (q.z * u0 - q.x * u2);
-  y2 = a * u2 + b * q.z + cw * (q.x * u1 - q.y * u0);
+  const float vv = fmaf(q.x, q.x, fmaf(q.y, q.y, q.z * q.z));
+  const float inv = __builtin_amdgcn_rcpf(fmaf(q.w, q.w, vv));
+  const float a = fmaf(q.w, q.w, -vv) * inv;
+  const float b = fmaf(q.x, u0, fmaf(q.y, u1, q.z * u2)) * (2.f * inv);
+  const float cw = (2.f * q.w) * inv;
+  y0 = fmaf(a, u0, fmaf(b, q.x, cw * fmaf(q.y, u2, -(q.z * u1))));
+  y1 = fmaf(a, u1, fmaf(b, q.y, cw * fmaf(q.z, u0, -(q.x * u2))));
+  y2 = fmaf(a, u2, fmaf(b, q.z, cw * fmaf(q.x, u1, -(q.y * u0))));
 }
 
 __device__ inline quat load_quat(const float* p) {
@@ -162,6 +165,13 @@ __device__ inline void store_quat_snorm16(short* p, const quat& q) {
   const float s = 32767.f * __builtin_amdgcn_rsqf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
   auto cv = [&](float v) { return (unsigned)(int)__builtin_rintf(v * s) & 0xffffu; };
   *reinterpret_cast<u32x2*>(p) = u32x2{cv(q.w) | (cv(q.x) << 16), cv(q.y) | (cv(q.z) << 16)};
+}
+
+// store_quat_snorm16 with a non-temporal store (outputs streamed to HBM)
+__device__ inline void store_quat_snorm16_nt(short* p, const quat& q) {
+  const float s = 32767.f * __builtin_amdgcn_rsqf(q.w * q.w + q.x * q.x + q.y * q.y + q.z * q.z);
+  auto cv = [&](float v) { return (unsigned)(int)__builtin_rintf(v * s) & 0xffffu; };
+  __builtin_nontemporal_store(u32x2{cv(q.w) | (cv(q.x) << 16), cv(q.y) | (cv(q.z) << 16)}, reinterpret_cast<u32x2*>(p));
 }
 
 // The stored integers of store_quat_snorm16 as a quaternion (norm ~32767) of

@@ -170,7 +170,7 @@ __device__ inline void chunk_prefix(const ScanArgs& a, float* gs, float* ss, flo
       const quat p = qmul(load_quat(slot), X);
       store_quat(slot, p);
       if (t0 + r < a.T) {
-        if (a.p_format) store_quat_snorm16(reinterpret_cast<short*>(a.P) + (q0 + (int64_t)r * nb) * 4, p);
+        if (a.p_format) store_quat_snorm16_nt(reinterpret_cast<short*>(a.P) + (q0 + (int64_t)r * nb) * 4, p);
         else store_quat(a.P + (q0 + (int64_t)r * nb) * 4, p);
       }
     }
@@ -309,7 +309,7 @@ __device__ __forceinline__ void store_row(T* p, const float* in) {
   });
 }
 
-template <typename IO, typename OP, typename GT, int NG, int DP>
+template <typename IO, typename OP, typename GT, int NG, int DP, bool DIRECT>
 __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   constexpr int NT = 64 * NG;           // threads
   constexpr int NB = 8 * NG;            // blocks per head (nb)
@@ -319,10 +319,14 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   constexpr int KS = DP + E;             // row stride of the staged qh / kh tiles
   constexpr int GS_BYTES = kChunk * NB * 16, QK_BYTES = 2 * kChunk * KS * (int)sizeof(OP);
   // link quaternions / P, later reused for the transported qh and kh tiles
+  // (packing both phases and the value tile into 38 KB, four workgroups per
+  // CU, measured 1.5% slower at d = 96)
   __shared__ __align__(16) float gs[(GS_BYTES > QK_BYTES ? GS_BYTES : QK_BYTES) / 4];
   __shared__ __align__(16) float ss[8 * NB * 4];
   __shared__ __align__(16) float cs[NB * 4];
   __shared__ __align__(16) OP vts[DP * VS];
+  OP* const qts = reinterpret_cast<OP*>(gs);
+  OP* const kts = qts + kChunk * KS;
 
   const int tid = threadIdx.x;
   const int i = tid / NG, g = tid % NG;
@@ -337,12 +341,11 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   const bool link = t + 1 < a.T;
   if (link) {
     load_row<GT, 24>(reinterpret_cast<const GT*>(a.gq) + (b * a.T + t) * a.gq_rs + h * a.gq_hs + 24 * g, gq);
-    if (a.gen_mode == 0) {
+    if constexpr (!DIRECT) {
       load_row<GT, 24>(reinterpret_cast<const GT*>(a.gk) + (b * a.T + t + 1) * a.gk_rs + h * a.gk_hs + 24 * g, gk);
-    } else {
-      static_for<24>([&](auto j) { gk[j] = 0.f; });
     }
   }
+  if constexpr (DIRECT) static_for<24>([&](auto j) { gk[j] = 0.f; });
   const bool tok = t < a.T;
   if (tok) {
     load_row<IO, 24>(reinterpret_cast<const IO*>(a.q) + (b * a.T + t) * a.q_rs + h * a.q_hs + 24 * g, qv);
@@ -351,10 +354,6 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   } else {
     static_for<24>([&](auto j) { qv[j] = 0.f; kv[j] = 0.f; vv[j] = 0.f; });
   }
-  // zero the padded rows of the value tile
-  for (int idx = tid; idx < (DP - D) * kChunk; idx += NT)
-    vts[(D + idx / kChunk) * VS + idx % kChunk] = from_f32<OP>(0.f);
-
   // ---- link quaternions of link t -> LDS ----
   static_for<8>([&](auto j) {
     quat q = qident();
@@ -389,8 +388,9 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   // every thread has read its own), then write each with whole 16-byte rows
   // per lane: the qh and kh tiles of a chunk are contiguous 64 x DP blocks ----
   __syncthreads();
-  OP* qts = reinterpret_cast<OP*>(gs);
-  OP* kts = qts + kChunk * KS;
+  // zero the padded rows of the value tile
+  for (int idx = tid; idx < (DP - D) * kChunk; idx += NT)
+    vts[(D + idx / kChunk) * VS + idx % kChunk] = from_f32<OP>(0.f);
   store_row<OP, 24>(qts + i * KS + 24 * g, qv);
   store_row<OP, 24>(kts + i * KS + 24 * g, kv);
   if (DP > D && g == NG - 1) {
@@ -406,14 +406,16 @@ __global__ void __launch_bounds__(64 * NG) chunk_apply_wide(ScanArgs a) {
   u32x4* qdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.qh) + (bh * a.Tp + t0) * DP);
   u32x4* kdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.kh) + (bh * a.Tp + t0) * DP);
   constexpr int KR = DP / E;
+  // non-temporal stores: the outputs stream to HBM (the attention reads them
+  // back after the whole scan) instead of evicting the inputs in flight
   for (int idx = tid; idx < kChunk * KR; idx += NT) {
-    qdst[idx] = *reinterpret_cast<const u32x4*>(&qts[(idx / KR) * KS + (idx % KR) * E]);
-    kdst[idx] = *reinterpret_cast<const u32x4*>(&kts[(idx / KR) * KS + (idx % KR) * E]);
+    __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&qts[(idx / KR) * KS + (idx % KR) * E]), qdst + idx);
+    __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&kts[(idx / KR) * KS + (idx % KR) * E]), kdst + idx);
   }
   u32x4* vdst = reinterpret_cast<u32x4*>(reinterpret_cast<OP*>(a.vh_t) + (bh * a.nch + c) * DP * kChunk);
   constexpr int VR = kChunk / E;
   for (int idx = tid; idx < DP * VR; idx += NT)
-    vdst[idx] = *reinterpret_cast<const u32x4*>(&vts[(idx / VR) * VS + (idx % VR) * E]);
+    __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&vts[(idx / VR) * VS + (idx % VR) * E]), vdst + idx);
 }
 
 hipError_t launch_chain_reset(void* state, int64_t n_pairs, unsigned* ticket, hipStream_t s) {
@@ -431,10 +433,20 @@ hipError_t launch_scan(const ScanArgs& a, hipStream_t s) {
                      dim3(tpb), 0, s, reinterpret_cast<uint64_t*>(a.incl), n_pairs, a.ticket);
   const dim3 grid((unsigned)((int64_t)a.B * a.H * a.nch));
   if (a.wide) {
+    const bool direct = a.gen_mode == 1;
     switch (a.d) {
-      case 48: hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 2, 64>), grid, dim3(128), 0, s, a); break;
-      case 72: hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 3, 96>), grid, dim3(192), 0, s, a); break;
-      case 96: hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 4, 96>), grid, dim3(256), 0, s, a); break;
+      case 48:
+        if (direct) hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 2, 64, true>), grid, dim3(128), 0, s, a);
+        else hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 2, 64, false>), grid, dim3(128), 0, s, a);
+        break;
+      case 72:
+        if (direct) hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 3, 96, true>), grid, dim3(192), 0, s, a);
+        else hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 3, 96, false>), grid, dim3(192), 0, s, a);
+        break;
+      case 96:
+        if (direct) hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 4, 96, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((chunk_apply_wide<IO, OP, GT, 4, 96, false>), grid, dim3(256), 0, s, a);
+        break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
