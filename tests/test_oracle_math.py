@@ -134,3 +134,28 @@ def test_prefix_transport_is_the_arc_walk():
     """forward_blocks (prefix products) equals the O(L^3) arc walk at small L."""
     x, W = layer(35, 2, 9, 24, 2, dtype=torch.float64)
     assert np.abs(R.forward_blocks(x, W, 2, 1.3) - R.forward_arc_walk(x, W, 2, 1.3)).max() < 1e-12
+
+
+def test_attention_rows_equal_full_causal_attention():
+    """oracle.attention_rows64 (the parity-bar tests' row-wise oracle) against
+    the rows of causal_attention64 and against torch's causal
+    scaled_dot_product_attention (float64), at unsorted and repeated rows,
+    row 0 (one key) and the last row; an off-by-one causal mask (query i sees
+    keys 0..i-1, row 0 dropped) must fail the comparison."""
+    rng = np.random.default_rng(5)
+    qh, kh, vh = (rng.standard_normal((2, 3, 150, 12)) for _ in range(3))
+    scale = 1.0 / math.sqrt(12)
+    rows = np.array([149, 0, 37, 37, 64, 1, 148])
+    got = R.attention_rows64(qh, kh, vh, scale, rows)
+    full = R.causal_attention64(qh, kh, vh, scale)
+    np.testing.assert_allclose(got, full[..., rows, :], rtol=0, atol=1e-12)
+    sdpa = torch.nn.functional.scaled_dot_product_attention(
+        *(torch.from_numpy(u) for u in (qh, kh, vh)), is_causal=True, scale=scale).numpy()
+    np.testing.assert_allclose(got, sdpa[..., rows, :], rtol=0, atol=1e-12)
+    # planted mistake: strict causality (keys j < i) on rows >= 1
+    r1 = rows[rows > 0]
+    s = np.matmul(qh[..., r1, :], np.swapaxes(kh, -1, -2)) * scale
+    s = np.where(r1[:, None] > np.arange(150)[None, :], s, -np.inf)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    wrong = np.matmul(p / p.sum(axis=-1, keepdims=True), vh)
+    assert np.abs(wrong - R.attention_rows64(qh, kh, vh, scale, r1)).max() > 1e-3
