@@ -30,8 +30,10 @@ Under autograd the projections are ordinary differentiable torch GEMMs and the
 scan + attention core is one autograd function whose backward is the gfx950
 backward (holo_attn_bwd; the reference recomputes its forward under autograd,
 kernel/attention_kernel.py:174-187); that backward covers the causal + tril
-path, and other calls under autograd raise NotImplementedError. The geometry
-output is not differentiable (return_geometry under autograd raises).
+path. Other calls under autograd (any other mask, inert mode, return_geometry)
+run their forward as with gradients off and return outputs whose backward
+raises NotImplementedError: the exact path and the geometry output have no
+gfx950 backward.
 """
 from __future__ import annotations
 
@@ -89,6 +91,26 @@ class _MatmulF32Out(torch.autograd.Function):
         dx = dgl @ w if ctx.needs_input_grad[0] else None
         dw = dgl.t() @ x2 if ctx.needs_input_grad[1] else None
         return dx, dw
+
+
+class _ForwardOnly(torch.autograd.Function):
+    """Attaches outputs computed without autograd (the exact path, the
+    geometry output) to the inputs they depend on: forward returns them
+    unchanged, backward raises NotImplementedError, so a forward under autograd
+    (e.g. an eval() model outside torch.no_grad()) works and only an actual
+    backward through these outputs fails."""
+
+    @staticmethod
+    def forward(ctx, what: str, n_out: int, *tensors):
+        ctx.what = what
+        outs = tuple(t.view_as(t) for t in tensors[:n_out])
+        return outs[0] if n_out == 1 else outs
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(
+            f"holonomyawareattention_amd kernel path does not support this call: the gradient of {ctx.what} "
+            "(the gfx950 backward covers causal mode with attn_mask == tril(L) and no geometry output)")
 
 
 class _PathAttention(torch.autograd.Function):
@@ -333,17 +355,26 @@ class PathOrderedGeometricMHA(nn.Module):
         params = [p for p in self.parameters() if p.requires_grad]
         track = torch.is_grad_enabled() and (x.requires_grad or bool(params))
         if track:
-            if return_geometry:
-                raise NotImplementedError(
-                    "holonomyawareattention_amd kernel path does not support this call: "
-                    "return_geometry under autograd (the geometry output is not differentiable)")
-            if not tril:
-                raise NotImplementedError(
-                    "holonomyawareattention_amd kernel path does not support this call: under autograd "
-                    "only causal mode with attn_mask == tril(L) (the fused backward's path) is supported")
-            return self._forward_autograd(x), None
+            if tril and not return_geometry:
+                return self._forward_autograd(x), None
+            with torch.no_grad():
+                y, geo = self._forward_exact(x, attn_mask, return_geometry) if not tril else \
+                    self._forward_kernels(x, True)
+            what = "the geometry output" if tril else \
+                ("inert mode" if self.mode != "causal" else "an attention mask other than tril(L)")
+            deps = [x] + params
+            if geo is None:
+                return _ForwardOnly.apply(what, 1, y, *deps), None
+            y, C, Hm = _ForwardOnly.apply(what, 3, y, geo["C"], geo["H"], *deps)
+            return y, {"C": C, "H": Hm}
         if not tril:
             return self._forward_exact(x, attn_mask, return_geometry)
+        return self._forward_kernels(x, return_geometry)
+
+    def _forward_kernels(self, x: torch.Tensor, return_geometry: bool
+                         ) -> Tuple[torch.Tensor, Optional[Dict[str, torch.Tensor]]]:
+        """The causal + tril forward on the gfx950 kernels, without autograd."""
+        B, L, D = x.shape
         ev = self._stage_events
         with torch.no_grad():
             if ev is not None:

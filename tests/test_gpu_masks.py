@@ -23,7 +23,7 @@ import torch
 
 from holonomyawareattention_amd import kernels
 from oracle import holo_ref as R
-from tests._util import layer, make_module
+from tests._util import tril, layer, make_module
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -145,9 +145,31 @@ def test_modes_agree_on_the_flat_connection():
     assert np.abs(yc - yi).max() <= 2e-6
 
 
-def test_exact_path_under_autograd_raises():
+def test_exact_path_under_autograd_forward_only():
+    """Under autograd (x requiring grad, or only the parameters, as in an eval()
+    model outside torch.no_grad()) the exact path and the geometry output run
+    their forward, bit-identical to the forward with gradients off; only the
+    backward raises NotImplementedError (no gfx950 backward for them)."""
     x, W = layer(73, 1, 16, 24, 2, dtype=torch.float32)
     m = make_module(W, 24, 2, 0.5, "additive", torch.float32, DEV)
-    xt = torch.as_tensor(x).to(DEV).requires_grad_(True)
-    with pytest.raises(NotImplementedError):
-        m(xt, attn_mask=None)
+    xt = torch.as_tensor(x).to(DEV, torch.float32)
+    mask = tril(16, DEV)
+    with torch.no_grad():
+        y0, _ = m(xt, attn_mask=None)
+        yg0, g0 = m(xt, attn_mask=mask, return_geometry=True)
+    xg = xt.clone().requires_grad_(True)
+    y1, _ = m(xg, attn_mask=None)                       # x and the parameters require grad
+    assert y1.requires_grad and torch.equal(y1.detach(), y0)
+    with pytest.raises(NotImplementedError, match="attention mask other than tril"):
+        y1.sum().backward()
+    y2, _ = m.eval()(xt, attn_mask=None)                # only the parameters require grad
+    assert y2.requires_grad and torch.equal(y2.detach(), y0)
+    yg1, g1 = m(xg, attn_mask=mask, return_geometry=True)
+    assert torch.equal(yg1.detach(), yg0)
+    assert torch.equal(g1["C"].detach(), g0["C"]) and torch.equal(g1["H"].detach(), g0["H"])
+    with pytest.raises(NotImplementedError, match="geometry output"):
+        g1["C"].sum().backward()
+    m.mode = "inert"
+    y3, _ = m(xg, attn_mask=mask)
+    with pytest.raises(NotImplementedError, match="inert mode"):
+        y3.sum().backward()

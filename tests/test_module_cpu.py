@@ -74,3 +74,24 @@ def test_unsupported_calls_raise(kind):
     with pytest.raises(NotImplementedError):
         m(x, attn_mask=mask)
     assert not m._kernel_supported(x, mask)
+
+
+def test_forward_only_outputs_raise_on_backward():
+    """The outputs of calls with no gfx950 backward (exact path, geometry
+    output) pass through unchanged and keep the graph to x and the parameters;
+    backward raises NotImplementedError naming the call."""
+    from holonomyawareattention_amd.attention_kernel import _ForwardOnly
+    x = torch.randn(2, 3, requires_grad=True)
+    w = torch.nn.Parameter(torch.randn(3))
+    y0, c0 = torch.randn(2, 3), torch.randn(4)
+    y = _ForwardOnly.apply("inert mode", 1, y0, x, w)
+    assert y.requires_grad and torch.equal(y.detach(), y0)
+    with pytest.raises(NotImplementedError, match="inert mode"):
+        y.sum().backward()
+    y, c = _ForwardOnly.apply("the geometry output", 2, y0, c0, x, w)
+    assert torch.equal(y.detach(), y0) and torch.equal(c.detach(), c0) and c.requires_grad
+    with pytest.raises(NotImplementedError, match="geometry output"):
+        (y.sum() + c.sum()).backward()
+    with torch.no_grad():
+        y = _ForwardOnly.apply("x", 1, y0, x, w)
+    assert not y.requires_grad
