@@ -47,14 +47,10 @@ __device__ __forceinline__ void store_tile_output(const AttnArgs& a, float* Os, 
   const float lt = pair_sum(l_run);
   const float inv = __builtin_amdgcn_rcpf(fmaxf(lt, 1e-20f));
   if (a.lse && g == 0 && qw + lr < a.T) a.lse[(int64_t)bh * a.Tp + qw + lr] = m_run + __log2f(lt);
-  static_for<DP / 32>([&](auto db) {
-    static_for<16>([&](auto r) {
-      Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][(int)r] * inv;
-    });
-  });
-  __syncthreads();
   // items (row, 8 consecutive 3-dim groups = 24 dims); a row's 8 quaternions
-  // are 128 contiguous bytes in fp32, 64 in int16
+  // are 128 contiguous bytes in fp32, 64 in int16. Their loads are issued
+  // before the staging (the loop's registers are free by then: O and the
+  // quaternions fit), so the staging and its barrier cover their latency.
   typedef typename std::conditional<PQ16, u32x2, f32x4>::type pq_t;
   const pq_t pq_ident = [] {
     if constexpr (PQ16) return u32x2{1u, 0u};            // (1, 0, 0, 0)
@@ -73,6 +69,12 @@ __device__ __forceinline__ void store_tile_output(const AttnArgs& a, float* Os, 
       static_for<8>([&](auto jb) { pq[it][jb] = (row_ok && 8 * gi + jb < a.nb) ? base[jb] : pq_ident; });
     }
   });
+  static_for<DP / 32>([&](auto db) {
+    static_for<16>([&](auto r) {
+      Os[(32 * w + lr) * C::OS + 32 * db + 8 * (r >> 2) + 4 * g + (r & 3)] = O[db][(int)r] * inv;
+    });
+  });
+  __syncthreads();
   // item = (row, 8 consecutive 3-dim groups = 24 dims), quaternions in pq
   static_for<C::EPI>([&](auto it) {
     const int idx = tid + it * kThreads, r = idx / C::NG8, gi = idx % C::NG8;
