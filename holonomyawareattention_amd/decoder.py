@@ -67,6 +67,10 @@ def _fused_norms(mod: nn.Module, h: torch.Tensor) -> bool:
         return False
     if torch.is_grad_enabled() and (h.requires_grad or any(p.requires_grad for p in mod.parameters())):
         return False
+    for ln in mod.modules():             # the kernel takes affine norms with weights of h's dtype and device
+        if isinstance(ln, nn.LayerNorm) and (ln.weight is None or ln.bias is None or ln.weight.dtype != h.dtype
+                                             or ln.bias.dtype != h.dtype or ln.weight.device != h.device):
+            return False
     e16 = 16 // h.element_size()
     d = h.shape[-1]
     return d % e16 == 0 and d <= 1024 * e16

@@ -35,6 +35,26 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def _one_gpu(what: str, *tensors: Optional[torch.Tensor]) -> torch.device:
+    """The device of `tensors` (None entries skipped): every one must live on
+    the same GPU, since the kernels dereference their data pointers as device
+    addresses. Raises ValueError otherwise, before anything is launched."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+            raise ValueError(f"{what}: every tensor must be on a GPU "
+                             f"(got {t.device if isinstance(t, torch.Tensor) else type(t).__name__})")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{what}: all tensors must be on one device ({dev} and {t.device})")
+    if dev is None:
+        raise ValueError(f"{what}: no tensor given")
+    return dev
+
+
 def _token_view(t: torch.Tensor, B: int, T: int, H: int, width: int, name: str):
     """(B, T, H, width) view with unit inner stride and row-major (b, t) rows.
     Returns (row_stride, head_stride) in elements (row stride 0: one row
@@ -69,13 +89,16 @@ def qkvg_projection(x: torch.Tensor, w_qkv: torch.Tensor, w_gq: Optional[torch.T
     """holo_qkvg_proj_fwd: x (B, T, K) bf16 -> qkv (B, T, n_qkv) bf16 = x w_qkv^T
     and g (B, T, n_gen) fp32 = x_t w_gq^T + x_{(t+1) mod T} w_gk^T (None when
     w_gq is None). Weights (n, K) bf16 (the nn.Linear layout)."""
+    _one_gpu("qkvg_projection", x, w_qkv, w_gq, w_gk)
     lib = _lib.load()
-    if x.dim() != 3 or x.dtype != torch.bfloat16 or x.device.type != "cuda":
+    if x.dim() != 3 or x.dtype != torch.bfloat16:
         raise ValueError("qkvg_projection: x must be a (B, T, K) bfloat16 GPU tensor")
     B, T, K = (int(n) for n in x.shape)
     x2 = x.reshape(B * T, K)
     if x2.stride(1) != 1:
         raise ValueError("qkvg_projection: x rows must be contiguous")
+    if (w_gq is None) != (w_gk is None):
+        raise ValueError("qkvg_projection: w_gq and w_gk go together")
     ws = [w_qkv] + ([w_gq, w_gk] if w_gq is not None else [])
     for w in ws:
         if w.dtype != torch.bfloat16 or w.dim() != 2 or w.shape[1] != K or not w.is_contiguous() \
@@ -114,12 +137,10 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
     holo_geom_scan_fwd_static, whose chained state lives in the library's
     per-device static array (no workspace; inputs whose state exceeds it
     raise NotImplementedError; calls that overlap on one device race)."""
+    dev = _one_gpu("geom_scan", k, q, v, gq, gk, status)
     lib = _lib.load()
     B, T, H, d = k.shape
     nb = d // 3
-    dev = k.device
-    if dev.type != "cuda":
-        raise ValueError("geom_scan: tensors must be on a GPU")
     dt = k.dtype
     if dt not in _DT:
         raise ValueError(f"geom_scan: unsupported dtype {dt}")
@@ -181,6 +202,7 @@ def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tenso
 def workspace_status(ws: torch.Tensor, status: torch.Tensor) -> None:
     """Copy the status word of a chained workspace (HOLO_WS_* bits) into
     `status`, an int32 device tensor of one element, on the current stream."""
+    _one_gpu("workspace_status", ws, status)
     if status.dtype != torch.int32 or status.numel() != 1 or status.device != ws.device:
         raise ValueError("workspace_status: status must be a one-element int32 tensor on the workspace's device")
     rc = _lib.load().holo_workspace_status(_ptr(ws), ws.numel() * ws.element_size(), _ptr(status),
@@ -197,6 +219,7 @@ def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.T
     fp32 operands, bf16 for 16-bit ones; float32 is allowed with any
     operands). `lse`, a (B, H, Tp) fp32 tensor, receives each query's log2
     softmax normaliser (what `attention_backward` needs)."""
+    _one_gpu("attention", qh, kh, vh_t, P, out, lse)
     lib = _lib.load()
     if P.dim() != 5:
         raise ValueError("attention: P must be (B, H, T, nb, 4)")
@@ -245,6 +268,7 @@ def attention_masked(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: 
     (the scan's holonomy, needed in causal mode); mask (T, T) bool (True =
     allowed) or None (every pair allowed). A row that allows no key is NaN.
     Returns o as a (B,T,H,d) tensor, or writes `out`."""
+    _one_gpu("attention_masked", qh, kh, vh_t, P, hol, mask, out)
     lib = _lib.load()
     if mode not in _MODE:
         raise ValueError(f"attention_masked: mode must be one of {sorted(_MODE)}")
@@ -298,6 +322,7 @@ def attention_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge_scale:
     writes dq, dk, dv ((B,T,H,d) views, dtype of o) and dgq, dgk ((B,T,H,m)
     fp32 views; gk/dgk None for the direct generator). P must be the fp32
     quaternions of the same forward, lse the normalisers its attention wrote."""
+    _one_gpu("attention_backward", qh, kh, vh_t, P, lse, o, dout, dq, dk, dv, gq, gk, dgq, dgk, workspace)
     lib = _lib.load()
     B, H, T = (int(n) for n in P.shape[:3])
     dev, dt = qh.device, qh.dtype
@@ -329,6 +354,8 @@ def attention_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge_scale:
     gv = [(0, 0) if t is None else _token_view(t, B, T, H, m, n)
           for n, t in (("gq", gq), ("gk", gk), ("dgq", dgq), ("dgk", dgk))]
     need = int(lib.holo_attn_bwd_workspace_size(B, T, H, d, _DT[dt]))
+    if workspace is not None and not workspace.is_contiguous():
+        raise ValueError("attention_backward: workspace must be contiguous")
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     mode = _lib.HOLO_GEN_ADDITIVE if gk is not None else _lib.HOLO_GEN_DIRECT
@@ -344,6 +371,7 @@ def attention_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge_scale:
 
 def quat_to_dense(quat: torch.Tensor, d: int) -> torch.Tensor:
     """(..., nb, 4) fp32 quaternions -> (..., d, d) fp32 block rotations."""
+    _one_gpu("quat_to_dense", quat)
     lib = _lib.load()
     nb = d // 3
     if quat.shape[-2:] != (nb, 4) or quat.dtype != torch.float32 or not quat.is_contiguous():
@@ -374,6 +402,7 @@ def decode_geom(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g_prev: Optio
     output g in direct mode (gk None); not read when t = 0. P (B,H,nb,4) fp32
     is updated in place from P_{t-1} to P_t; qh (B,H,Dp) receives P_t^T q_t
     and row t of the caches the transported key and value."""
+    _one_gpu("decode_geom", k, q, v, g_prev, gk, P, qh, kh_cache, vh_cache)
     lib = _lib.load()
     B, H, d = k.shape
     nb = d // 3
@@ -413,16 +442,32 @@ def decode_workspace_bytes(B: int, H: int, d: int, t: int) -> int:
 def decode_attention(qh: torch.Tensor, kh_cache: torch.Tensor, vh_cache: torch.Tensor, P: torch.Tensor,
                      t: int, d: int, scale: float, out: Optional[torch.Tensor] = None,
                      workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """o_t (B,H,d) = P_t sum_{j<=t} softmax_j(scale qh . kh_j) vh_j over cache rows 0..t."""
+    """o_t (B,H,d) = P_t sum_{j<=t} softmax_j(scale qh . kh_j) vh_j over cache rows 0..t
+    (qh, the caches and P as decode_geom leaves them)."""
+    dev = _one_gpu("decode_attention", qh, kh_cache, vh_cache, P, out, workspace)
     lib = _lib.load()
+    dt = qh.dtype
+    if dt not in _DT or qh.dim() != 3:
+        raise ValueError("decode_attention: qh must be a (B, H, Dp) float32/bfloat16 tensor")
     B, H, Dp = (int(n) for n in qh.shape)
-    dev, dt = qh.device, qh.dtype
     nb = d // 3
-    cap = int(kh_cache.shape[2])
+    if Dp != padded_head_dim(d) or not qh.is_contiguous():
+        raise ValueError(f"decode_attention: qh must be a contiguous (B, H, {padded_head_dim(d)}) tensor")
+    cap = int(kh_cache.shape[2]) if kh_cache.dim() == 4 else -1
+    if tuple(kh_cache.shape) != (B, H, cap, Dp) or not kh_cache.is_contiguous() or kh_cache.dtype != dt:
+        raise ValueError("decode_attention: kh_cache must be a contiguous (B, H, capacity, Dp) tensor of qh's dtype")
+    if tuple(vh_cache.shape) != (B, H, cap // 64, Dp, 64) or not vh_cache.is_contiguous() or vh_cache.dtype != dt:
+        raise ValueError("decode_attention: vh_cache must be a contiguous (B, H, capacity/64, Dp, 64) tensor")
+    if tuple(P.shape) != (B, H, nb, 4) or P.dtype != torch.float32 or not P.is_contiguous():
+        raise ValueError("decode_attention: P must be a contiguous fp32 (B, H, nb, 4) tensor")
     if out is None:
         out = torch.empty((B, H, d), dtype=dt, device=dev)
+    elif out.dtype != dt:
+        raise ValueError("decode_attention: out must have qh's dtype")
     o_s = _bh_view(out, B, H, d, "out")
     need = int(lib.holo_decode_attn_workspace_size(B, H, d, int(t)))
+    if workspace is not None and not workspace.is_contiguous():
+        raise ValueError("decode_attention: workspace must be contiguous")
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     rc = lib.holo_decode_attn_fwd(B, H, d, int(t), cap, _DT[dt], float(scale),
@@ -438,8 +483,9 @@ def add_layernorm(x: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor, bi
     """h = x + delta and y = LayerNorm(h) (weight, bias, eps over the last
     dimension) in one pass: the residual add and the next norm of a pre-LN
     decoder. Returns (h, y), both shaped like x."""
+    _one_gpu("add_layernorm", x, delta, weight, bias)
     lib = _lib.load()
-    if x.shape != delta.shape or x.dtype != delta.dtype or x.dtype not in _DT or x.device.type != "cuda":
+    if x.shape != delta.shape or x.dtype != delta.dtype or x.dtype not in _DT:
         raise ValueError("add_layernorm: x and delta must be GPU tensors of one shape and dtype (fp32/bf16)")
     d = int(x.shape[-1])
     if tuple(weight.shape) != (d,) or tuple(bias.shape) != (d,) or weight.dtype != x.dtype or bias.dtype != x.dtype:

@@ -80,3 +80,18 @@ def test_decoder_fused_norms_match_torch_path():
     err = (h_fused - h_torch).abs().max().item()
     print(f"decoder fused norms vs torch: max-abs {err:.3e} (max |h| {scale:.2f})")
     assert err <= 1e-4 * scale, err
+
+
+def test_fused_norms_predicate_needs_matching_affine_norms():
+    """The fused add + LayerNorm path is taken only for affine norms whose
+    weights have the activations' dtype and device; otherwise the block runs
+    torch's ops (no kernel launch in this test: the predicate alone)."""
+    from holonomyawareattention_amd.decoder import HoloBlock, _fused_norms
+    blk = HoloBlock(192, 2, 0.3, "additive").to(DEV, torch.bfloat16).eval()
+    h = torch.zeros(1, 4, 192, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        assert _fused_norms(blk, h)
+        blk.ln2.float()                                   # fp32 weights with bf16 activations
+        assert not _fused_norms(blk, h)
+        blk.ln2 = torch.nn.LayerNorm(192, elementwise_affine=False).to(DEV, torch.bfloat16)
+        assert not _fused_norms(blk, h)
