@@ -72,7 +72,7 @@ C_SMOKE_BIN = os.path.join(PKG, "_build", "abi_smoke")
 
 def build_c_smoke() -> str:
     """Compile the C caller of the ABI (tests/c/abi_smoke.c, which also calls
-    the C binding of INTEGRATION.md, tests/c/integration_example.c) with gcc
+    the documented C binding example, tests/c/integration_example.c) with gcc
     against the HIP runtime and this library (no PyTorch); returns the
     binary's path. A stale signature in either fails here."""
     os.makedirs(os.path.dirname(C_SMOKE_BIN), exist_ok=True)

@@ -3,7 +3,7 @@
  * holo_geom_scan_fwd + holo_attn_fwd (the causal tril path) and
  * holo_attn_masked_fwd (the ring mask, causal mode) on fp32 inputs read from
  * files, the bf16 path through holo_example_core_bf16 (tests/c/
- * integration_example.c, the C binding INTEGRATION.md shows) on the same
+ * integration_example.c, the documented C binding example) on the same
  * inputs rounded to bf16, outputs written to files; plus the error path of a
  * bad call and the scan's workspace status.
  *

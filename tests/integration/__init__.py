@@ -1,1 +1,1 @@
-"""The reference-side bindings shown in INTEGRATION.md, as runnable files."""
+"""The reference-side bindings of the integration guide, as runnable files."""

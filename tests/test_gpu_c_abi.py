@@ -4,7 +4,7 @@ holo_attn_fwd (causal, tril) and holo_attn_masked_fwd (ring mask), fp32,
 against the float64 oracle on the same inputs; the driver also checks the
 error path (status code and message of a bad call).
 
-The driver also runs the C binding INTEGRATION.md shows
+The driver also runs the documented C binding example
 (tests/c/integration_example.c: the bf16 path with fp16 operands, o in fp32)
 on the same q, k, v rounded to bf16.
 

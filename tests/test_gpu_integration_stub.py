@@ -1,4 +1,4 @@
-"""The Python binding INTEGRATION.md shows (tests/integration/
+"""The documented Python binding (tests/integration/
 attention_kernel_mi355x.py: ctypes on the library, torch for memory and the
 stream) against the fp64 oracle. A stale signature in that file fails here.
 

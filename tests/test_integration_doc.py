@@ -1,4 +1,4 @@
-"""INTEGRATION.md's code blocks are the committed files they claim to be.
+"""The integration guide's code blocks are the committed files they claim to be.
 
 A block preceded by `<!-- file: <path> -->` must equal that file byte for
 byte; the files themselves are compiled (tests/c/integration_example.c, by
@@ -53,7 +53,7 @@ def _top_level_args(text: str, open_at: int) -> tuple:
 
 
 def test_every_c_snippet_call_has_the_header_arity():
-    """Every holo_* call in INTEGRATION.md's C snippets (other than those
+    """Every holo_* call in the integration guide's C snippets (other than those
     eliding arguments with '...') passes as many arguments as the header's
     prototype declares, so a signature change that the page missed fails here."""
     hdr = open(os.path.join(REPO, "include", "holo_mi355x.h")).read()
