@@ -1,0 +1,697 @@
+"""Cases run on the CPU emulation of the kernels (test infrastructure only):
+each builds seeded inputs in guarded "device" buffers, calls the C ABI of
+tests/emu/_build/libholo_emu.so exactly as a caller of libholo_mi355x.so would
+(the layouts of include/holo_mi355x.h), and measures the outputs against the
+oracle (oracle/holo_ref.py) and the layouts' invariants (zero padding).
+
+    python -m tests.emu.cases <case> '<json parameters>' [<case> '<json>' ...]
+
+(started by tests/emu/device.run_child with AddressSanitizer preloaded).
+Prints one JSON object per case and, last, {"cases": [...], "stats": ...}.
+A kernel access outside its buffers aborts the process with a report.
+"""
+from __future__ import annotations
+
+import json
+import math
+import sys
+import time
+
+import numpy as np
+
+from tests.emu.device import Emu, round_bf16
+from holonomyawareattention_amd import synth
+from oracle import holo_ref as R
+
+F32, BF16, F16 = 0, 1, 2
+QUAT_F32, QUAT_S16 = 0, 1
+GEN_ADD, GEN_DIRECT = 0, 1
+MODE_CAUSAL, MODE_INERT = 0, 1
+_NP = {F32: np.float32, F16: np.float16}
+
+
+def _dtype(code):
+    return "bf16" if code == BF16 else _NP[code]
+
+
+def padded_head_dim(d):
+    return (d + 31) // 32 * 32
+
+
+def padded_seq(T):
+    return (T + 63) // 64 * 64
+
+
+def quat_to_mat(q: np.ndarray) -> np.ndarray:
+    """(..., 4) quaternions (w, x, y, z) -> (..., 3, 3): the homogeneous
+    rotation (1/|q|^2)[...], the map the kernels apply."""
+    w, x, y, z = (q[..., i].astype(np.float64) for i in range(4))
+    n = w * w + x * x + y * y + z * z
+    R_ = np.stack([
+        np.stack([w * w + x * x - y * y - z * z, 2 * (x * y - w * z), 2 * (x * z + w * y)], -1),
+        np.stack([2 * (x * y + w * z), w * w - x * x + y * y - z * z, 2 * (y * z - w * x)], -1),
+        np.stack([2 * (x * z - w * y), 2 * (y * z + w * x), w * w - x * x - y * y + z * z], -1)], -2)
+    return R_ / n[..., None, None]
+
+
+class Layer:
+    """Seeded q, k, v (B, T, H, d) and additive generator halves gq, gk
+    (B, T, H, m), as the projections would hand them to the scan."""
+
+    def __init__(self, seed, B, T, H, d, io, es, gen_scale=1.0):
+        rng = np.random.default_rng(seed)
+        self.B, self.T, self.H, self.d, self.es = B, T, H, d, es
+        self.nb = d // 3
+        self.m = 3 * self.nb
+        f = (lambda a: round_bf16(a)) if io == BF16 else (lambda a: a.astype(np.float32).astype(np.float64))
+        self.q, self.k, self.v = (f(rng.standard_normal((B, T, H, d))) for _ in range(3))
+        self.gq = (rng.standard_normal((B, T, H, self.m)) * gen_scale).astype(np.float32).astype(np.float64)
+        self.gk = (rng.standard_normal((B, T, H, self.m)) * gen_scale).astype(np.float32).astype(np.float64)
+
+    def a(self, gen_mode):
+        bh = lambda u: u.transpose(0, 2, 1, 3)
+        if gen_mode == GEN_DIRECT:
+            return self.es * bh(self.gq)
+        return self.es * (bh(self.gq) + np.roll(bh(self.gk), -1, axis=2))
+
+
+def scan(emu: Emu, L: Layer, io, op, p_format, gen_mode=GEN_ADD, mode=MODE_CAUSAL, static=False):
+    B, T, H, d, nb, m = L.B, L.T, L.H, L.d, L.nb, L.m
+    Dp, Tp = padded_head_dim(d), padded_seq(T)
+    q, k, v = (emu.to_dev(u, _dtype(io)) for u in (L.q, L.k, L.v))
+    gq = emu.to_dev(L.gq, np.float32)
+    gk = emu.to_dev(L.gk, np.float32) if gen_mode == GEN_ADD else None
+    qh = emu.empty((B, H, Tp, Dp), _dtype(op))
+    kh = emu.empty((B, H, Tp, Dp), _dtype(op))
+    vh = emu.empty((B, H, Tp // 64, Dp, 64), _dtype(op))
+    P = emu.empty((B, H, T, nb, 4), np.float32 if p_format == QUAT_F32 else np.int16)
+    hol = emu.empty((B, H, nb, 4), np.float32)
+    lib = emu.lib
+    common = (B, T, H, d, gen_mode, float(L.es), io, op, F32, p_format, mode,
+              gq.ptr, H * m, m, gk.ptr if gk else None, H * m if gk else 0, m if gk else 0,
+              q.ptr, H * d, d, k.ptr, H * d, d, v.ptr, H * d, d,
+              qh.ptr, kh.ptr, vh.ptr, P.ptr if nb else None, hol.ptr if nb else None)
+    if static:
+        emu.check(lib.holo_geom_scan_fwd_static(*common, None), "holo_geom_scan_fwd_static")
+        ws = None
+    else:
+        n = int(lib.holo_geom_scan_workspace_size(B, T, H, d))
+        ws = emu.empty((max(n, 1),), np.uint8)
+        emu.check(lib.holo_geom_scan_fwd(*common, ws.ptr, n, None), "holo_geom_scan_fwd")
+    return dict(q=q, k=k, v=v, gq=gq, gk=gk, qh=qh, kh=kh, vh=vh, P=P, hol=hol, ws=ws)
+
+
+def unpack_vh(vh: np.ndarray, T: int) -> np.ndarray:
+    B, H, nch, Dp, C = vh.shape
+    return vh.transpose(0, 1, 2, 4, 3).reshape(B, H, nch * C, Dp)[:, :, :T]
+
+
+def case_scan_attn(emu: Emu, p):
+    """holo_geom_scan_fwd then holo_attn_fwd against the fp64 oracle fed the
+    same q, k, v and generator: P, Hol, qh/kh/vh (and their zero padding),
+    per-head o."""
+    B, T, H, d = p["B"], p["T"], p["H"], p["d"]
+    io, op, pf = p.get("io", F32), p.get("op", F32), p.get("pf", QUAT_F32)
+    gen_mode, out = p.get("gen", GEN_ADD), p.get("out", F32)
+    L = Layer(p.get("seed", 1), B, T, H, d, io, p.get("es", 0.5))
+    s = scan(emu, L, io, op, pf, gen_mode, static=p.get("static", False))
+    nb, Dp, Tp = L.nb, padded_head_dim(d), padded_seq(T)
+    Pr, Holr = R.geometry_blocks(L.a(gen_mode))
+    bh = lambda u: u.transpose(0, 2, 1, 3)
+    qr, kr, vr = (R.apply_blocks_T(Pr, bh(u)) for u in (L.q, L.k, L.v))
+    res = {}
+    if nb:
+        Pg = s["P"].a.astype(np.float64)
+        res["P_err"] = float(np.abs(quat_to_mat(Pg) - Pr).max())
+        res["hol_err"] = float(np.abs(quat_to_mat(s["hol"].a) - Holr).max())
+    qhg, khg = emu.host(s["qh"], _dtype(op)), emu.host(s["kh"], _dtype(op))
+    vhg = unpack_vh(emu.host(s["vh"], _dtype(op)), Tp)
+    res["pad_nonzero"] = int(np.count_nonzero(qhg[:, :, T:]) + np.count_nonzero(qhg[..., d:])
+                             + np.count_nonzero(khg[:, :, T:]) + np.count_nonzero(khg[..., d:])
+                             + np.count_nonzero(vhg[:, :, T:]) + np.count_nonzero(vhg[..., d:]))
+    scale_ref = max(np.abs(qr).max(), np.abs(kr).max(), np.abs(vr).max())
+    res["qkvh_rel"] = float(max(np.abs(qhg[:, :, :T, :d] - qr).max(), np.abs(khg[:, :, :T, :d] - kr).max(),
+                                np.abs(vhg[:, :, :T, :d] - vr).max()) / scale_ref)
+    # attention on the exact operands the kernel reads
+    o = emu.empty((B, T, H, d), _dtype(out))
+    lse = emu.empty((B, H, Tp), np.float32)
+    scale = 1.0 / math.sqrt(d)
+    emu.check(emu.lib.holo_attn_fwd(B, T, H, d, op, out, pf, scale, s["qh"].ptr, s["kh"].ptr, s["vh"].ptr,
+                                    s["P"].ptr if nb else None, o.ptr, H * d, d, lse.ptr, None), "holo_attn_fwd")
+    Pm = quat_to_mat(s["P"].a.astype(np.float64)) if nb else np.zeros((B, H, T, 0, 3, 3))
+    oh = R.causal_attention64(qhg[:, :, :T, :d], khg[:, :, :T, :d], vhg[:, :, :T, :d], scale)
+    o_ref = R.apply_blocks(Pm, oh)
+    og = bh(emu.host(o, _dtype(out)))
+    res["o_err"] = float(np.abs(og - o_ref).max())
+    res["o_max"] = float(np.abs(o_ref).max())
+    if op != F32 and out == F32:
+        # the rounding of the softmax weights to the operand type (unit
+        # roundoff u), which the row sum shares: per 3-dim block at most
+        # 2u/(1-u) ||sum_j a_ij |vh_j| ||, plus fp32 products and sums
+        u = 2.0 ** -8 if op == BF16 else 2.0 ** -11
+        vh_ = vhg[:, :, :T, :d]
+        spread = R.causal_attention64(qhg[:, :, :T, :d], khg[:, :, :T, :d], np.abs(vh_), scale) * (2 * u / (1 - u))
+        blk = np.sqrt((spread[..., :3 * nb].reshape(*spread.shape[:-1], nb, 3) ** 2).sum(-1))
+        bound = np.concatenate([np.repeat(blk, 3, axis=-1), spread[..., 3 * nb:]], axis=-1)
+        bound = bound + (1e-5 + T * 2.0 ** -25) * np.abs(vh_).max()
+        res["o_err_over_bound"] = float((np.abs(og - o_ref) / bound).max())
+    # lse: log2 of the normaliser in units of scale*log2(e) times the score
+    s_ = np.einsum("bhid,bhjd->bhij", qhg[:, :, :T, :d], khg[:, :, :T, :d]) * scale * math.log2(math.e)
+    s_ = np.where(np.tril(np.ones((T, T), bool)), s_, -np.inf)
+    mx = s_.max(-1)
+    lse_ref = mx + np.log2(np.exp2(s_ - mx[..., None]).sum(-1))
+    res["lse_err"] = float(np.abs(lse.a[:, :, :T] - lse_ref).max())
+    return res
+
+
+def case_gemm(emu: Emu, p):
+    """holo_qkvg_proj_fwd against float64 products of the same bf16 inputs:
+    errors relative to the rounding bounds of test_gpu_gemm.py (<= 1 passes)."""
+    B, T, K, n_qkv, n_gen = p["B"], p["T"], p["K"], p["n_qkv"], p["n_gen"]
+    rows = p.get("rows")
+    M = B * T
+    rng = np.random.default_rng(p.get("seed", 3))
+    x = round_bf16(rng.standard_normal((M, K)))
+    wq = round_bf16(rng.standard_normal((n_qkv, K)) / math.sqrt(K))
+    wg0 = round_bf16(rng.standard_normal((n_gen, K)) / math.sqrt(K)) if n_gen else None
+    wg1 = round_bf16(rng.standard_normal((n_gen, K)) / math.sqrt(K)) if n_gen else None
+    xd, wqd = emu.to_dev(x, "bf16"), emu.to_dev(wq, "bf16")
+    g0d = emu.to_dev(wg0, "bf16") if n_gen else None
+    g1d = emu.to_dev(wg1, "bf16") if n_gen else None
+    qkv = emu.empty((M, n_qkv), "bf16")
+    g = emu.empty((M, n_gen), np.float32) if n_gen else None
+    if p.get("sample"):
+        emu.sample(*p["sample"])
+    emu.check(emu.lib.holo_qkvg_proj_fwd(M, T, K, n_qkv, n_gen, xd.ptr, K, wqd.ptr, g0d.ptr if g0d else None,
+                                         g1d.ptr if g1d else None, qkv.ptr, n_qkv, g.ptr if g else None, n_gen,
+                                         None), "holo_qkvg_proj_fwd")
+    emu.sample()
+    r = np.arange(M) if rows is None else np.asarray(rows)
+    xs = x[r]
+    xn = np.roll(x.reshape(B, T, K), -1, axis=1).reshape(M, K)[r]
+    ref_q, mag_q = xs @ wq.T, np.abs(xs) @ np.abs(wq).T
+    got_q = emu.host(qkv, "bf16")[r]
+    bq = 2.0 ** -8 * np.abs(ref_q) + (1 + 2.0 ** -8) * K * 2.0 ** -24 * mag_q
+    res = {"qkv_err_over_bound": float((np.abs(got_q - ref_q) / bq).max())}
+    if n_gen:
+        ref_g = xs @ wg0.T + xn @ wg1.T
+        mag_g = np.abs(xs) @ np.abs(wg0).T + np.abs(xn) @ np.abs(wg1).T
+        got_g = g.a.astype(np.float64)[r]
+        res["g_err_over_bound"] = float((np.abs(got_g - ref_g) / (2 * K * 2.0 ** -24 * mag_g)).max())
+    if p.get("keep"):
+        res["_qkv"], res["_g"] = qkv.a.copy(), (g.a.copy() if g else None)
+    return res
+
+
+def case_masked(emu: Emu, p):
+    """holo_attn_masked_fwd (exact path: any mask, causal mode's wrap branch
+    through the holonomy, inert mode) against oracle.exact_attention64 on the
+    same q, k, v and generator."""
+    B, T, H, d = p["B"], p["T"], p["H"], p["d"]
+    io, pf = p.get("io", F32), p.get("pf", QUAT_F32)
+    mode = MODE_INERT if p.get("mode") == "inert" else MODE_CAUSAL
+    L = Layer(p.get("seed", 4), B, T, H, d, io, p.get("es", 0.9))
+    s = scan(emu, L, io, io, pf, GEN_ADD, mode=mode)
+    kind = p.get("mask", "none")
+    mask = None
+    if kind == "ring":
+        mask = R.ring_mask(T)
+    elif kind == "tril":
+        mask = np.tril(np.ones((T, T), bool))
+    elif kind in ("random", "empty_row"):
+        mask = np.random.default_rng(5).random((T, T)) < 0.3
+        mask[np.arange(T), np.arange(T)] = True
+        if kind == "empty_row":
+            mask[T // 2] = False
+    nb, Tp = L.nb, padded_seq(T)
+    md = emu.to_dev(mask.astype(np.uint8), np.uint8) if mask is not None else None
+    o = emu.empty((B, T, H, d), _dtype(io))
+    n = int(emu.lib.holo_attn_masked_workspace_size(B, T, H, d, io, mode, int(mask is not None)))
+    ws = emu.empty((max(n, 1),), np.uint8)
+    scale = 1.0 / math.sqrt(d)
+    emu.check(emu.lib.holo_attn_masked_fwd(B, T, H, d, io, pf, mode, scale, s["qh"].ptr, s["kh"].ptr, s["vh"].ptr,
+                                           s["P"].ptr if nb else None,
+                                           s["hol"].ptr if (mode == MODE_CAUSAL and nb) else None,
+                                           md.ptr if md else None, T if md else 0, o.ptr, H * d, d, ws.ptr, n, None),
+              "holo_attn_masked_fwd")
+    Pr, Holr = R.geometry_blocks(L.a(GEN_ADD))
+    bh = lambda u: u.transpose(0, 2, 1, 3)
+    ref = R.exact_attention64(bh(L.q), bh(L.k), bh(L.v), Pr, Holr, scale, mask, "inert" if mode else "causal")
+    got = bh(emu.host(o, _dtype(io)))
+    nan_ref = np.isnan(ref)
+    res = {"nan_match": bool(np.array_equal(np.isnan(got), nan_ref)), "nan_rows": int(nan_ref.any(-1).sum())}
+    ok = ~nan_ref
+    res["o_err"] = float(np.abs(got[ok] - ref[ok]).max())
+    res["o_rel_fro"] = float(np.linalg.norm(got[ok] - ref[ok]) / np.linalg.norm(ref[ok]))
+    return res
+
+
+def case_bwd(emu: Emu, p):
+    """holo_attn_bwd after holo_geom_scan_fwd (fp32 quaternions) and
+    holo_attn_fwd (with lse): dq, dk, dv, dgq, dgk against the float64
+    backward of the same forward (oracle.attention_backward64 and
+    link_grad_from_cross), each relative to its largest entry."""
+    B, T, H, d = p["B"], p["T"], p["H"], p["d"]
+    io = p.get("io", F32)
+    gen_mode = p.get("gen", GEN_ADD)
+    es = p.get("es", 0.9)
+    L = Layer(p.get("seed", 6), B, T, H, d, io, es)
+    s = scan(emu, L, io, io, QUAT_F32, gen_mode)
+    nb, m, Tp = L.nb, L.m, padded_seq(T)
+    scale = 1.0 / math.sqrt(d)
+    o = emu.empty((B, T, H, d), _dtype(io))
+    lse = emu.empty((B, H, Tp), np.float32)
+    emu.check(emu.lib.holo_attn_fwd(B, T, H, d, io, io, QUAT_F32, scale, s["qh"].ptr, s["kh"].ptr, s["vh"].ptr,
+                                    s["P"].ptr if nb else None, o.ptr, H * d, d, lse.ptr, None), "holo_attn_fwd")
+    rng = np.random.default_rng(p.get("seed", 6) + 100)
+    do_h = rng.standard_normal((B, T, H, d))
+    do_h = round_bf16(do_h) if io == BF16 else do_h.astype(np.float32).astype(np.float64)
+    dout = emu.to_dev(do_h, _dtype(io))
+    dq, dk, dv = (emu.empty((B, T, H, d), _dtype(io)) for _ in range(3))
+    dgq = emu.empty((B, T, H, m), np.float32)
+    dgk = emu.empty((B, T, H, m), np.float32) if gen_mode == GEN_ADD else None
+    n = int(emu.lib.holo_attn_bwd_workspace_size(B, T, H, d, io))
+    ws = emu.empty((max(n, 1),), np.uint8)
+    gk = s["gk"]
+    emu.check(emu.lib.holo_attn_bwd(
+        B, T, H, d, gen_mode, float(es), io, F32, scale,
+        s["gq"].ptr, H * m, m, gk.ptr if gk else None, H * m if gk else 0, m if gk else 0,
+        s["qh"].ptr, s["kh"].ptr, s["vh"].ptr, s["P"].ptr if nb else None, lse.ptr,
+        o.ptr, H * d, d, dout.ptr, H * d, d,
+        dq.ptr, H * d, d, dk.ptr, H * d, d, dv.ptr, H * d, d,
+        dgq.ptr, H * m, m, dgk.ptr if dgk else None, H * m if dgk else 0, m if dgk else 0,
+        ws.ptr, n, None), "holo_attn_bwd")
+    bh = lambda u: u.transpose(0, 2, 1, 3)
+    a = L.a(gen_mode)
+    Pr, _ = R.geometry_blocks(a)
+    qh, kh, vh = (R.apply_blocks_T(Pr, bh(u)) for u in (L.q, L.k, L.v))
+    oh = R.causal_attention64(qh, kh, vh, scale)
+    doh = R.apply_blocks_T(Pr, bh(do_h))
+    dqh, dkh, dvh = R.attention_backward64(qh, kh, vh, oh, doh, scale)
+    b3 = lambda u: u[..., :3 * nb].reshape(*u.shape[:-1], nb, 3)
+    c = (np.cross(b3(oh), b3(doh)) + np.cross(b3(dqh), b3(qh)) + np.cross(b3(dkh), b3(kh))
+         + np.cross(b3(dvh), b3(vh)))
+    da = R.link_grad_from_cross(a.reshape(B, H, T, nb, 3), Pr, c).reshape(B, H, T, m)
+    ref = {"dq": R.apply_blocks(Pr, dqh), "dk": R.apply_blocks(Pr, dkh), "dv": R.apply_blocks(Pr, dvh),
+           "dgq": es * da}
+    got = {"dq": bh(emu.host(dq, _dtype(io))), "dk": bh(emu.host(dk, _dtype(io))),
+           "dv": bh(emu.host(dv, _dtype(io))), "dgq": bh(dgq.a.astype(np.float64))}
+    if dgk is not None:
+        ref["dgk"] = np.roll(es * da, 1, axis=2)
+        got["dgk"] = bh(dgk.a.astype(np.float64))
+    res = {}
+    for k_, r_ in ref.items():
+        res[k_ + "_rel"] = float(np.abs(got[k_] - r_).max() / max(np.abs(r_).max(), 1e-30))
+        res[k_ + "_fro"] = float(np.linalg.norm(got[k_] - r_) / max(np.linalg.norm(r_), 1e-30))
+    return res
+
+
+def case_decode(emu: Emu, p):
+    """Prefill by holo_geom_scan_fwd over tokens 0..T0-1 (its kh / vh_t rows
+    copied into caches of `cap` rows), then holo_decode_geom_fwd +
+    holo_decode_attn_fwd for tokens T0..T-1: each step's per-head o against
+    the full-sequence oracle at that position; the running P against the
+    oracle's P_{T-1}."""
+    B, T, H, d, T0 = p["B"], p["T"], p["H"], p["d"], p["T0"]
+    io = p.get("io", F32)
+    es = p.get("es", 0.7)
+    L = Layer(p.get("seed", 7), B, T, H, d, io, es)
+    nb, m, Dp = L.nb, L.m, padded_head_dim(d)
+    cap = (max(p.get("cap", T), T) + 63) // 64 * 64
+    # prefill: the scan of the prefix
+    Lp = Layer.__new__(Layer)
+    Lp.__dict__.update(L.__dict__)
+    Lp.T = T0
+    for nm in ("q", "k", "v", "gq", "gk"):
+        setattr(Lp, nm, getattr(L, nm)[:, :T0])
+    s = scan(emu, Lp, io, io, QUAT_F32, GEN_ADD)
+    Tp0 = padded_seq(T0)
+    kc = emu.empty((B, H, cap, Dp), _dtype(io))
+    vc = emu.empty((B, H, cap // 64, Dp, 64), _dtype(io))
+    kc.a[...] = 0
+    vc.a[...] = 0
+    kc.a[:, :, :Tp0] = s["kh"].a
+    vc.a[:, :, :Tp0 // 64] = s["vh"].a
+    Pst = emu.empty((B, H, nb, 4), np.float32)
+    Pst.a[...] = s["P"].a[:, :, T0 - 1]
+    qh = emu.empty((B, H, Dp), _dtype(io))
+    o = emu.empty((B, H, d), _dtype(io))
+    nws = int(emu.lib.holo_decode_attn_workspace_size(B, H, d, cap - 1))
+    ws = emu.empty((max(nws, 16),), np.uint8)
+    scale = 1.0 / math.sqrt(d)
+    # the full-sequence oracle
+    Pr, _ = R.geometry_blocks(L.a(GEN_ADD))
+    bh = lambda u: u.transpose(0, 2, 1, 3)
+    qr, kr, vr = (R.apply_blocks_T(Pr, bh(u)) for u in (L.q, L.k, L.v))
+    worst = 0.0
+    for t in range(T0, T):
+        tok = lambda u: emu.to_dev(u[:, t], _dtype(io))
+        q1, k1, v1 = tok(L.q), tok(L.k), tok(L.v)
+        gprev = emu.to_dev(L.gq[:, t - 1], np.float32)
+        gk1 = emu.to_dev(L.gk[:, t], np.float32)
+        emu.check(emu.lib.holo_decode_geom_fwd(B, H, d, t, cap, GEN_ADD, float(es), io, F32,
+                                               gprev.ptr, H * m, m, gk1.ptr, H * m, m,
+                                               q1.ptr, H * d, d, k1.ptr, H * d, d, v1.ptr, H * d, d,
+                                               Pst.ptr if nb else None, qh.ptr, kc.ptr, vc.ptr, None),
+                  "holo_decode_geom_fwd")
+        emu.check(emu.lib.holo_decode_attn_fwd(B, H, d, t, cap, io, scale, qh.ptr, kc.ptr, vc.ptr,
+                                               Pst.ptr if nb else None, o.ptr, H * d, d, ws.ptr, ws.nbytes, None),
+                  "holo_decode_attn_fwd")
+        oh = R.attention_rows64(qr, kr, vr, scale, np.array([t]))
+        o_ref = R.apply_blocks(Pr[:, :, t:t + 1], oh)[:, :, 0]
+        worst = max(worst, float(np.abs(emu.host(o, _dtype(io)) - o_ref).max()))
+        for b_ in (q1, k1, v1, gprev, gk1):
+            b_.free()
+    res = {"o_err": worst, "steps": T - T0}
+    if nb:
+        res["P_err"] = float(np.abs(quat_to_mat(Pst.a) - Pr[:, :, T - 1]).max())
+    return res
+
+
+def case_norm(emu: Emu, p):
+    """holo_add_layernorm_fwd: h = x + delta (rounded to dtype) and
+    LayerNorm(h) against float64 on the same rounded values."""
+    n, d = p["n"], p["d"]
+    io = p.get("io", F32)
+    rng = np.random.default_rng(p.get("seed", 8))
+    rnd = (lambda a: round_bf16(a)) if io == BF16 else (lambda a: a.astype(np.float32).astype(np.float64))
+    # four rows per workgroup (one per wave); a sampled run fills and checks only its rows
+    rows = np.arange(n) if not p.get("sample") else np.r_[0:min(n, 4 * p["sample"][0]), max(0, n - 4 * p["sample"][1]):n]
+    x, dl = np.zeros((n, d)), np.zeros((n, d))
+    x[rows] = rnd(rng.standard_normal((len(rows), d)))
+    dl[rows] = rnd(rng.standard_normal((len(rows), d)))
+    w, b = rnd(1 + 0.1 * rng.standard_normal(d)), rnd(0.1 * rng.standard_normal(d))
+    xd, dd, wd, bd = (emu.to_dev(u, _dtype(io)) for u in (x, dl, w, b))
+    h, y = emu.empty((n, d), _dtype(io)), emu.empty((n, d), _dtype(io))
+    if p.get("sample"):
+        emu.sample(*p["sample"])
+    emu.check(emu.lib.holo_add_layernorm_fwd(n, d, io, 1e-5, xd.ptr, d, dd.ptr, d, wd.ptr, bd.ptr, h.ptr, d, y.ptr,
+                                             d, None), "holo_add_layernorm_fwd")
+    emu.sample()
+    href = rnd(x + dl)[rows]
+    mu = href.mean(-1, keepdims=True)
+    var = ((href - mu) ** 2).mean(-1, keepdims=True)
+    yref = (href - mu) / np.sqrt(var + 1e-5) * w + b
+    return {"h_err": float(np.abs(emu.host(h, _dtype(io))[rows] - href).max()),
+            "y_err": float(np.abs(emu.host(y, _dtype(io))[rows] - yref).max()),
+            "y_max": float(np.abs(yref).max())}
+
+
+def case_quat_dense(emu: Emu, p):
+    """holo_quat_to_dense: block b of the dense matrix is the rotation of
+    quaternion b, identity on the leftover dims, zero elsewhere."""
+    n, d = p["n"], p["d"]
+    nb = d // 3
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((n, nb, 4)).astype(np.float32)
+    qd = emu.to_dev(q, np.float32)
+    out = emu.empty((n, d, d), np.float32)
+    emu.check(emu.lib.holo_quat_to_dense(n, d, qd.ptr if nb else None, out.ptr, None), "holo_quat_to_dense")
+    ref = np.zeros((n, d, d))
+    ref[:, np.arange(d), np.arange(d)] = 1.0
+    Rm = quat_to_mat(q.astype(np.float64))
+    for b_ in range(nb):
+        ref[:, 3 * b_:3 * b_ + 3, 3 * b_:3 * b_ + 3] = Rm[:, b_]
+    return {"err": float(np.abs(out.a - ref).max())}
+
+
+def case_status(emu: Emu, p):
+    """holo_workspace_status after a clean scan (0) and after a scan whose
+    fp16 operands overflow (HOLO_WS_OVERFLOW), copied into a device word."""
+    B, T, H, d = 1, 70, 2, 48
+    res = {}
+    for name, big in (("clean", 1.0), ("overflow", 1e5)):
+        L = Layer(10, B, T, H, d, BF16, 0.3)
+        L.v = round_bf16(L.v * big)
+        s = scan(emu, L, BF16, F16, QUAT_S16)
+        st = emu.empty((1,), np.uint32)
+        emu.check(emu.lib.holo_workspace_status(s["ws"].ptr, s["ws"].nbytes, st.ptr, None), "holo_workspace_status")
+        res[name] = int(st.a[0])
+        res[name + "_inf"] = int(np.isinf(s["vh"].a.astype(np.float64)).sum())
+    return res
+
+
+def case_layer(emu: Emu, p):
+    """The bf16 causal layer as the module runs it (holo_qkvg_proj_fwd ->
+    holo_geom_scan_fwd in direct mode on strided q/k/v views of the GEMM's
+    output, fp16 operands, int16 quaternions -> holo_attn_fwd with a bf16 or
+    fp32 o), with the row and head strides the module passes. "sample_gemm" /
+    "sample_attn" run only some workgroups of those independent launches (a
+    bounds check at full size); the chained scan always runs whole. With
+    "check", per-head o (fp32) against the fp64 oracle fed the same q, k, v
+    and generator, at rows "rows" (default all)."""
+    B, T, D, H = p["B"], p["T"], p["D"], p["H"]
+    d = D // H
+    nb, m = d // 3, 3 * (d // 3)
+    M, Dp, Tp = B * T, padded_head_dim(d), padded_seq(T)
+    es = p.get("es", 0.05)
+    rng = np.random.default_rng(p.get("seed", 11))
+    fill = p.get("fill", True)
+
+    def rand_bf16(shape, std):
+        if fill:
+            return emu.to_dev(rng.standard_normal(shape, dtype=np.float32) * np.float32(std), "bf16")
+        return emu.empty(shape, "bf16", mark=False)
+    x = rand_bf16((M, D), 1.0)
+    wq = rand_bf16((3 * D, D), 1 / math.sqrt(D))
+    wg0 = rand_bf16((H * m, D), 1 / math.sqrt(D))
+    wg1 = rand_bf16((H * m, D), 1 / math.sqrt(D))
+    qkv = emu.empty((M, 3 * D), "bf16", mark=fill)
+    g = emu.empty((M, H * m), np.float32, mark=fill)
+    t0 = time.time()
+    if p.get("sample_gemm"):
+        emu.sample(*p["sample_gemm"])
+    emu.check(emu.lib.holo_qkvg_proj_fwd(M, T, D, 3 * D, H * m, x.ptr, D, wq.ptr, wg0.ptr, wg1.ptr,
+                                         qkv.ptr, 3 * D, g.ptr, H * m, None), "holo_qkvg_proj_fwd")
+    emu.sample()
+    if p.get("sample_gemm") and fill:   # unwritten outputs hold the marker; give the scan finite inputs
+        qkv.a[...] = f32_bits_small(qkv.a.shape, rng, "bf16")
+        g.a[...] = rng.standard_normal(g.a.shape).astype(np.float32)
+    t1 = time.time()
+    qh = emu.empty((B, H, Tp, Dp), np.float16, mark=fill)
+    kh = emu.empty((B, H, Tp, Dp), np.float16, mark=fill)
+    vh = emu.empty((B, H, Tp // 64, Dp, 64), np.float16, mark=fill)
+    P = emu.empty((B, H, T, nb, 4), np.int16, mark=fill)
+    if p.get("skip_scan"):            # unit quaternions for the epilogue
+        P.a[..., 0] = 32767
+    n = int(emu.lib.holo_geom_scan_workspace_size(B, T, H, d))
+    ws = emu.empty((max(n, 1),), np.uint8)
+    E = qkv.a.itemsize
+    st = emu.empty((1,), np.uint32)
+    st.a[0] = 0
+    if not p.get("skip_scan"):
+        emu.check(emu.lib.holo_geom_scan_fwd(B, T, H, d, GEN_DIRECT, float(es), BF16, F16, F32, QUAT_S16, MODE_CAUSAL,
+                                             g.ptr, H * m, m, None, 0, 0,
+                                             qkv.ptr, 3 * D, 3 * d, qkv.ptr + d * E, 3 * D, 3 * d,
+                                             qkv.ptr + 2 * d * E, 3 * D, 3 * d,
+                                             qh.ptr, kh.ptr, vh.ptr, P.ptr, None, ws.ptr, n, None),
+                  "holo_geom_scan_fwd")
+        emu.check(emu.lib.holo_workspace_status(ws.ptr, ws.nbytes, st.ptr, None), "holo_workspace_status")
+    t2 = time.time()
+    out = p.get("out", BF16)
+    o = emu.empty((B, T, H, d), _dtype(out), mark=fill)
+    if p.get("sample_attn"):
+        emu.sample(*p["sample_attn"])
+    emu.check(emu.lib.holo_attn_fwd(B, T, H, d, F16, out, QUAT_S16, 1.0 / math.sqrt(d), qh.ptr, kh.ptr, vh.ptr,
+                                    P.ptr, o.ptr, H * d, d, None, None), "holo_attn_fwd")
+    emu.sample()
+    t3 = time.time()
+    res = {"status": int(st.a[0]), "t_gemm": round(t1 - t0, 1), "t_scan": round(t2 - t1, 1), "t_attn": round(t3 - t2, 1)}
+    if p.get("check"):
+        rows = np.arange(T) if p.get("rows") is None else np.asarray(p["rows"])
+        qkvh = emu.host(qkv, "bf16").reshape(B, T, H, 3 * d)
+        bh = lambda u: u.transpose(0, 2, 1, 3)
+        qq, kk, vv = (bh(qkvh[..., i * d:(i + 1) * d]) for i in range(3))
+        a = es * bh(g.a.astype(np.float64).reshape(B, T, H, m))
+        Pr, _ = R.geometry_blocks(a)
+        o_ref = R.apply_blocks(Pr[:, :, rows], R.attention_rows64(*(R.apply_blocks_T(Pr, u) for u in (qq, kk, vv)),
+                                                                  1.0 / math.sqrt(d), rows))
+        og = bh(emu.host(o, _dtype(out)))[:, :, rows]
+        res["o_err"] = float(np.abs(og - o_ref).max())
+        res["o_max"] = float(np.abs(o_ref).max())
+    return res
+
+
+def f32_bits_small(shape, rng, kind):
+    from tests.emu.device import f32_to_bf16_bits
+    return f32_to_bf16_bits(rng.standard_normal(shape).astype(np.float32))
+
+
+def case_dma_modes(emu: Emu, p):
+    """The same launches with buffer->LDS data landing at the lane's covering
+    waitcnt (mode 0: a read before the wait sees the old LDS contents) and at
+    issue (mode 1: a stage still being read by another wave is overwritten
+    early): outputs must be bit-identical, or a wait or barrier is missing.
+    Covers the 16-bit attention ring and the projection GEMM ring."""
+    res = {}
+    outs = []
+    for mode in (0, 1):
+        emu.lds_dma_mode(mode == 1)
+        L = Layer(p.get("seed", 12), p["B"], p["T"], p["H"], p["d"], BF16, 0.5)
+        s = scan(emu, L, BF16, F16, QUAT_S16)
+        B, T, H, d = L.B, L.T, L.H, L.d
+        o = emu.empty((B, T, H, d), np.float32)
+        emu.check(emu.lib.holo_attn_fwd(B, T, H, d, F16, F32, QUAT_S16, 1.0 / math.sqrt(d), s["qh"].ptr, s["kh"].ptr,
+                                        s["vh"].ptr, s["P"].ptr, o.ptr, H * d, d, None, None), "holo_attn_fwd")
+        r = case_gemm(emu, dict(B=p["B"], T=p["T"], K=p["K"], n_qkv=3 * p["K"], n_gen=p["K"], seed=13, keep=True))
+        outs.append((o.a.copy(), r.pop("_qkv"), r.pop("_g")))
+    emu.lds_dma_mode(False)
+    res["attn_identical"] = bool(np.array_equal(outs[0][0], outs[1][0]))
+    res["gemm_identical"] = bool(np.array_equal(outs[0][1], outs[1][1]) and np.array_equal(outs[0][2], outs[1][2]))
+    return res
+
+
+def case_static_scan(emu: Emu, p):
+    """holo_geom_scan_fwd_static against holo_geom_scan_fwd on the same
+    inputs, bit for bit, on two calls in a row (the second smaller)."""
+    res = {}
+    for i, (T, H) in enumerate(((p["T"], p["H"]), (max(1, p["T"] // 3), 1))):
+        outs = []
+        for static in (False, True):
+            L = Layer(p.get("seed", 14), p["B"], T, H, p["d"], BF16, 0.7)
+            s = scan(emu, L, BF16, F16, QUAT_S16, static=static)
+            outs.append([s[k].a.copy() for k in ("qh", "kh", "vh", "P")])
+        res[f"identical_{i}"] = bool(all(np.array_equal(a, b) for a, b in zip(*outs)))
+    return res
+
+
+def case_layer_paths(emu: Emu, p):
+    """The scan and attention of the module's other layouts at a given shape,
+    for bounds (no oracle): "fp32" -- one fp32 GEMM output y5 (B, T, 3D + 2Hm)
+    holding q | k | v | gq | gk (row stride 3D + 2Hm), additive generator, fp32
+    operands and quaternions; "interaction" -- bf16 q | k | v (row stride 3D),
+    the edge MLP's unbiased output gq (B, T, Hm) fp32 and its bias broadcast
+    as gk with row stride 0, fp16 operands, int16 quaternions; "exact" -- the
+    fused GEMM's layout (direct generator), bf16 operands, int16 quaternions,
+    the scan in `mode` and holo_attn_masked_fwd with `mask` ("none" or
+    "ring"). Attention workgroups may be sampled; the scan runs whole."""
+    B, T, D, H = p["B"], p["T"], p["D"], p["H"]
+    d = D // H
+    nb, m = d // 3, 3 * (d // 3)
+    M, Dp, Tp = B * T, padded_head_dim(d), padded_seq(T)
+    rng = np.random.default_rng(p.get("seed", 15))
+    path = p["path"]
+    scale = 1.0 / math.sqrt(d)
+    if path == "fp32":
+        W = 3 * D + 2 * H * m
+        y5 = emu.to_dev(rng.standard_normal((M, W), dtype=np.float32) * 0.5, np.float32)
+        E = 4
+        base = y5.ptr
+        qp, kp, vp = base, base + d * E, base + 2 * d * E
+        gqp, gkp = base + 3 * D * E, base + (3 * D + H * m) * E
+        rs, hs, grs, gks = W, 3 * d, W, W
+        io = op = F32
+        pf = QUAT_F32
+        keep = [y5]
+    else:
+        qkv = emu.to_dev(rng.standard_normal((M, 3 * D), dtype=np.float32) * 0.5, "bf16")
+        gq = emu.to_dev(rng.standard_normal((M, H * m), dtype=np.float32), np.float32)
+        E = 2
+        qp, kp, vp = qkv.ptr, qkv.ptr + d * E, qkv.ptr + 2 * d * E
+        rs, hs, grs = 3 * D, 3 * d, H * m
+        if path == "interaction":
+            bias = emu.to_dev(rng.standard_normal(H * m).astype(np.float32) * 0.1, np.float32)
+            gqp, gkp, gks = gq.ptr, bias.ptr, 0
+            io, op, pf = BF16, F16, QUAT_S16
+            keep = [qkv, gq, bias]
+        else:                           # "exact": the fused GEMM's layout, direct generator, bf16 operands
+            gqp, gkp, gks = gq.ptr, None, 0
+            io, op, pf = BF16, BF16, QUAT_S16
+            keep = [qkv, gq]
+    gen_mode = GEN_DIRECT if gkp is None else GEN_ADD
+    mode = MODE_INERT if p.get("mode") == "inert" else MODE_CAUSAL
+    qh = emu.empty((B, H, Tp, Dp), _dtype(op))
+    kh = emu.empty((B, H, Tp, Dp), _dtype(op))
+    vh = emu.empty((B, H, Tp // 64, Dp, 64), _dtype(op))
+    P = emu.empty((B, H, T, nb, 4), np.float32 if pf == QUAT_F32 else np.int16)
+    hol = emu.empty((B, H, nb, 4), np.float32)
+    n = int(emu.lib.holo_geom_scan_workspace_size(B, T, H, d))
+    ws = emu.empty((max(n, 1),), np.uint8)
+    t0 = time.time()
+    emu.check(emu.lib.holo_geom_scan_fwd(B, T, H, d, gen_mode, 0.05, io, op, F32, pf, mode,
+                                         gqp, grs, m, gkp, gks if gkp else 0, m if gkp else 0,
+                                         qp, rs, hs, kp, rs, hs, vp, rs, hs,
+                                         qh.ptr, kh.ptr, vh.ptr, P.ptr, hol.ptr, ws.ptr, n, None), "holo_geom_scan_fwd")
+    st = emu.empty((1,), np.uint32)
+    emu.check(emu.lib.holo_workspace_status(ws.ptr, ws.nbytes, st.ptr, None), "holo_workspace_status")
+    t1 = time.time()
+    o = emu.empty((B, T, H, d), _dtype(io))
+    if path != "exact":
+        if p.get("sample_attn"):
+            emu.sample(*p["sample_attn"])
+        emu.check(emu.lib.holo_attn_fwd(B, T, H, d, op, io, pf, scale, qh.ptr, kh.ptr, vh.ptr, P.ptr, o.ptr, H * d, d,
+                                        None, None), "holo_attn_fwd")
+        emu.sample()
+    res = {"status": int(st.a[0]), "t_scan": round(t1 - t0, 1), "t_attn": round(time.time() - t1, 1)}
+    if path == "exact":               # the exact path's kernel on these operands
+        kind = p.get("mask", "none")
+        mask = R.ring_mask(T) if kind == "ring" else None
+        md = emu.to_dev(mask.astype(np.uint8), np.uint8) if mask is not None else None
+        om = emu.empty((B, T, H, d), _dtype(io))
+        nm = int(emu.lib.holo_attn_masked_workspace_size(B, T, H, d, io, mode, int(mask is not None)))
+        wm = emu.empty((max(nm, 1),), np.uint8)
+        if p.get("sample_attn"):
+            emu.sample(*p["sample_attn"])
+        emu.check(emu.lib.holo_attn_masked_fwd(B, T, H, d, io, pf, mode, scale, qh.ptr, kh.ptr, vh.ptr, P.ptr,
+                                               hol.ptr if mode == MODE_CAUSAL else None, md.ptr if md else None,
+                                               T if md else 0, om.ptr, H * d, d, wm.ptr, nm, None),
+                  "holo_attn_masked_fwd")
+        emu.sample()
+        res["t_attn"] = round(time.time() - t1, 1)
+    return res
+
+
+def case_decode_bounds(emu: Emu, p):
+    """Decode steps at the given positions for bounds (no oracle): caches of
+    `cap` rows (the scan's kh / vh_t layouts), holo_decode_geom_fwd whole,
+    holo_decode_attn_fwd with its split workgroups sampled."""
+    B, H, d, cap = p["B"], p["H"], p["d"], p["cap"]
+    io = p.get("io", BF16)
+    nb, m, Dp = d // 3, 3 * (d // 3), padded_head_dim(d)
+    kc = emu.empty((B, H, cap, Dp), _dtype(io), mark=False)
+    vc = emu.empty((B, H, cap // 64, Dp, 64), _dtype(io), mark=False)
+    Pst = emu.empty((B, H, nb, 4), np.float32)
+    Pst.a[...] = 0
+    Pst.a[..., 0] = 1
+    qh = emu.empty((B, H, Dp), _dtype(io))
+    o = emu.empty((B, H, d), _dtype(io))
+    nws = int(emu.lib.holo_decode_attn_workspace_size(B, H, d, cap - 1))
+    ws = emu.empty((max(nws, 16),), np.uint8)
+    rng = np.random.default_rng(16)
+    tok = lambda w, dt: emu.to_dev(rng.standard_normal((B, H, w)) * 0.5, dt)
+    res = {}
+    for t in p["steps"]:
+        q1, k1, v1 = (tok(d, _dtype(io)) for _ in range(3))
+        gp, gk1 = tok(m, np.float32), tok(m, np.float32)
+        emu.check(emu.lib.holo_decode_geom_fwd(B, H, d, t, cap, GEN_ADD, 0.05, io, F32, gp.ptr, H * m, m, gk1.ptr, H * m,
+                                               m, q1.ptr, H * d, d, k1.ptr, H * d, d, v1.ptr, H * d, d, Pst.ptr, qh.ptr,
+                                               kc.ptr, vc.ptr, None), "holo_decode_geom_fwd")
+        if p.get("sample"):
+            emu.sample(*p["sample"])
+        emu.check(emu.lib.holo_decode_attn_fwd(B, H, d, t, cap, io, 1.0 / math.sqrt(d), qh.ptr, kc.ptr, vc.ptr, Pst.ptr,
+                                               o.ptr, H * d, d, ws.ptr, ws.nbytes, None), "holo_decode_attn_fwd")
+        emu.sample()
+        res[f"finite_{t}"] = bool(np.isfinite(emu.host(o, _dtype(io))).all())
+    return res
+
+
+CASES = {"layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
+         "decode": case_decode, "norm": case_norm, "quat_dense": case_quat_dense, "status": case_status}
+
+
+def main(argv):
+    emu = Emu()
+    out = []
+    for name, params in zip(argv[0::2], argv[1::2]):
+        p = json.loads(params)
+        emu.reset_stats()
+        t0 = time.time()
+        r = CASES[name](emu, p)
+        r.update(case=name, params=p, seconds=round(time.time() - t0, 2), stats=emu.stats())
+        print(json.dumps(r), flush=True)
+        out.append(r)
+    print(json.dumps({"cases": out}), flush=True)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])

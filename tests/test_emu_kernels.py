@@ -1,0 +1,226 @@
+"""The product's HIP kernels executed on the CPU (tests/emu: the same sources
+compiled for x86-64 with AddressSanitizer, every lane a fiber, the gfx950
+matrix-core, buffer, LDS and cross-lane instructions emulated), called
+through the C ABI at the shapes of the -m gpu tests, against the float64
+oracle. Every global access is bounds-checked against guarded buffers of
+exactly the sizes include/holo_mi355x.h documents, every buffer resource's
+range against its allocation, dynamic LDS against the launch's LDS bytes: an
+out-of-bounds access aborts the child process with a report naming the
+kernel line, and every test of this file then fails with that report.
+
+This is parity evidence for the kernels' logic (index arithmetic, tiling,
+masking, chained carries, epilogues) independent of a GPU; it is not a
+measurement and does not model timing, caches or the hardware's exact
+rounding of exp2 / reciprocal / MFMA accumulation (the emulation computes
+those in double precision and rounds once).
+
+Tolerances (written per case below):
+  fp32 path   -- P, Hol within 2e-5; qh/kh/vh within 2e-5 relative; per-head
+                 o within 1e-5 * max(1, max|o|) (the fp32 bar); lse 1e-5.
+  16-bit path -- per-head o written in fp32, against the oracle fed the
+                 kernel's own operands and P: within the derived bound of
+                 tests/test_gpu_parity_bar.py (the softmax weights rounded to
+                 the operand type, unit roundoff 2^-8 bf16 / 2^-11 fp16), and
+                 with fp16 operands (the module's bf16 path) within 2e-3 (the
+                 bf16 bar); bf16 o within 2.5e-2 * max(1, max|o| / 4).
+  GEMM        -- every element within the rounding bounds of
+                 tests/test_gpu_gemm.py (err / bound <= 1).
+  exact path  -- fp32 max-abs 2e-5; bf16 max-abs 2.5e-2 and relative
+                 Frobenius 1e-2; NaN rows exactly where the oracle's are.
+  backward    -- fp32: each gradient within 2e-5 of its largest entry; bf16:
+                 relative Frobenius 3e-2.
+  decode      -- fp32 2e-5; bf16 2e-2 (per-head o per step).
+  LayerNorm   -- h exact (one rounding of x + delta); y within 1e-5 (fp32) or
+                 one bf16 rounding of |y| plus 1e-5 (bf16).
+"""
+from __future__ import annotations
+
+import os
+
+import pytest
+
+from tests.emu import build_emu, jobs
+
+F32, BF16, F16 = 0, 1, 2
+S16 = 1
+
+pytestmark = pytest.mark.skipif(not (os.path.exists(build_emu.CLANG) and os.path.exists(build_emu.ASAN_RT)),
+                                reason="the CPU emulation needs ROCm's clang and its AddressSanitizer runtime")
+
+CASES = []          # (id, case name, params, check(result) -> None)
+
+
+def _add(cid, name, params, check):
+    CASES.append((cid, name, params, check))
+
+
+def _bar16(o_max):
+    return 2.5e-2 * max(1.0, o_max / 4)
+
+
+# ---- scan + attention, fp32 (tests/test_gpu_parity.py, tests/test_gpu_shapes.py) ----
+def _fp32_scan_attn(r):
+    if "P_err" in r:
+        assert r["P_err"] < 2e-5 and r["hol_err"] < 2e-5, r
+    assert r["pad_nonzero"] == 0, r
+    assert r["qkvh_rel"] < 2e-5, r
+    assert r["o_err"] < 1e-5 * max(1.0, r["o_max"]), r
+    assert r["lse_err"] < 1e-5 * max(1.0, r["o_max"]), r
+
+
+for (B, T, D, H, es) in [(2, 150, 96, 2, 0.5), (1, 1, 48, 4, 1.5), (1, 65, 32, 2, 1.5), (2, 64, 36, 3, 0.05),
+                         (2, 300, 192, 2, 0.5), (1, 129, 96, 2, 0.5), (1, 7, 48, 4, 0.5), (2, 200, 64, 2, 0.5)]:
+    _add(f"scan_attn_f32_B{B}_T{T}_d{D // H}_H{H}", "scan_attn", dict(B=B, T=T, H=H, d=D // H, es=es), _fp32_scan_attn)
+for d in [3, 5, 8, 24, 33, 64, 72, 94, 96]:
+    for (B, T, H) in [(1, 129, 1), (2, 70, 3), (2, 1, 2)]:
+        _add(f"scan_attn_f32_sweep_d{d}_B{B}_T{T}_H{H}", "scan_attn", dict(B=B, T=T, H=H, d=d, es=0.7), _fp32_scan_attn)
+
+
+# ---- 16-bit operands (tests/test_gpu_parity_bar.py, tests/test_gpu_shapes.py) ----
+def _h16(out, op=F16):
+    def check(r):
+        assert r["pad_nonzero"] == 0, r
+        if out == F32:
+            assert r["o_err_over_bound"] <= 1.0, r
+            if op == F16:
+                assert r["o_err"] <= 2e-3, r
+        else:
+            assert r["o_err"] <= _bar16(r["o_max"]), r
+    return check
+
+
+for op in (BF16, F16):
+    for (B, T, D, H) in [(2, 300, 192, 2), (1, 129, 96, 2), (1, 7, 48, 4), (2, 200, 64, 2)]:
+        _add(f"scan_attn_op{op}_B{B}_T{T}_d{D // H}", "scan_attn",
+             dict(B=B, T=T, H=H, d=D // H, io=BF16, op=op, pf=S16, out=F32, es=0.5), _h16(F32, op))
+for d in [5, 33, 72, 94]:
+    _add(f"scan_attn_bf16_sweep_d{d}", "scan_attn", dict(B=1, T=129, H=2, d=d, io=BF16, op=F16, pf=S16, out=BF16, es=0.7),
+         _h16(BF16))
+for d in [32, 64, 96]:
+    for T in [1, 64, 65, 257]:
+        _add(f"scan_attn_xcd_grid_d{d}_T{T}", "scan_attn",
+             dict(B=2, T=T, H=4, d=d, io=BF16, op=F16, pf=S16, out=BF16, es=0.7), _h16(BF16))
+for (B, T, D, H, es) in [(2, 150, 96, 2, 0.5), (1, 65, 192, 2, 1.5), (2, 64, 144, 3, 0.05)]:
+    _add(f"scan_attn_f16_pf32_B{B}_T{T}_d{D // H}", "scan_attn",
+         dict(B=B, T=T, H=H, d=D // H, io=BF16, op=F16, pf=0, out=F32, es=es), _h16(F32))
+_add("scan_attn_direct_generator", "scan_attn", dict(B=2, T=150, H=2, d=96, io=BF16, op=F16, pf=S16, out=F32, gen=1),
+     _h16(F32))
+
+
+# ---- projection GEMM (tests/test_gpu_gemm.py) ----
+def _gemm(r):
+    assert r["qkv_err_over_bound"] <= 1.0, r
+    assert r["g_err_over_bound"] <= 1.0, r
+
+
+for (B, T, D, H) in [(3, 100, 128, 4), (5, 1, 128, 4), (2, 257, 192, 4), (1, 300, 384, 4)]:
+    _add(f"gemm_B{B}_T{T}_D{D}_H{H}", "gemm", dict(B=B, T=T, K=D, n_qkv=3 * D, n_gen=H * 3 * (D // H // 3)), _gemm)
+
+
+# ---- exact path (tests/test_gpu_masks.py) ----
+def _masked(io):
+    def check(r):
+        assert r["nan_match"], r
+        if io == F32:
+            assert r["o_err"] <= 2e-5, r
+        else:
+            assert r["o_err"] <= 2.5e-2 and r["o_rel_fro"] <= 1e-2, r
+    return check
+
+
+for mode in ("causal", "inert"):
+    for mask in ("none", "ring", "random", "tril", "empty_row"):
+        for (io, B, T, D, H) in [(F32, 2, 130, 96, 2), (BF16, 1, 200, 192, 2), (F32, 2, 70, 64, 4)]:
+            _add(f"masked_{mode}_{mask}_io{io}_B{B}_T{T}_d{D // H}", "masked",
+                 dict(B=B, T=T, H=H, d=D // H, io=io, mode=mode, mask=mask, pf=0 if io == F32 else S16), _masked(io))
+for d in [3, 5, 8, 24, 33, 64, 72, 94, 96]:
+    _add(f"masked_sweep_none_d{d}", "masked", dict(B=2, T=70, H=3, d=d, mode="causal", mask="none"), _masked(F32))
+    _add(f"masked_sweep_ring_inert_d{d}", "masked", dict(B=1, T=129, H=1, d=d, mode="inert", mask="ring"),
+         _masked(F32))
+
+
+# ---- fused backward (tests/test_gpu_backward.py) ----
+def _bwd(io):
+    def check(r):
+        for k, v in r.items():
+            if k.endswith("_rel") and io == F32:
+                assert v <= 2e-5, (k, r)
+            if k.endswith("_fro") and io == BF16:
+                assert v <= 3e-2, (k, r)
+    return check
+
+
+for (B, T, D, H, es) in [(2, 100, 96, 2, 0.9), (1, 130, 60, 4, 1.2), (2, 70, 64, 4, 0.5)]:
+    for gen in (0, 1):
+        _add(f"bwd_f32_gen{gen}_B{B}_T{T}_d{D // H}", "bwd", dict(B=B, T=T, H=H, d=D // H, es=es, gen=gen), _bwd(F32))
+_add("bwd_bf16_B2_T200_d96", "bwd", dict(B=2, T=200, H=2, d=96, es=0.3, io=BF16), _bwd(BF16))
+
+
+# ---- incremental decode (tests/test_gpu_decode.py) ----
+def _decode(io):
+    def check(r):
+        assert r["o_err"] <= (2e-5 if io == F32 else 2e-2), r
+        if "P_err" in r:
+            assert r["P_err"] <= 1e-5, r
+    return check
+
+
+_add("decode_f32_B2_T100", "decode", dict(B=2, T=100, H=2, d=48, T0=37), _decode(F32))
+_add("decode_bf16_B2_T100", "decode", dict(B=2, T=100, H=2, d=48, T0=37, io=BF16), _decode(BF16))
+_add("decode_f32_B2_T140_d48", "decode", dict(B=2, T=140, H=3, d=48, T0=70, es=0.9), _decode(F32))
+_add("decode_bf16_segments_T800", "decode", dict(B=1, T=800, H=2, d=48, T0=790, io=BF16, es=0.3), _decode(BF16))
+_add("decode_f32_from_one_token_d15", "decode", dict(B=3, T=20, H=4, d=15, T0=1, es=1.1, cap=64), _decode(F32))
+
+
+# ---- residual add + LayerNorm (tests/test_gpu_norm.py) ----
+def _norm(io):
+    def check(r):
+        assert r["h_err"] == 0.0, r
+        assert r["y_err"] <= (1e-5 if io == F32 else 2.0 ** -8 * r["y_max"] + 1e-5), r
+    return check
+
+
+for (io, n, d) in [(F32, 1, 96), (F32, 4097, 1536), (F32, 37, 4096), (F32, 5, 260), (BF16, 4099, 1536),
+                   (BF16, 3, 8192), (BF16, 64, 520), (BF16, 2, 96)]:
+    _add(f"norm_io{io}_n{n}_d{d}", "norm", dict(n=n, d=d, io=io), _norm(io))
+
+
+# ---- the rest ----
+_add("quat_dense_d50", "quat_dense", dict(n=5, d=50), lambda r: r["err"] <= 1e-6)
+_add("quat_dense_d96", "quat_dense", dict(n=3, d=96), lambda r: r["err"] <= 1e-6)
+
+
+def _status(r):
+    assert r["clean"] == 0 and r["clean_inf"] == 0, r
+    assert r["overflow"] == 2 and r["overflow_inf"] > 0, r          # HOLO_WS_OVERFLOW
+
+
+_add("workspace_status", "status", {}, _status)
+_add("layer_bf16_fused_chain", "layer", dict(B=2, T=300, D=192, H=2, check=True, out=F32, es=0.5),
+     lambda r: r["status"] == 0 and r["o_err"] <= 2e-3)
+_add("dma_landing_modes", "dma_modes", dict(B=2, T=300, H=2, d=96, K=128),
+     lambda r: r["attn_identical"] and r["gemm_identical"])
+_add("static_scratch_scan", "static_scan", dict(B=2, T=300, H=2, d=96),
+     lambda r: r["identical_0"] and r["identical_1"])
+
+
+jobs.register("kernels", [(name, params) for _, name, params, _ in CASES], timeout=1500)
+
+
+@pytest.fixture(scope="module")
+def emu_results():
+    rc, out, res = jobs.result("kernels")
+    if rc != 0 or res is None:
+        pytest.fail(f"emulated run failed (status {rc}):\n{out[-12000:]}")
+    got = res["cases"]
+    assert len(got) == len(CASES)
+    return {cid: r for (cid, *_), r in zip(CASES, got)}
+
+
+@pytest.mark.parametrize("cid", [c[0] for c in CASES])
+def test_emulated_kernel(emu_results, cid):
+    check = next(c[3] for c in CASES if c[0] == cid)
+    r = emu_results[cid]
+    assert r["stats"]["launches"] > 0
+    ok = check(r)
+    assert ok is None or ok, r
