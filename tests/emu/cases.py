@@ -675,7 +675,31 @@ def case_decode_bounds(emu: Emu, p):
     return res
 
 
-CASES = {"layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
+def case_planted(emu: Emu, p):
+    """A caller mistake planted in the buffers (never in the kernels), for the
+    tests that the checker fires: "short_output" -- holo_attn_fwd's o one
+    token row too short (the kernel's last stores leave the allocation);
+    "short_kh" -- kh one row too short (the attention's buffer resource over
+    the last (b, h) slice ends past the allocation). The run must abort."""
+    B, T, H, d = 1, 70, 2, 48
+    L = Layer(17, B, T, H, d, BF16, 0.5)
+    s = scan(emu, L, BF16, F16, QUAT_S16)
+    Dp, Tp = padded_head_dim(d), padded_seq(T)
+    kh = s["kh"]
+    rows = B * T
+    if p["kind"] == "short_output":
+        rows -= 1
+    elif p["kind"] == "short_kh":
+        kh = emu.empty((B * H * Tp - 1, Dp), np.float16)
+        kh.a[...] = s["kh"].a.reshape(-1, Dp)[:-1]
+    o = emu.empty((rows, H, d), np.float32)
+    print("planted: launching", flush=True)
+    emu.check(emu.lib.holo_attn_fwd(B, T, H, d, F16, F32, QUAT_S16, 1.0 / math.sqrt(d), s["qh"].ptr, kh.ptr,
+                                    s["vh"].ptr, s["P"].ptr, o.ptr, H * d, d, None, None), "holo_attn_fwd")
+    return {"completed": True}
+
+
+CASES = {"planted": case_planted, "layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
          "decode": case_decode, "norm": case_norm, "quat_dense": case_quat_dense, "status": case_status}
 
 

@@ -217,6 +217,7 @@ def emu_results():
     return {cid: r for (cid, *_), r in zip(CASES, got)}
 
 
+@pytest.mark.emu_jobs("kernels")
 @pytest.mark.parametrize("cid", [c[0] for c in CASES])
 def test_emulated_kernel(emu_results, cid):
     check = next(c[3] for c in CASES if c[0] == cid)
@@ -224,3 +225,19 @@ def test_emulated_kernel(emu_results, cid):
     assert r["stats"]["launches"] > 0
     ok = check(r)
     assert ok is None or ok, r
+
+
+# ---- the checker fires: mistakes planted in the caller's buffers (CPU only) ----
+PLANTED = {"short_output": ("AddressSanitizer", "holo_attn.hip"),
+           "short_kh": ("EMU FAILURE: buffer resource", "past its allocation")}
+for kind in PLANTED:
+    jobs.register(f"planted_{kind}", [("planted", {"kind": kind})], timeout=600)
+
+
+@pytest.mark.parametrize("kind", [pytest.param(k, marks=pytest.mark.emu_jobs(f"planted_{k}")) for k in sorted(PLANTED)])
+def test_checker_stops_planted_overrun(kind):
+    rc, out, res = jobs.result(f"planted_{kind}")
+    assert "planted: launching" in out, out[-4000:]
+    assert rc != 0 and (res is None or "cases" not in res), out[-4000:]
+    for needle in PLANTED[kind]:
+        assert needle in out, (needle, out[-6000:])

@@ -80,6 +80,7 @@ def checked():
     return out_all
 
 
+@pytest.mark.emu_jobs("launch_checker_0", "launch_checker_1", "launch_checker_2")
 @pytest.mark.parametrize("cid", [c[0] for c in CHECKS])
 def test_launch_in_bounds(checked, cid):
     r = checked[cid]
