@@ -45,7 +45,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import kernels
+from . import _lib, kernels
 
 
 class _Verified:
@@ -178,6 +178,16 @@ class PathOrderedGeometricMHA(nn.Module):
             nn.Linear(4 * d_model, self.m_dim * n_heads),
         )
         self.link_mode = "interaction"
+        # Options of this build (not reference attributes; defaults keep the
+        # validated behaviour). fp16_operands: the bf16 inference path stores
+        # the transported q, k, v in fp16 (11-bit significands; a value
+        # beyond +-65504 becomes inf); False keeps bf16 operands, whose range
+        # is fp32's. check_status: read the scan's status word after each
+        # inference forward (one host synchronisation) and raise RuntimeError
+        # if a carry wait timed out (outputs NaN) or an fp16 operand
+        # overflowed; off, the word is never read.
+        self.fp16_operands = True
+        self.check_status = False
         self._wcat_src = None          # _Verified of each weight behind _wcat
         self._wcat = None
         self._mask_ok = None           # _Verified of the last mask found to be tril(L)
@@ -237,14 +247,25 @@ class PathOrderedGeometricMHA(nn.Module):
         return self._wcat
 
     def _fused_projection_ok(self, x: torch.Tensor) -> bool:
-        """holo_qkvg_proj_fwd's conditions: bf16, additive generator, K a
-        multiple of 64, output widths multiples of 4, 16-byte aligned rows."""
-        D = x.shape[-1]
+        """holo_qkvg_proj_fwd's conditions, so that every input it would
+        refuse takes the library GEMMs instead: bf16, additive generator, K a
+        multiple of 64, output widths multiples of 4, 16-byte aligned pointers
+        and row strides, and operands within the kernel's 32-bit buffer
+        offsets (M * row stride and max(3D, H*m) * K bf16 elements below
+        2 GiB)."""
+        if x.dim() != 3:
+            return False
+        B, L, D = (int(n) for n in x.shape)
+        n_gen = self.h * self.m_dim
         ws = (self.qkv.weight, self.gqproj.weight, self.gkproj.weight)
-        return (x.dtype == torch.bfloat16 and self.link_mode == "additive" and D % 64 == 0
-                and (self.h * self.m_dim) % 4 == 0 and self.h * self.m_dim > 0 and x.stride(-1) == 1
-                and x.data_ptr() % 16 == 0 and all(w.dtype == torch.bfloat16 and w.is_contiguous()
-                                                   and w.data_ptr() % 16 == 0 for w in ws))
+        if not (x.dtype == torch.bfloat16 and self.link_mode == "additive" and D % 64 == 0
+                and n_gen % 4 == 0 and n_gen > 0 and x.stride(-1) == 1
+                and all(w.dtype == torch.bfloat16 and w.is_contiguous() and w.data_ptr() % 16 == 0 for w in ws)):
+            return False
+        rs, view = kernels.token_rows_stride(x)
+        if view and (x.data_ptr() % 16 != 0 or rs % 8 != 0):
+            return False
+        return B * L * rs * 2 <= 0x7fffffff and max(3 * D, n_gen) * D * 2 <= 0x7fffffff
 
     def _link_inputs(self, x: torch.Tensor, fused: bool = False):
         """q, k, v views (B,L,H,d) and generator views gq, gk (B,L,H,m).
@@ -328,12 +349,38 @@ class PathOrderedGeometricMHA(nn.Module):
         o = _PathAttention.apply(qkv, g, self.edge_scale, self.scale, additive, d)
         return F.linear(o.reshape(B, L, D), self.out.weight)
 
-    @staticmethod
-    def _op_dtype(x: torch.Tensor) -> torch.dtype:
+    def _op_dtype(self, x: torch.Tensor) -> torch.dtype:
         """Operand type of the transported q, k, v on the causal inference
         path: fp16 for bf16 activations (11-bit significands on the matrix
-        cores at the bf16 rate; the parity bar needs them), fp32 otherwise."""
-        return torch.float16 if x.dtype == torch.bfloat16 else x.dtype
+        cores at the bf16 rate; the parity bar needs them) unless
+        fp16_operands is off, fp32 otherwise."""
+        if x.dtype == torch.bfloat16 and getattr(self, "fp16_operands", True):
+            return torch.float16
+        return x.dtype
+
+    def _status_word(self, device: torch.device) -> Optional[torch.Tensor]:
+        """A one-element int32 device tensor for the scan's status word when
+        check_status is on, else None (the word is never copied or read)."""
+        return torch.zeros(1, dtype=torch.int32, device=device) if getattr(self, "check_status", False) else None
+
+    @staticmethod
+    def _raise_on_status(status: Optional[torch.Tensor]) -> None:
+        """Reads the status word (a host synchronisation) and raises for any
+        bit set: HOLO_WS_TIMEOUT (a chained carry wait ran out of polls; the
+        outputs are NaN) or HOLO_WS_OVERFLOW (a transported value exceeded
+        fp16's range and was stored as inf)."""
+        if status is None:
+            return
+        word = int(status.item())
+        if word == 0:
+            return
+        what = []
+        if word & _lib.HOLO_WS_TIMEOUT:
+            what.append("a chained carry wait timed out (outputs NaN)")
+        if word & _lib.HOLO_WS_OVERFLOW:
+            what.append("a transported q/k/v value exceeded fp16's range (stored as inf; "
+                        "set fp16_operands = False to keep bf16 operands)")
+        raise RuntimeError(f"holonomyawareattention_amd: scan status 0x{word:x}: " + "; ".join(what or ["unknown bits"]))
 
     @staticmethod
     def _p_format(x: torch.Tensor, return_geometry: bool) -> str:
@@ -382,10 +429,11 @@ class PathOrderedGeometricMHA(nn.Module):
             q, k, v, gq, gk = self._link_inputs(x, fused=True)
             if ev is not None:
                 ev[1].record()
+            status = self._status_word(x.device)
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
                                                      want_hol=return_geometry,
                                                      p_format=self._p_format(x, return_geometry),
-                                                     op_dtype=self._op_dtype(x))
+                                                     op_dtype=self._op_dtype(x), status=status)
             if ev is not None:
                 ev[2].record()
             o = kernels.attention(qh, kh, vh_t, P, self.d, self.scale, out_dtype=x.dtype)
@@ -394,6 +442,7 @@ class PathOrderedGeometricMHA(nn.Module):
             y = F.linear(o.view(B, L, D), self.out.weight)
             if ev is not None:
                 ev[4].record()
+        self._raise_on_status(status)
         if not return_geometry:
             return y, None
         d = self.d
@@ -418,10 +467,11 @@ class PathOrderedGeometricMHA(nn.Module):
             q, k, v, gq, gk = self._link_inputs(x, fused=True)
             if ev is not None:
                 ev[1].record()
+            status = self._status_word(x.device)
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, self.edge_scale,
                                                      want_hol=causal or return_geometry,
                                                      p_format=self._p_format(x, return_geometry),
-                                                     mode=self.mode)
+                                                     mode=self.mode, status=status)
             if ev is not None:
                 ev[2].record()
             o = kernels.attention_masked(qh, kh, vh_t, P, hol, self.d, self.scale, mode=self.mode,
@@ -431,6 +481,7 @@ class PathOrderedGeometricMHA(nn.Module):
             y = F.linear(o.view(B, L, D), self.out.weight)
             if ev is not None:
                 ev[4].record()
+        self._raise_on_status(status)
         if not return_geometry:
             return y, None
         C = kernels.quat_to_dense(P, self.d).to(x.dtype)

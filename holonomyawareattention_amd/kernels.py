@@ -76,6 +76,18 @@ def _token_view(t: torch.Tensor, B: int, T: int, H: int, width: int, name: str):
     return rs, hs
 
 
+def token_rows_stride(x: torch.Tensor) -> Tuple[int, bool]:
+    """(row stride in elements, is_view) of x.reshape(B*T, K) for x (B, T, K)
+    with a unit last stride: a view when the (b, t) rows are evenly strided,
+    otherwise torch copies into contiguous rows of stride K."""
+    B, T, K = (int(n) for n in x.shape)
+    if T == 1:
+        return (int(x.stride(0)) if B > 1 else K), True
+    if B == 1 or x.stride(0) == T * x.stride(1):
+        return int(x.stride(1)), True
+    return K, False
+
+
 def padded_head_dim(d: int) -> int:
     return int(_lib.load().holo_padded_head_dim(d))
 

@@ -95,3 +95,67 @@ def test_forward_only_outputs_raise_on_backward():
     with torch.no_grad():
         y = _ForwardOnly.apply("x", 1, y0, x, w)
     assert not y.requires_grad
+
+
+def test_fused_projection_predicate_follows_the_abi_limits():
+    """Inputs the hand-written projection GEMM refuses (holo_qkvg_proj_fwd:
+    row strides not a multiple of 8 elements, operands above its 32-bit buffer
+    offsets) take the library GEMMs instead of raising. The large inputs are
+    never written (torch.empty leaves the pages untouched): only the
+    metadata is read."""
+    D, H = 1536, 16
+    m = PathOrderedGeometricMHA(D, n_heads=H, edge_scale=0.05).to(torch.bfloat16)
+    m.link_mode = "additive"
+    big = lambda B, T: torch.empty(B, T, D, dtype=torch.bfloat16)
+    assert m._fused_projection_ok(torch.empty(2, 8, D, dtype=torch.bfloat16))
+    assert m._fused_projection_ok(big(64, 8192))                      # 1.61e9 bytes of x: inside
+    assert not m._fused_projection_ok(big(128, 8192))                 # 3.2e9 bytes: beyond 2 GiB
+    assert not m._fused_projection_ok(torch.empty(2, 8, D + 4, dtype=torch.bfloat16)[..., :D])  # row stride 1540
+    assert m._fused_projection_ok(torch.empty(2, 8, D + 8, dtype=torch.bfloat16)[..., :D])      # row stride 1544
+    assert m._fused_projection_ok(torch.empty(2, 9, D, dtype=torch.bfloat16)[:, ::2])           # copied rows
+    assert not m._fused_projection_ok(torch.empty(2, 8, D, dtype=torch.bfloat16)[..., 1:D - 63])  # D' % 64 != 0
+    m.link_mode = "interaction"
+    assert not m._fused_projection_ok(torch.empty(2, 8, D, dtype=torch.bfloat16))
+    m32 = PathOrderedGeometricMHA(D, n_heads=H)
+    m32.link_mode = "additive"
+    assert not m32._fused_projection_ok(torch.empty(2, 8, D))
+
+
+def test_status_word_and_operand_options_reach_the_scan(monkeypatch):
+    """check_status passes a status word to the scan and raises on any bit
+    the scan set (carry time-out, fp16 overflow); off, no word is passed.
+    fp16_operands=False keeps bf16 operands on the bf16 path. The kernel
+    wrappers are replaced by stand-ins that record their arguments (no GPU
+    here); only the module's plumbing is under test."""
+    from holonomyawareattention_amd import attention_kernel as AK, _lib
+    B, T, D, H = 1, 5, 24, 2
+    seen = {}
+
+    def fake_scan(q, k, v, gq, gk, es, want_hol=False, p_format="f32", mode="causal", op_dtype=None,
+                  status=None, static_scratch=False):
+        seen["status"], seen["op_dtype"] = status, op_dtype
+        if status is not None:
+            status.fill_(seen.get("word", 0))
+        return None, None, None, None, None
+
+    def fake_attention(qh, kh, vh_t, P, d, scale, out=None, lse=None, out_dtype=None):
+        return torch.zeros(B, T, H, d, dtype=out_dtype or torch.float32)
+
+    monkeypatch.setattr(AK.kernels, "geom_scan", fake_scan)
+    monkeypatch.setattr(AK.kernels, "attention", fake_attention)
+    m = PathOrderedGeometricMHA(D, n_heads=H).eval()
+    m.link_mode = "additive"
+    x = torch.randn(B, T, D)
+    m._forward_kernels(x, False)
+    assert seen["status"] is None and seen["op_dtype"] == torch.float32
+    m.check_status = True
+    m._forward_kernels(x, False)
+    assert seen["status"] is not None and seen["status"].dtype == torch.int32
+    for word, needle in ((_lib.HOLO_WS_OVERFLOW, "fp16"), (_lib.HOLO_WS_TIMEOUT, "timed out")):
+        seen["word"] = word
+        with pytest.raises(RuntimeError, match=needle):
+            m._forward_kernels(x, False)
+    xb = torch.randn(B, T, D).to(torch.bfloat16)
+    assert m._op_dtype(xb) == torch.float16
+    m.fp16_operands = False
+    assert m._op_dtype(xb) == torch.bfloat16 and m._op_dtype(x) == torch.float32
