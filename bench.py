@@ -111,7 +111,9 @@ def pmc_summary(dirs):
     copy = {c: max(v) for (n, c), v in acc.items() if "copyBuffer" in n}
     fs = (1 << 20) / copy["FETCH_SIZE"] if "FETCH_SIZE" in copy else PMC_FETCH_SCALE
     ws = (1 << 20) / copy["WRITE_SIZE"] if "WRITE_SIZE" in copy else PMC_WRITE_SCALE
-    out = {"fetch_scale": fs, "write_scale": ws, "kernels": {}}
+    from holonomyawareattention_amd import build as holo_build
+    # the build the counters were collected with (what traffic_from_profile matches against)
+    out = {"fetch_scale": fs, "write_scale": ws, "sources_sha": holo_build.library_digest(), "kernels": {}}
     for (name, ctr), v in acc.items():
         if ctr not in ("FETCH_SIZE", "WRITE_SIZE"):
             continue
@@ -123,18 +125,30 @@ def pmc_summary(dirs):
 
 
 def traffic_from_profile(config, kernel_prefix):
-    """HBM bytes per launch of the kernels whose name starts with any of
-    `kernel_prefix` (summed), from the committed profiles/pmc_traffic_<config>.json."""
-    path = os.path.join(REPO, "profiles", f"pmc_traffic_{config}.json")
+    """(HBM bytes per launch, source) of the kernels whose name contains any
+    of `kernel_prefix` (summed), from the committed
+    profiles/pmc_traffic_<config>.json. The bytes are not measured in this
+    run: the profile records the sources digest of the build it was measured
+    with, and the bytes are returned only when that digest equals the loaded
+    library's (build.library_digest()); otherwise None, so a profile of an
+    older kernel cannot pass for this one. `source` names the profile and
+    both digests either way."""
+    from holonomyawareattention_amd import build as holo_build
+    rel = f"profiles/pmc_traffic_{config}.json"
+    path = os.path.join(REPO, rel)
+    lib_sha = holo_build.library_digest()
     if not os.path.exists(path):
-        return None
+        return None, {"profile": None, "library_sources_sha": lib_sha}
     data = json.load(open(path))
+    src = {"profile": rel, "measured_sources_sha": data.get("sources_sha"), "library_sources_sha": lib_sha,
+           "same_build": data.get("sources_sha") is not None and data.get("sources_sha") == lib_sha,
+           "measured_in_this_run": False}
     tot, found = 0.0, False
     for name, e in data["kernels"].items():
         if any(p in name for p in kernel_prefix) and "fetch_size_bytes" in e and "write_size_bytes" in e:
             tot += e["fetch_size_bytes"] + e["write_size_bytes"]
             found = True
-    return tot if found else None
+    return (tot if found and src["same_build"] else None), src
 
 
 def orthogonality_report(m, x, config, kernels, torch):
@@ -585,6 +599,13 @@ def main():
     core_peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
     core_tflops = fl_core / (stage_ms[2] * 1e-3) / 1e12
     scan_gbs = scan_bytes / (stage_ms[1] * 1e-3) / 1e9
+    # HBM traffic per launch from the committed counter profile of the same
+    # build (None when the profile's sources digest differs from the library's)
+    no_profile = (None, {"profile": None, "reason": "no traffic profile for this workload"})
+    attn_traffic = no_profile if exact else traffic_from_profile(
+        args.config, ["attn_fwd_h16" if dt == torch.bfloat16 else "attn_fwdIf"])
+    scan_traffic = (traffic_from_profile(args.config, ["scan_reset", "chunk_apply"]) if args.link == "additive"
+                    else no_profile)
 
     out = {
         "metric": METRIC,
@@ -615,13 +636,12 @@ def main():
                                       if dt == torch.bfloat16 else "attn_fwd (holo_attn_fwd)")), "bound": "mfma",
                      "achieved": core_tflops, "peak": core_peak, "unit": "TFLOP/s",
                      "frac": core_tflops / core_peak,
-                     "traffic": None if exact else traffic_from_profile(args.config, ["attn_fwd_h16" if dt == torch.bfloat16 else "attn_fwdIf"]),
+                     "traffic": attn_traffic[0], "traffic_source": attn_traffic[1],
                      "work_per_launch": f"{fl_core:.4e} FLOP = 4*d*(allowed pairs {pairs})*B*H"},
         "roofline_scan": {"kernels": "scan_reset + chunk_apply (holo_geom_scan_fwd)",
                           "bound": "hbm", "achieved": scan_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": scan_gbs / PEAK_HBM_GBS,
-                          "traffic": (traffic_from_profile(args.config, ["scan_reset", "chunk_apply"])
-                                      if args.link == "additive" else None),
+                          "traffic": scan_traffic[0], "traffic_source": scan_traffic[1],
                           "bytes_per_launch": scan_bytes,
                           "bytes_per_token_head": scan_bytes_per_token_head(d, io_bytes, quat_bytes=qbytes,
                                                                             gen_reads=greads),

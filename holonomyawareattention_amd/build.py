@@ -31,6 +31,35 @@ HIPCC_FLAGS = [
 ]
 
 
+STAMP_PATH = LIB_PATH + ".sources"
+
+
+def sources_digest() -> str:
+    """sha256 of what the library is compiled from: the compiler flags, every
+    HIP source and header under csrc/ and the ABI header. build_library()
+    writes it next to the library, so a measurement recorded with one build
+    (e.g. an HBM-traffic profile) can be matched against the library loaded
+    later."""
+    import hashlib
+    h = hashlib.sha256(" ".join(HIPCC_FLAGS[:-2]).encode())
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".hip", ".h")):
+            with open(os.path.join(CSRC, name), "rb") as fh:
+                h.update(name.encode() + b"\0" + fh.read())
+    with open(os.path.join(REPO, "include", "holo_mi355x.h"), "rb") as fh:
+        h.update(fh.read())
+    return h.hexdigest()
+
+
+def library_digest():
+    """The sources digest recorded when the present library was built, or None."""
+    try:
+        with open(STAMP_PATH) as fh:
+            return fh.read().strip() or None
+    except OSError:
+        return None
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -62,6 +91,8 @@ def build_library(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"hipcc link failed:\n{r.stderr[-6000:]}")
     os.replace(tmp, LIB_PATH)
+    with open(STAMP_PATH, "w") as fh:
+        fh.write(sources_digest() + "\n")
     return LIB_PATH
 
 
