@@ -112,8 +112,10 @@ def pmc_summary(dirs):
     fs = (1 << 20) / copy["FETCH_SIZE"] if "FETCH_SIZE" in copy else PMC_FETCH_SCALE
     ws = (1 << 20) / copy["WRITE_SIZE"] if "WRITE_SIZE" in copy else PMC_WRITE_SCALE
     from holonomyawareattention_amd import build as holo_build
-    # the build the counters were collected with (what traffic_from_profile matches against)
+    # the build the counters were collected with: its sources digest, and
+    # each kernel's instruction fingerprint (what traffic_from_profile matches)
     out = {"fetch_scale": fs, "write_scale": ws, "sources_sha": holo_build.library_digest(), "kernels": {}}
+    code = library_code() or {}
     for (name, ctr), v in acc.items():
         if ctr not in ("FETCH_SIZE", "WRITE_SIZE"):
             continue
@@ -121,18 +123,37 @@ def pmc_summary(dirs):
         scale = fs if ctr == "FETCH_SIZE" else ws
         e[ctr.lower() + "_bytes"] = sum(v) / len(v) * 1024 * scale
         e["dispatches"] = len(v)
+        if name in code:
+            e["code_sha256"] = code[name]
     return out
+
+
+_LIB_CODE = {}
+
+
+def library_code():
+    """{kernel name (mangled and as profilers print it): instruction
+    fingerprint} of the loaded library, computed once (None where ROCm's
+    disassembler is absent)."""
+    if "v" not in _LIB_CODE:
+        from holonomyawareattention_amd import _lib, kernel_code
+        try:
+            _LIB_CODE["v"] = kernel_code.by_name(_lib.LIB_PATH) if kernel_code.tools_present() else None
+        except (OSError, RuntimeError):
+            _LIB_CODE["v"] = None
+    return _LIB_CODE["v"]
 
 
 def traffic_from_profile(config, kernel_prefix):
     """(HBM bytes per launch, source) of the kernels whose name contains any
     of `kernel_prefix` (summed), from the committed
     profiles/pmc_traffic_<config>.json. The bytes are not measured in this
-    run: the profile records the sources digest of the build it was measured
-    with, and the bytes are returned only when that digest equals the loaded
-    library's (build.library_digest()); otherwise None, so a profile of an
-    older kernel cannot pass for this one. `source` names the profile and
-    both digests either way."""
+    run: the profile records each kernel's instruction fingerprint in the
+    build it was measured with (code_sha256), and the bytes are returned only
+    when every matched kernel of the loaded library has the same fingerprint
+    (the same machine code); otherwise None, so a profile of another kernel
+    cannot pass for this one. `source` names the profile, the kernels and the
+    outcome either way."""
     from holonomyawareattention_amd import build as holo_build
     rel = f"profiles/pmc_traffic_{config}.json"
     path = os.path.join(REPO, rel)
@@ -140,15 +161,16 @@ def traffic_from_profile(config, kernel_prefix):
     if not os.path.exists(path):
         return None, {"profile": None, "library_sources_sha": lib_sha}
     data = json.load(open(path))
-    src = {"profile": rel, "measured_sources_sha": data.get("sources_sha"), "library_sources_sha": lib_sha,
-           "same_build": data.get("sources_sha") is not None and data.get("sources_sha") == lib_sha,
+    matched = {name: e for name, e in data["kernels"].items()
+               if any(p in name for p in kernel_prefix) and "fetch_size_bytes" in e and "write_size_bytes" in e}
+    code = library_code()
+    same = bool(matched) and code is not None and all(
+        e.get("code_sha256") is not None and code.get(name) == e["code_sha256"] for name, e in matched.items())
+    src = {"profile": rel, "kernels": sorted(matched), "same_code": same,
+           "measured_sources_sha": data.get("sources_sha"), "library_sources_sha": lib_sha,
            "measured_in_this_run": False}
-    tot, found = 0.0, False
-    for name, e in data["kernels"].items():
-        if any(p in name for p in kernel_prefix) and "fetch_size_bytes" in e and "write_size_bytes" in e:
-            tot += e["fetch_size_bytes"] + e["write_size_bytes"]
-            found = True
-    return (tot if found and src["same_build"] else None), src
+    tot = sum(e["fetch_size_bytes"] + e["write_size_bytes"] for e in matched.values())
+    return (tot if same else None), src
 
 
 def orthogonality_report(m, x, config, kernels, torch):
@@ -600,7 +622,7 @@ def main():
     core_tflops = fl_core / (stage_ms[2] * 1e-3) / 1e12
     scan_gbs = scan_bytes / (stage_ms[1] * 1e-3) / 1e9
     # HBM traffic per launch from the committed counter profile of the same
-    # build (None when the profile's sources digest differs from the library's)
+    # machine code (None when a profiled kernel's fingerprint differs)
     no_profile = (None, {"profile": None, "reason": "no traffic profile for this workload"})
     attn_traffic = no_profile if exact else traffic_from_profile(
         args.config, ["attn_fwd_h16" if dt == torch.bfloat16 else "attn_fwdIf"])

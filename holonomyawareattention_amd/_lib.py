@@ -49,6 +49,8 @@ SIGNATURES = [
     ("holo_padded_head_dim", _I, [_I]),
     ("holo_padded_seq_len", _L, [_L]),
     ("holo_qkvg_proj_fwd", _I, [_L, _L, _I, _I, _I, _P, _L, _P, _P, _P, _P, _L, _P, _L, _P]),
+    ("holo_edge_hidden_fwd", _I, [_L, _L, _I, _I, _I, _P, _L, _P, _P, _L, _P, _P, _L, _P, _L, _P]),
+    ("holo_gemm_f32out_fwd", _I, [_L, _I, _I, _P, _L, _P, _P, _L, _P]),
     ("holo_geom_scan_workspace_size", _S, [_I, _L, _I, _I]),
     ("holo_workspace_status", _I, [_P, _S, _P, _P]),
     ("holo_geom_scan_fwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I, _I, _I,

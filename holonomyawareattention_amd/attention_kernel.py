@@ -185,9 +185,15 @@ class PathOrderedGeometricMHA(nn.Module):
         # is fp32's. check_status: read the scan's status word after each
         # inference forward (one host synchronisation) and raise RuntimeError
         # if a carry wait timed out (outputs NaN) or an fp16 operand
-        # overflowed; off, the word is never read.
+        # overflowed; off, the word is never read. fused_interaction: the
+        # bf16 interaction generator's edge MLP on the hand-written GEMM
+        # (holo_edge_hidden_fwd with q/k/v in the same launch, then
+        # holo_gemm_f32out_fwd) instead of torch's GEMMs and GELU; off by
+        # default: these two entry points have been executed on the CPU
+        # only, never on a GPU.
         self.fp16_operands = True
         self.check_status = False
+        self.fused_interaction = False
         self._wcat_src = None          # _Verified of each weight behind _wcat
         self._wcat = None
         self._mask_ok = None           # _Verified of the last mask found to be tril(L)
@@ -267,6 +273,33 @@ class PathOrderedGeometricMHA(nn.Module):
             return False
         return B * L * rs * 2 <= 0x7fffffff and max(3 * D, n_gen) * D * 2 <= 0x7fffffff
 
+    def _fused_interaction_ok(self, x: torch.Tensor) -> bool:
+        """The conditions of holo_edge_hidden_fwd and holo_gemm_f32out_fwd
+        for the interaction generator (fused_interaction on): bf16, the edge
+        MLP as built (Linear with bias, exact GELU, Linear), contiguous
+        16-byte aligned bf16 weights, D a multiple of 64, and every operand
+        within the kernels' 32-bit buffer offsets (weights counted to the end
+        of their last 256-row tile)."""
+        if not (getattr(self, "fused_interaction", False) and self.link_mode == "interaction" and x.dim() == 3):
+            return False
+        B, L, D = (int(n) for n in x.shape)
+        l1, act, l2 = self.edge_mlp[0], self.edge_mlp[1], self.edge_mlp[2]
+        n_gen = self.h * self.m_dim
+        if not (isinstance(act, nn.GELU) and act.approximate == "none" and l1.bias is not None):
+            return False
+        ws = (self.qkv.weight, l1.weight, l1.bias, l2.weight)
+        if not (x.dtype == torch.bfloat16 and D % 64 == 0 and n_gen % 4 == 0 and x.stride(-1) == 1
+                and tuple(l1.weight.shape) == (4 * D, 2 * D) and tuple(l2.weight.shape) == (n_gen, 4 * D)
+                and all(w.dtype == torch.bfloat16 and w.is_contiguous() and w.data_ptr() % 16 == 0 for w in ws)):
+            return False
+        rs, view = kernels.token_rows_stride(x)
+        if view and (x.data_ptr() % 16 != 0 or rs % 8 != 0):
+            return False
+        tile = lambda n: (n + 255) // 256 * 256
+        lim = 0x7fffffff
+        return (B * L * rs * 2 <= lim and 3 * D * D * 2 <= lim and tile(4 * D) * 2 * D * 2 <= lim
+                and B * L * 4 * D * 2 <= lim and tile(n_gen) * 4 * D * 2 <= lim)
+
     def _link_inputs(self, x: torch.Tensor, fused: bool = False):
         """q, k, v views (B,L,H,d) and generator views gq, gk (B,L,H,m).
 
@@ -276,7 +309,9 @@ class PathOrderedGeometricMHA(nn.Module):
         interaction: the edge MLP's last layer). fused=True (bf16, additive)
         runs q/k/v and the generator as one hand-written GEMM
         (holo_qkvg_proj_fwd) that returns gq = g_t = gq(x_t) + gk(x_{t+1})
-        and gk = None: the scan's direct mode, a_t = edge_scale * g_t."""
+        and gk = None: the scan's direct mode, a_t = edge_scale * g_t. With
+        fused=True and fused_interaction on (bf16, interaction), q/k/v and the
+        edge MLP run on holo_edge_hidden_fwd and holo_gemm_f32out_fwd."""
         B, L, D = x.shape
         H, d, m = self.h, self.d, self.m_dim
         if fused and self._fused_projection_ok(x):
@@ -295,6 +330,12 @@ class PathOrderedGeometricMHA(nn.Module):
                 g = torch.mm(x2, wg.t(), out_dtype=torch.float32).view(B, L, 2 * H * m)
             gq = g[..., :H * m].view(B, L, H, m)
             gk = g[..., H * m:].view(B, L, H, m)
+        elif fused and self._fused_interaction_ok(x):
+            qkv, hid = kernels.edge_hidden(x, self.qkv.weight, self.edge_mlp[0].weight, self.edge_mlp[0].bias)
+            qkv = qkv.view(B, L, H, 3 * d)
+            lin2 = self.edge_mlp[2]
+            gq = kernels.edge_out(hid, lin2.weight).view(B, L, H, m)
+            gk = None if lin2.bias is None else lin2.bias.detach().float().view(1, 1, H, m).expand(B, L, H, m)
         else:
             qkv = F.linear(x, self.qkv.weight).view(B, L, H, 3 * d)
             hid = self.edge_mlp[1](self.edge_mlp[0](self._pairs(x))).reshape(B * L, 4 * D)

@@ -86,7 +86,7 @@ extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (6 << 16) | 0; }
+int holo_abi_version(void) { return (6 << 16) | 1; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -126,6 +126,71 @@ int holo_qkvg_proj_fwd(int64_t M, int64_t T, int K, int n_qkv, int n_gen,
   a.g = g; a.ldg = g_rs;
   const hipError_t e = holo::launch_qkvg(a, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "projection GEMM launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+int holo_edge_hidden_fwd(int64_t M, int64_t T, int K, int n_qkv, int n_hid,
+                         const void* x, int64_t x_rs, const void* w_qkv, const void* w1, int64_t w1_rs,
+                         const void* b1, void* qkv, int64_t qkv_rs, void* hid, int64_t hid_rs, void* stream) {
+  g_last_error.clear();
+  if (M <= 0 || T <= 0 || K <= 0 || n_qkv < 0 || n_hid <= 0)
+    return fail(HOLO_ERR_BAD_SHAPE, "M, T, K, n_hid must be positive and n_qkv >= 0 (got %lld, %lld, %d, %d, %d)",
+                (long long)M, (long long)T, K, n_qkv, n_hid);
+  if (M % T != 0) return fail(HOLO_ERR_BAD_SHAPE, "M = %lld is not a whole number of sequences of T = %lld",
+                              (long long)M, (long long)T);
+  if (K % 64 != 0 || n_qkv % 4 != 0 || n_hid % 4 != 0)
+    return fail(HOLO_ERR_UNSUPPORTED, "K = %d must be a multiple of 64 and n_qkv = %d, n_hid = %d multiples of 4",
+                K, n_qkv, n_hid);
+  if (!x || !w1 || !b1 || !hid || (n_qkv > 0 && (!w_qkv || !qkv)))
+    return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(b1) || !aligned16(hid) ||
+      (n_qkv > 0 && (!aligned16(w_qkv) || !aligned16(qkv))))
+    return fail(HOLO_ERR_INVALID_ARG, "x, weights, bias, qkv and hid must be 16-byte aligned");
+  if (x_rs < K || x_rs % 8 != 0 || w1_rs < 2 * (int64_t)K || w1_rs % 8 != 0 || hid_rs < n_hid || hid_rs % 8 != 0 ||
+      (n_qkv > 0 && (qkv_rs < n_qkv || qkv_rs % 8 != 0)))
+    return fail(HOLO_ERR_INVALID_ARG, "row strides (x %lld, w1 %lld, qkv %lld, hid %lld) too small or misaligned",
+                (long long)x_rs, (long long)w1_rs, (long long)qkv_rs, (long long)hid_rs);
+  // 32-bit buffer byte offsets, also for the weight rows of the last
+  // 256-feature tile that lie past n_hid (read as zero, never stored)
+  const int64_t hid_rows = (n_hid + 255) / 256 * 256;
+  if (M * x_rs * 2 > 0x7fffffff || hid_rows * w1_rs * 2 > 0x7fffffff || (int64_t)n_qkv * K * 2 > 0x7fffffff)
+    return fail(HOLO_ERR_UNSUPPORTED, "operands above 2 GiB (M = %lld, K = %d, n_hid = %d)", (long long)M, K, n_hid);
+  holo::EdgeGemmArgs a{};
+  a.M = M; a.T = T; a.K = K; a.n_qkv = n_qkv; a.n_gen = n_hid;
+  a.x = static_cast<const holo::bf16*>(x); a.ldx = x_rs;
+  a.wq = static_cast<const holo::bf16*>(w_qkv);
+  a.wg0 = static_cast<const holo::bf16*>(w1); a.wg1 = a.wg0 + K; a.ldw = w1_rs;
+  a.bias = static_cast<const holo::bf16*>(b1);
+  a.qkv = static_cast<holo::bf16*>(qkv); a.ldq = qkv_rs;
+  a.hid = static_cast<holo::bf16*>(hid); a.ldh = hid_rs;
+  const hipError_t e = holo::launch_edge_hidden(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "edge hidden-layer GEMM launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+int holo_gemm_f32out_fwd(int64_t M, int K, int N, const void* a_in, int64_t a_rs, const void* w,
+                         float* c, int64_t c_rs, void* stream) {
+  g_last_error.clear();
+  if (M <= 0 || K <= 0 || N <= 0)
+    return fail(HOLO_ERR_BAD_SHAPE, "M, K, N must be positive (got %lld, %d, %d)", (long long)M, K, N);
+  if (K % 64 != 0 || N % 4 != 0)
+    return fail(HOLO_ERR_UNSUPPORTED, "K = %d must be a multiple of 64 and N = %d a multiple of 4", K, N);
+  if (!a_in || !w || !c) return fail(HOLO_ERR_INVALID_ARG, "null input or output pointer");
+  if (!aligned16(a_in) || !aligned16(w) || !aligned16(c))
+    return fail(HOLO_ERR_INVALID_ARG, "a, w and c must be 16-byte aligned");
+  if (a_rs < K || a_rs % 8 != 0 || c_rs < N || c_rs % 4 != 0)
+    return fail(HOLO_ERR_INVALID_ARG, "row strides (a %lld, c %lld) too small or misaligned",
+                (long long)a_rs, (long long)c_rs);
+  const int64_t w_rows = ((int64_t)N + 255) / 256 * 256;
+  if (M * a_rs * 2 > 0x7fffffff || w_rows * K * 2 > 0x7fffffff)
+    return fail(HOLO_ERR_UNSUPPORTED, "operands above 2 GiB (M = %lld, K = %d, N = %d)", (long long)M, K, N);
+  holo::EdgeGemmArgs a{};
+  a.M = M; a.T = M; a.K = K; a.n_qkv = 0; a.n_gen = N;
+  a.x = static_cast<const holo::bf16*>(a_in); a.ldx = a_rs;
+  a.wg0 = static_cast<const holo::bf16*>(w); a.ldw = K;
+  a.g = c; a.ldg = c_rs;
+  const hipError_t e = holo::launch_gemm_f32out(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "fp32-output GEMM launch: %s", hipGetErrorString(e));
   return HOLO_OK;
 }
 

@@ -58,7 +58,24 @@ __device__ __forceinline__ void xcd_tile(int L, int tm, int tn, int& mb, int& nb
   mb = x * per + grp * gm + r % gm;
 }
 
+// GELU of the exact erf form (nn.GELU(), approximate='none'), on the
+// pre-activation rounded to bf16 first, as the reference's bf16 Linear
+// hands it to GELU
+__device__ __forceinline__ float gelu_of_bf16(float v) {
+  const float r = (float)(bf16)v;
+  return 0.5f * r * (1.f + erff(r * 0.70710678118654752f));
+}
+
 }  // namespace
+
+// Argument block of each mode (MODE 0: the layer's projections; 1 and 2: the
+// interaction generator's edge MLP, with the extra fields of EdgeGemmArgs).
+// Outside the anonymous namespace: a kernel whose signature names an
+// internal type gets internal linkage, and the compiler then treats its
+// arguments differently (the MODE 0 kernel would no longer compile to the
+// instructions of the projection GEMM as validated).
+template <int MODE> struct GemmArgsOf { typedef EdgeGemmArgs type; };
+template <> struct GemmArgsOf<0> { typedef QkvgArgs type; };
 
 // FT features x TT tokens per workgroup, WF x WT waves (each FT/WF x TT/WT),
 // NST pipeline stages of BK.
@@ -78,9 +95,16 @@ template <int FT, int TT, int WF, int WT, int BK, int NST> struct GemmCfg {
   static_assert(TT * FT * 2 <= kLds && (TT / 2) * FT * 4 <= kLds, "epilogue staging exceeds the ring");
 };
 
-template <int FT, int TT, int WF, int WT, int BK, int NST, int WPE>
+// MODE 0: q/k/v tiles and the additive generator's tiles (two K segments over
+//         the token rows t and t+1, fp32 output): holo_qkvg_proj_fwd.
+// MODE 1: q/k/v tiles and the edge MLP's hidden tiles (two K segments of W1,
+//         weight row stride ldw, bias + exact GELU, bf16 output to hid):
+//         holo_edge_hidden_fwd.
+// MODE 2: one GEMM with an fp32 output, every tile a generator tile with one
+//         K segment (the edge MLP's second layer): holo_gemm_f32out_fwd.
+template <int FT, int TT, int WF, int WT, int BK, int NST, int WPE, int MODE>
 __global__ void __launch_bounds__(64 * WF * WT) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
-gemm_qkvg(QkvgArgs a) {
+gemm_qkvg(typename GemmArgsOf<MODE>::type a) {
   using C = GemmCfg<FT, TT, WF, WT, BK, NST>;
   constexpr int NT = C::kThreadsG;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -97,13 +121,18 @@ gemm_qkvg(QkvgArgs a) {
   else xcd_tile(L - n_gen_tiles, a.tm, a.tnq, mb, nb, a.group_m);
   const int64_t m0 = (int64_t)mb * TT;
   const int n0 = nb * FT;
-  const int nseg = gen ? 2 : 1;
+  const int nseg = gen ? (MODE == 2 ? 1 : 2) : 1;
   const int nks = a.K / BK;                   // K steps per segment
   const int nit = nseg * nks;
 
   // ---- buffer resources: out-of-range rows read as zero ----
   const int n_rows_w = gen ? a.n_gen : a.n_qkv;
-  const int wbytes = (int)((int64_t)n_rows_w * a.K * 2);
+  // MODE 1: a weight of n rows with row stride ldw (>= K) is read as the range
+  // from its first element to the last element of its last row, so the
+  // second K segment (W1 + K) never reaches past W1's end
+  int wbytes;
+  if constexpr (MODE == 1) wbytes = (int)(((int64_t)(n_rows_w - 1) * (gen ? a.ldw : (int64_t)a.K) + a.K) * 2);
+  else wbytes = (int)((int64_t)n_rows_w * a.K * 2);
   const __amdgpu_buffer_rsrc_t wr0 = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<bf16*>(gen ? a.wg0 : a.wq), 0, wbytes, kBufferWord3);
   const __amdgpu_buffer_rsrc_t wr1 = __builtin_amdgcn_make_buffer_rsrc(
@@ -117,7 +146,8 @@ gemm_qkvg(QkvgArgs a) {
   int wo[C::kWLoads], xo0[C::kXLoads], xo1[C::kXLoads];
   static_for<C::kWLoads>([&](auto i) {
     const int p = i * NT + tid, r = p / C::kCPR, c = (p % C::kCPR) ^ gemm_swz<BK>(r);
-    wo[i] = ((n0 + r) * a.K + c * 8) * 2;
+    if constexpr (MODE == 1) wo[i] = (int)(((n0 + r) * (gen ? a.ldw : (int64_t)a.K) + c * 8) * 2);
+    else wo[i] = ((n0 + r) * a.K + c * 8) * 2;
   });
   static_for<C::kXLoads>([&](auto i) {
     const int p = i * NT + tid, r = p / C::kCPR, c = (p % C::kCPR) ^ gemm_swz<BK>(r);
@@ -211,11 +241,13 @@ gemm_qkvg(QkvgArgs a) {
   // reads). The fp32 generator tile goes in two halves of the tokens (128 KB
   // each). ----
   ring_barrier();
-  const int es = gen ? 4 : 2;                         // output bytes per element
+  // generator tiles leave in fp32 (MODE 0, 2) or, MODE 1's hidden tiles, in bf16
+  const bool f32out = gen && MODE != 1;
+  const int es = f32out ? 4 : 2;                      // output bytes per element
   const int rowb = FT * es;                           // staged row bytes (512 or 1024)
   const int cpr = rowb / 16;                          // 16-byte chunks per staged row
   const int xm = (cpr < 32 ? cpr : 32) - 1;           // XOR mask: stays inside the row
-  const int passes = gen ? 2 : 1;
+  const int passes = f32out ? 2 : 1;
   const int tp = TT / passes;                         // tokens per pass
   const int n_out = gen ? a.n_gen : a.n_qkv;
   for (int hp = 0; hp < passes; ++hp) {
@@ -227,12 +259,27 @@ gemm_qkvg(QkvgArgs a) {
           static_for<4>([&](auto q) {
             const int f = wf * (FT / WF) + i * 32 + 8 * q + 4 * g;   // first of 4 features
             const f32x16& c = acc[i][j];
-            if (gen) {
+            // (the condition names `gen`, not f32out: capturing another
+            // variable here changes how the compiler schedules MODE 0)
+            if (MODE != 1 && gen) {
               const int ch = (f >> 2) ^ (r & xm);
               *reinterpret_cast<f32x4*>(smem + r * rowb + ch * 16) =
                   f32x4{c[4 * q], c[4 * q + 1], c[4 * q + 2], c[4 * q + 3]};
             } else {
               const int ch = (f >> 3) ^ (r & xm);
+              if constexpr (MODE == 1) {
+                if (gen) {                            // hidden tile: GELU(sum + bias) in bf16
+                  // buffer load of the 4 biases: features past n_gen read as zero
+                  const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+                      const_cast<bf16*>(a.bias), 0, a.n_gen * 2, kBufferWord3);
+                  const u32x2 raw = __builtin_amdgcn_raw_buffer_load_b64(br, (n0 + f) * 2, 0, 0);
+                  const bf16x4 bv = __builtin_bit_cast(bf16x4, raw);
+                  *reinterpret_cast<bf16x4*>(smem + r * rowb + ch * 16 + (f & 4) * 2) =
+                      bf16x4{(bf16)gelu_of_bf16(c[4 * q] + (float)bv[0]), (bf16)gelu_of_bf16(c[4 * q + 1] + (float)bv[1]),
+                             (bf16)gelu_of_bf16(c[4 * q + 2] + (float)bv[2]), (bf16)gelu_of_bf16(c[4 * q + 3] + (float)bv[3])};
+                  return;
+                }
+              }
               *reinterpret_cast<bf16x4*>(smem + r * rowb + ch * 16 + (f & 4) * 2) =
                   bf16x4{(bf16)c[4 * q], (bf16)c[4 * q + 1], (bf16)c[4 * q + 2], (bf16)c[4 * q + 3]};
             }
@@ -247,7 +294,9 @@ gemm_qkvg(QkvgArgs a) {
       const int n = n0 + c * 16 / es;
       if (m >= a.M || n >= n_out) continue;
       const u32x4 v = *reinterpret_cast<const u32x4*>(smem + r * rowb + (c ^ (r & xm)) * 16);
-      char* dst = gen ? reinterpret_cast<char*>(a.g + m * a.ldg + n) : reinterpret_cast<char*>(a.qkv + m * a.ldq + n);
+      char* dst;
+      if constexpr (MODE == 1) dst = gen ? reinterpret_cast<char*>(a.hid + m * a.ldh + n) : reinterpret_cast<char*>(a.qkv + m * a.ldq + n);
+      else dst = gen ? reinterpret_cast<char*>(a.g + m * a.ldg + n) : reinterpret_cast<char*>(a.qkv + m * a.ldq + n);
       // non-temporal: the outputs (503 MB at config 2) stream to HBM instead
       // of evicting the token rows the other tiles still read (3% measured)
       if (n + 16 / es <= n_out) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
@@ -257,17 +306,17 @@ gemm_qkvg(QkvgArgs a) {
   }
 }
 
-template <int FT, int TT, int WF, int WT, int BK, int NST, int WPE>
-static hipError_t launch_cfg(QkvgArgs a, hipStream_t s) {
+template <int FT, int TT, int WF, int WT, int BK, int NST, int WPE, int MODE>
+static hipError_t launch_cfg(typename GemmArgsOf<MODE>::type a, hipStream_t s) {
   using C = GemmCfg<FT, TT, WF, WT, BK, NST>;
   a.tm = (int)((a.M + TT - 1) / TT);
   a.tnq = (a.n_qkv + FT - 1) / FT;
   a.tng = (a.n_gen + FT - 1) / FT;
-  const hipError_t attr = allow_dynamic_lds<&gemm_qkvg<FT, TT, WF, WT, BK, NST, WPE>>();
+  const hipError_t attr = allow_dynamic_lds<&gemm_qkvg<FT, TT, WF, WT, BK, NST, WPE, MODE>>();
   if (attr != hipSuccess) return attr;
   const unsigned grid = (unsigned)(a.tm * (a.tng + a.tnq));
   if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_qkvg<FT, TT, WF, WT, BK, NST, WPE>), dim3(grid), dim3(C::kThreadsG), C::kLds, s, a);
+  hipLaunchKernelGGL((gemm_qkvg<FT, TT, WF, WT, BK, NST, WPE, MODE>), dim3(grid), dim3(C::kThreadsG), C::kLds, s, a);
   return hipGetLastError();
 }
 
@@ -278,7 +327,22 @@ static hipError_t launch_cfg(QkvgArgs a, hipStream_t s) {
 hipError_t launch_qkvg(const QkvgArgs& a, hipStream_t s) {
   QkvgArgs b = a;
   b.group_m = 8;
-  return launch_cfg<256, 256, 4, 2, 64, 2, 2>(b, s);
+  return launch_cfg<256, 256, 4, 2, 64, 2, 2, 0>(b, s);
+}
+
+// the edge MLP on the same tiling (hidden layer with q/k/v tiles; second layer)
+hipError_t launch_edge_hidden(const EdgeGemmArgs& a, hipStream_t s) {
+  EdgeGemmArgs b = a;
+  b.group_m = 8;
+  return launch_cfg<256, 256, 4, 2, 64, 2, 2, 1>(b, s);
+}
+
+hipError_t launch_gemm_f32out(const EdgeGemmArgs& a, hipStream_t s) {
+  EdgeGemmArgs b = a;
+  b.group_m = 8;
+  b.n_qkv = 0;
+  b.wg1 = b.wg0;                 // one K segment: the second resource is never read
+  return launch_cfg<256, 256, 4, 2, 64, 2, 2, 2>(b, s);
 }
 
 }  // namespace holo

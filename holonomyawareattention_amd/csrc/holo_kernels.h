@@ -127,6 +127,21 @@ struct QkvgArgs {
 };
 hipError_t launch_qkvg(const QkvgArgs& a, hipStream_t s);
 
+// The interaction generator's edge MLP (core/attention_fast_chunked.py:56-60,
+// 73-79) on the same GEMM: the hidden layer GELU([x_t ; x_{t+1}] W1^T + b1)
+// reads W1 (n_gen, 2K) as two K segments, W1[:, :K] on the token rows t and
+// W1[:, K:] on the rows t+1 (wg0 = W1, wg1 = W1 + K, weight row stride
+// ldw = 2K), and writes bf16 `hid`; q/k/v tiles (n_qkv > 0) run in the same
+// launch. The second layer is a plain GEMM with an fp32 output (g = hid W2^T,
+// one K segment; the scan adds its bias per head).
+struct EdgeGemmArgs : QkvgArgs {
+  int64_t ldw;               // row stride of the generator weight (elements)
+  const bf16* bias;          // (n_gen) hidden-layer bias (hidden layer only)
+  bf16* hid; int64_t ldh;    // (M, n_gen) hidden output (hidden layer only)
+};
+hipError_t launch_edge_hidden(const EdgeGemmArgs& a, hipStream_t s);
+hipError_t launch_gemm_f32out(const EdgeGemmArgs& a, hipStream_t s);
+
 template <typename IO, typename OP, typename GT> hipError_t launch_scan(const ScanArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_add_layernorm(const AddNormArgs& a, hipStream_t s);
 hipError_t launch_pack_mask(const uint8_t* mask, int64_t mask_rs, int64_t T, int64_t Tp, uint64_t* bits,

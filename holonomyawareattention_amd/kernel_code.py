@@ -1,13 +1,15 @@
 """Fingerprints of the gfx950 machine code of every kernel in a built
-libholo_mi355x.so (test infrastructure only).
+libholo_mi355x.so.
 
 The library's .hip_fatbin section holds one offload bundle per compiled
 source; each bundle's gfx950 code object is disassembled with ROCm's
 llvm-objdump and every kernel's instruction stream (addresses and encoding
 comments stripped; branch offsets are relative) is hashed. Two builds whose
-fingerprints agree for a kernel run the same instructions for it.
+fingerprints agree for a kernel run the same instructions for it. Used to
+hold a rebuilt library to the kernels a GPU run validated or profiled
+(tests/test_validated_kernels.py, bench.py's traffic figures).
 
-    python -m tests.kernel_code [library.so]      # prints {symbol: sha256}
+    python -m holonomyawareattention_amd.kernel_code [library.so]   # {symbol: sha256}
 """
 from __future__ import annotations
 
@@ -25,12 +27,15 @@ TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
 
 
+CXXFILT = "/usr/bin/c++filt"       # binutils: names kernels as rocprofv3 prints them
+
+
 def tools_present() -> bool:
     return all(os.path.exists(os.path.join(LLVM, t)) for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump"))
 
 
-def _run(*cmd):
-    r = subprocess.run(cmd, capture_output=True, text=True)
+def _run(*cmd, stdin=None):
+    r = subprocess.run(cmd, capture_output=True, text=True, input=stdin)
     if r.returncode != 0:
         raise RuntimeError(f"{cmd[0]} failed: {r.stderr[-2000:]}")
     return r.stdout
@@ -61,6 +66,29 @@ def fingerprints(lib_path: str) -> Dict[str, str]:
     return out
 
 
+def demangle(symbols) -> Dict[str, str]:
+    """{mangled: demangled} with binutils' c++filt, whose names are the ones
+    rocprofv3 prints (both leave symbols with bf16 template arguments
+    mangled). Identity where c++filt is absent."""
+    symbols = list(symbols)
+    if not os.path.exists(CXXFILT):
+        return {n: n for n in symbols}
+    out = _run(CXXFILT, stdin="\n".join(symbols) + "\n").splitlines()
+    if len(out) != len(symbols):
+        raise RuntimeError("c++filt returned a different number of names")
+    return dict(zip(symbols, out))
+
+
+def by_name(lib_path: str) -> Dict[str, str]:
+    """fingerprints() keyed by both the mangled and the demangled symbol, so
+    that a profiler's kernel name (either form) finds its kernel."""
+    fp = fingerprints(lib_path)
+    out = dict(fp)
+    for mangled, plain in demangle(fp).items():
+        out.setdefault(plain, fp[mangled])
+    return out
+
+
 def _per_symbol(text: str) -> Dict[str, str]:
     res: Dict[str, str] = {}
     name, lines = None, []
@@ -85,6 +113,6 @@ def _per_symbol(text: str) -> Dict[str, str]:
 
 
 if __name__ == "__main__":
-    lib = sys.argv[1] if len(sys.argv) > 1 else os.path.join(
-        os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "holonomyawareattention_amd", "libholo_mi355x.so")
+    lib = sys.argv[1] if len(sys.argv) > 1 else os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                             "libholo_mi355x.so")
     print(json.dumps(fingerprints(lib), indent=1, sort_keys=True))

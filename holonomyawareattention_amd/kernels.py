@@ -6,6 +6,8 @@
 ``attention_backward`` -> holo_attn_bwd : gradients of both wrt q, k, v and the generator
 ``quat_to_dense`` -> holo_quat_to_dense
 ``add_layernorm`` -> holo_add_layernorm_fwd : residual add + LayerNorm of the decoder stack
+``edge_hidden`` -> holo_edge_hidden_fwd : q/k/v and the interaction edge MLP's first layer
+``edge_out``  -> holo_gemm_f32out_fwd : the edge MLP's last layer, fp32 output
 
 Each wrapper checks devices, dtypes and strides on the host before the launch
 (the kernels index exactly what these shapes describe), allocates its outputs
@@ -126,6 +128,66 @@ def qkvg_projection(x: torch.Tensor, w_qkv: torch.Tensor, w_gq: Optional[torch.T
                                 _ptr(w_gk), _ptr(qkv), n_qkv, _ptr(g), n_gen, _stream(x.device))
     _lib.check(rc, "holo_qkvg_proj_fwd")
     return qkv, g
+
+
+def _bf16_weight(what: str, w: torch.Tensor, dev: torch.device, shape: Tuple[int, ...]) -> None:
+    if w.dtype != torch.bfloat16 or tuple(w.shape) != shape or not w.is_contiguous() or w.device != dev:
+        raise ValueError(f"{what}: expected a contiguous bfloat16 tensor of shape {shape} on {dev}, "
+                         f"got {w.dtype} {tuple(w.shape)} on {w.device}")
+
+
+def edge_hidden(x: torch.Tensor, w_qkv: Optional[torch.Tensor], w1: torch.Tensor, b1: torch.Tensor
+                ) -> Tuple[Optional[torch.Tensor], torch.Tensor]:
+    """holo_edge_hidden_fwd: x (B, T, K) bf16 -> qkv (B, T, n_qkv) bf16 =
+    x w_qkv^T (None when w_qkv is None) and hid (B, T, n_hid) bf16 =
+    GELU([x_t ; x_{(t+1) mod T}] w1^T + b1), the interaction edge MLP's first
+    layer (core/attention_fast_chunked.py:73-76) without the pair tensor.
+    w1 (n_hid, 2K), b1 (n_hid), w_qkv (n_qkv, K): bf16, contiguous."""
+    dev = _one_gpu("edge_hidden", x, w_qkv, w1, b1)
+    lib = _lib.load()
+    if x.dim() != 3 or x.dtype != torch.bfloat16:
+        raise ValueError("edge_hidden: x must be a (B, T, K) bfloat16 GPU tensor")
+    B, T, K = (int(n) for n in x.shape)
+    x2 = x.reshape(B * T, K)
+    if x2.stride(1) != 1:
+        raise ValueError("edge_hidden: x rows must be contiguous")
+    n_hid = int(w1.shape[0]) if w1.dim() == 2 else -1
+    _bf16_weight("edge_hidden: w1", w1, dev, (n_hid, 2 * K))
+    _bf16_weight("edge_hidden: b1", b1, dev, (n_hid,))
+    n_qkv = 0
+    if w_qkv is not None:
+        n_qkv = int(w_qkv.shape[0]) if w_qkv.dim() == 2 else -1
+        _bf16_weight("edge_hidden: w_qkv", w_qkv, dev, (n_qkv, K))
+    qkv = torch.empty((B, T, n_qkv), dtype=torch.bfloat16, device=dev) if n_qkv else None
+    hid = torch.empty((B, T, n_hid), dtype=torch.bfloat16, device=dev)
+    rc = lib.holo_edge_hidden_fwd(B * T, T, K, n_qkv, n_hid, _ptr(x2), x2.stride(0), _ptr(w_qkv), _ptr(w1),
+                                  2 * K, _ptr(b1), _ptr(qkv), n_qkv, _ptr(hid), n_hid, _stream(dev))
+    _lib.check(rc, "holo_edge_hidden_fwd")
+    return qkv, hid
+
+
+def edge_out(hid: torch.Tensor, w2: torch.Tensor) -> torch.Tensor:
+    """holo_gemm_f32out_fwd: hid (..., K) bf16 -> (..., N) fp32 = hid w2^T for
+    w2 (N, K) bf16 contiguous, the edge MLP's last layer
+    (core/attention_fast_chunked.py:76) with its sums kept in fp32 (no bias:
+    the scan adds it per head)."""
+    dev = _one_gpu("edge_out", hid, w2)
+    lib = _lib.load()
+    if hid.dtype != torch.bfloat16 or hid.dim() < 1:
+        raise ValueError("edge_out: hid must be a bfloat16 GPU tensor")
+    K = int(hid.shape[-1])
+    a2 = hid.reshape(-1, K)
+    if a2.stride(1) != 1:
+        raise ValueError("edge_out: hid rows must be contiguous")
+    N = int(w2.shape[0]) if w2.dim() == 2 else -1
+    _bf16_weight("edge_out: w2", w2, dev, (N, K))
+    c = torch.empty((*hid.shape[:-1], N), dtype=torch.float32, device=dev)
+    M = int(a2.shape[0])
+    if M == 0:
+        return c
+    rc = lib.holo_gemm_f32out_fwd(M, K, N, _ptr(a2), a2.stride(0), _ptr(w2), _ptr(c), N, _stream(dev))
+    _lib.check(rc, "holo_gemm_f32out_fwd")
+    return c
 
 
 def geom_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor,

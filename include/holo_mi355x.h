@@ -145,6 +145,35 @@ HOLO_API int holo_qkvg_proj_fwd(int64_t M, int64_t T, int K, int n_qkv, int n_ge
                        const void* w_qkv, const void* w_gq, const void* w_gk,
                        void* qkv, int64_t qkv_row_stride, float* g, int64_t g_row_stride, void* stream);
 
+/*
+ * holo_edge_hidden_fwd: the interaction generator's first edge-MLP layer on
+ * the same hand-written GEMM, replacing the pair [x_t ; x_{t+1}], its Linear
+ * and the GELU (core/attention_fast_chunked.py:56-59 and :73-76), with the
+ * q/k/v projection (:69) in the same launch:
+ *   qkv[r][n] = sum_c x[r][c] w_qkv[n][c]                                 bf16, n < n_qkv
+ *   hid[r][n] = GELU(bf16(sum_c x[r][c] w1[n][c] + x[r'][c] w1[n][K + c] + b1[n]))   bf16, n < n_hid
+ * for token rows r = b*T + t, r' = b*T + (t+1) mod T (the reference's roll),
+ * GELU the exact erf form (nn.GELU()). w1 is edge_mlp[0].weight, (n_hid, 2K)
+ * with row stride w1_row_stride >= 2K; b1 its bias (n_hid). n_qkv may be 0
+ * (w_qkv and qkv unused). K a multiple of 64, n_qkv and n_hid multiples of
+ * 4, pointers 16-byte aligned, row strides whole 16-byte multiples.
+ */
+HOLO_API int holo_edge_hidden_fwd(int64_t M, int64_t T, int K, int n_qkv, int n_hid,
+                         const void* x, int64_t x_row_stride, const void* w_qkv,
+                         const void* w1, int64_t w1_row_stride, const void* b1,
+                         void* qkv, int64_t qkv_row_stride, void* hid, int64_t hid_row_stride, void* stream);
+
+/*
+ * holo_gemm_f32out_fwd: c (M, N) fp32 = a (M, K) bf16 w^T, w (N, K)
+ * contiguous bf16 (the nn.Linear layout): the edge MLP's last layer
+ * (core/attention_fast_chunked.py:59 and :76) with its sums kept in fp32, the
+ * gq operand of holo_geom_scan_fwd (its bias goes in as gk with row stride
+ * 0). K a multiple of 64, N a multiple of 4, pointers 16-byte aligned, a's
+ * row stride a whole 16-byte multiple, c's a multiple of 4.
+ */
+HOLO_API int holo_gemm_f32out_fwd(int64_t M, int K, int N, const void* a, int64_t a_row_stride,
+                         const void* w, float* c, int64_t c_row_stride, void* stream);
+
 /* Workspace bytes for holo_geom_scan_fwd. */
 HOLO_API size_t holo_geom_scan_workspace_size(int B, int64_t T, int H, int d);
 

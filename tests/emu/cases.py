@@ -203,6 +203,161 @@ def case_gemm(emu: Emu, p):
     return res
 
 
+
+def _gelu(v):
+    from scipy.special import erf
+    return 0.5 * v * (1.0 + erf(v / math.sqrt(2.0)))
+
+
+def _edge_inputs(emu: Emu, rng, M, K, n_qkv, n_hid, N):
+    x = round_bf16(rng.standard_normal((M, K), dtype=np.float32))
+    wq = round_bf16(rng.standard_normal((n_qkv, K), dtype=np.float32) / np.float32(math.sqrt(K)))
+    w1 = round_bf16(rng.standard_normal((n_hid, 2 * K), dtype=np.float32) / np.float32(math.sqrt(2 * K)))
+    b1 = round_bf16(rng.standard_normal(n_hid, dtype=np.float32) * np.float32(0.5))
+    w2 = round_bf16(rng.standard_normal((N, n_hid), dtype=np.float32) / np.float32(math.sqrt(n_hid)))
+    dev = {k: emu.to_dev(v, "bf16") for k, v in dict(x=x, wq=wq, w1=w1, b1=b1, w2=w2).items()}
+    return dict(x=x, wq=wq, w1=w1, b1=b1, w2=w2), dev
+
+
+def case_edge(emu: Emu, p):
+    """holo_edge_hidden_fwd (q/k/v and the edge MLP's first layer on the
+    token rows t and t+1, bias + exact GELU) and holo_gemm_f32out_fwd (the
+    second layer in fp32) against float64 products of the same bf16 inputs,
+    as errors over the rounding bounds of tests/test_gpu_edge_mlp.py (<= 1
+    passes): the hidden value GELU(bf16(pre)) rounded to bf16, the fp32 sums,
+    the second layer on the kernel's own hidden values. Also the hidden layer
+    alone (n_qkv = 0), which must equal the combined launch's bit for bit.
+    With "sample" only some workgroups of each launch run (a bounds check at
+    full size): the entries they wrote are checked, and the second layer then
+    runs on hidden values refilled at random (every row whole)."""
+    B, T, K, H = p["B"], p["T"], p["K"], p["H"]
+    d = K // H
+    m = 3 * (d // 3)
+    M, n_qkv, n_hid, N = B * T, 3 * K, 4 * K, H * m
+    rng = np.random.default_rng(p.get("seed", 62))
+    h, dv = _edge_inputs(emu, rng, M, K, n_qkv, n_hid, N)
+    qkv = emu.empty((M, n_qkv), "bf16")
+    hid = emu.empty((M, n_hid), "bf16")
+    g = emu.empty((M, N), np.float32)
+    samp = p.get("sample")
+    lib = emu.lib
+    written = lambda b: (b.a.view(np.uint16) != 0xA5A5) if b.a.dtype == np.uint16 else (b.a.view(np.uint32) != 0xA5A5A5A5)
+    res = {}
+    if samp:
+        emu.sample(*samp)
+    emu.check(lib.holo_edge_hidden_fwd(M, T, K, n_qkv, n_hid, dv["x"].ptr, K, dv["wq"].ptr, dv["w1"].ptr, 2 * K,
+                                       dv["b1"].ptr, qkv.ptr, n_qkv, hid.ptr, n_hid, None), "holo_edge_hidden_fwd")
+    emu.sample()
+    if not samp:
+        hid1 = emu.empty((M, n_hid), "bf16")
+        emu.check(lib.holo_edge_hidden_fwd(M, T, K, 0, n_hid, dv["x"].ptr, K, None, dv["w1"].ptr, 2 * K,
+                                           dv["b1"].ptr, None, 0, hid1.ptr, n_hid, None), "holo_edge_hidden_fwd")
+        res["hid_only_identical"] = bool(np.array_equal(hid.a, hid1.a))
+        hid1.free()
+    wq_, wh_ = written(qkv), written(hid)
+    res.update(written_qkv=int(wq_.sum()), written_hid=int(wh_.sum()))
+    if not samp:
+        assert wq_.all() and wh_.all(), "unwritten outputs"
+    rq, rh = (np.flatnonzero(w.any(1)) for w in (wq_, wh_))
+    x, W1 = h["x"], h["w1"]
+    xn = np.roll(x.reshape(B, T, K), -1, axis=1).reshape(M, K)
+    # hidden layer
+    xs, xns = x[rh], xn[rh]
+    W1a, W1b, b1 = W1[:, :K], W1[:, K:], h["b1"]
+    pre = xs @ W1a.T + xns @ W1b.T + b1
+    mag = np.abs(xs) @ np.abs(W1a).T + np.abs(xns) @ np.abs(W1b).T + np.abs(b1)
+    ref_h = _gelu(pre)
+    got_h = emu.host(hid, "bf16")[rh]
+    bh = (2.0 ** -8 * np.abs(ref_h) + 1.2 * 2.0 ** -8 * np.abs(pre) + 1.2 * (2 * K + 1) * 2.0 ** -24 * mag
+          + 2.0 ** -22 * (np.abs(pre) + np.abs(ref_h)))
+    sel = wh_[rh]
+    res["hid_err_over_bound"] = float((np.abs(got_h - ref_h) / bh)[sel].max())
+    res["hid_max_err"] = float(np.abs(got_h - ref_h)[sel].max())
+    del pre, mag, ref_h, got_h, bh
+    # q/k/v tiles
+    if len(rq):
+        wqm = h["wq"]
+        xq = x[rq]
+        ref_q, mag_q = xq @ wqm.T, np.abs(xq) @ np.abs(wqm).T
+        got_q = emu.host(qkv, "bf16")[rq]
+        bq = 2.0 ** -8 * np.abs(ref_q) + (1 + 2.0 ** -8) * K * 2.0 ** -24 * mag_q
+        res["qkv_err_over_bound"] = float((np.abs(got_q - ref_q) / bq)[wq_[rq]].max())
+    # second layer on the kernel's own hidden values (sampled: refilled)
+    if samp:
+        hid.a[...] = f32_bits_small(hid.a.shape, rng, "bf16")
+        emu.sample(*samp)
+    emu.check(lib.holo_gemm_f32out_fwd(M, n_hid, N, hid.ptr, n_hid, dv["w2"].ptr, g.ptr, N, None),
+              "holo_gemm_f32out_fwd")
+    emu.sample()
+    wg_ = written(g)
+    res["written_g"] = int(wg_.sum())
+    if not samp:
+        assert wg_.all(), "unwritten outputs"
+    rg = np.flatnonzero(wg_.any(1))
+    hh = emu.host(hid, "bf16")[rg]
+    w2 = h["w2"]
+    ref_g, mag_g = hh @ w2.T, np.abs(hh) @ np.abs(w2).T
+    got_g = g.a[rg].astype(np.float64)
+    res["g_err_over_bound"] = float((np.abs(got_g - ref_g) / (n_hid * 2.0 ** -24 * mag_g))[wg_[rg]].max())
+    res["g_rows_checked"] = int(len(rg))
+    return res
+
+
+def case_layer_interaction(emu: Emu, p):
+    """The bf16 interaction layer as the module runs it with
+    fused_interaction on: holo_edge_hidden_fwd (q/k/v + hidden layer) ->
+    holo_gemm_f32out_fwd (g, fp32) -> holo_geom_scan_fwd in additive mode
+    with gk the second layer's bias at row stride 0 (a per-head constant) ->
+    holo_attn_fwd, fp16 operands, int16 quaternions, fp32 per-head o. Checked
+    against the fp64 oracle fed the kernels' own q, k, v and g + b2 at rows
+    "rows" (default all)."""
+    B, T, D, H = p["B"], p["T"], p["D"], p["H"]
+    d = D // H
+    nb, m = d // 3, 3 * (d // 3)
+    M, Dp, Tp, N = B * T, padded_head_dim(d), padded_seq(T), H * (3 * (d // 3))
+    es = p.get("es", 0.5)
+    rng = np.random.default_rng(p.get("seed", 64))
+    h, dv = _edge_inputs(emu, rng, M, D, 3 * D, 4 * D, N)
+    b2 = rng.standard_normal(N).astype(np.float32) * np.float32(0.5)
+    b2d = emu.to_dev(b2, np.float32)
+    qkv = emu.empty((M, 3 * D), "bf16")
+    hid = emu.empty((M, 4 * D), "bf16")
+    g = emu.empty((M, N), np.float32)
+    lib = emu.lib
+    emu.check(lib.holo_edge_hidden_fwd(M, T, D, 3 * D, 4 * D, dv["x"].ptr, D, dv["wq"].ptr, dv["w1"].ptr, 2 * D,
+                                       dv["b1"].ptr, qkv.ptr, 3 * D, hid.ptr, 4 * D, None), "holo_edge_hidden_fwd")
+    emu.check(lib.holo_gemm_f32out_fwd(M, 4 * D, N, hid.ptr, 4 * D, dv["w2"].ptr, g.ptr, N, None),
+              "holo_gemm_f32out_fwd")
+    qh = emu.empty((B, H, Tp, Dp), np.float16)
+    kh = emu.empty((B, H, Tp, Dp), np.float16)
+    vh = emu.empty((B, H, Tp // 64, Dp, 64), np.float16)
+    P = emu.empty((B, H, T, nb, 4), np.int16)
+    n = int(lib.holo_geom_scan_workspace_size(B, T, H, d))
+    ws = emu.empty((max(n, 1),), np.uint8)
+    st = emu.empty((1,), np.uint32)
+    st.a[0] = 0
+    E = 2
+    emu.check(lib.holo_geom_scan_fwd(B, T, H, d, GEN_ADD, float(es), BF16, F16, F32, QUAT_S16, MODE_CAUSAL,
+                                     g.ptr, N, m, b2d.ptr, 0, m,
+                                     qkv.ptr, 3 * D, 3 * d, qkv.ptr + d * E, 3 * D, 3 * d,
+                                     qkv.ptr + 2 * d * E, 3 * D, 3 * d,
+                                     qh.ptr, kh.ptr, vh.ptr, P.ptr, None, ws.ptr, n, None), "holo_geom_scan_fwd")
+    emu.check(lib.holo_workspace_status(ws.ptr, ws.nbytes, st.ptr, None), "holo_workspace_status")
+    o = emu.empty((B, T, H, d), np.float32)
+    emu.check(lib.holo_attn_fwd(B, T, H, d, F16, F32, QUAT_S16, 1.0 / math.sqrt(d), qh.ptr, kh.ptr, vh.ptr,
+                                P.ptr, o.ptr, H * d, d, None, None), "holo_attn_fwd")
+    rows = np.arange(T) if p.get("rows") is None else np.asarray(p["rows"])
+    qkvh = emu.host(qkv, "bf16").reshape(B, T, H, 3 * d)
+    bh = lambda u: u.transpose(0, 2, 1, 3)
+    qq, kk, vv = (bh(qkvh[..., i * d:(i + 1) * d]) for i in range(3))
+    a = es * bh(g.a.astype(np.float64).reshape(B, T, H, m) + b2.astype(np.float64).reshape(1, 1, H, m))
+    Pr, _ = R.geometry_blocks(a)
+    o_ref = R.apply_blocks(Pr[:, :, rows], R.attention_rows64(*(R.apply_blocks_T(Pr, u) for u in (qq, kk, vv)),
+                                                              1.0 / math.sqrt(d), rows))
+    og = bh(o.a.astype(np.float64))[:, :, rows]
+    return {"status": int(st.a[0]), "o_err": float(np.abs(og - o_ref).max()), "o_max": float(np.abs(o_ref).max())}
+
+
 def case_masked(emu: Emu, p):
     """holo_attn_masked_fwd (exact path: any mask, causal mode's wrap branch
     through the holonomy, inert mode) against oracle.exact_attention64 on the
@@ -699,7 +854,7 @@ def case_planted(emu: Emu, p):
     return {"completed": True}
 
 
-CASES = {"planted": case_planted, "layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
+CASES = {"edge": case_edge, "layer_interaction": case_layer_interaction, "planted": case_planted, "layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
          "decode": case_decode, "norm": case_norm, "quat_dense": case_quat_dense, "status": case_status}
 
 

@@ -123,6 +123,37 @@ def test_projection_argument_validation(lib):
     assert call(xs=120) == _lib.HOLO_ERR_INVALID_ARG                 # x row stride below K
 
 
+def test_edge_gemm_argument_validation(lib):
+    h = lib.holo_edge_hidden_fwd
+
+    def hidden(M=512, T=256, K=128, nq=384, nh=512, xs=128, w1s=256, hs=512, qs=384,
+               x=16, wq=16, w1=16, b1=16, q=16, hid=16):
+        return h(M, T, K, nq, nh, x, xs, wq, w1, w1s, b1, q, qs, hid, hs, None)
+    assert hidden(nh=0) == _lib.HOLO_ERR_BAD_SHAPE
+    assert hidden(T=300) == _lib.HOLO_ERR_BAD_SHAPE
+    assert hidden(K=96, xs=96, w1s=192) == _lib.HOLO_ERR_UNSUPPORTED
+    assert hidden(nh=510, hs=512) == _lib.HOLO_ERR_UNSUPPORTED        # hidden width not a multiple of 4
+    assert hidden(b1=None) == _lib.HOLO_ERR_INVALID_ARG               # the bias is required
+    assert hidden(wq=None) == _lib.HOLO_ERR_INVALID_ARG               # q/k/v weights needed when nq > 0
+    assert hidden(hid=8) == _lib.HOLO_ERR_INVALID_ARG                 # misaligned
+    assert hidden(w1s=248) == _lib.HOLO_ERR_INVALID_ARG               # W1 rows shorter than 2K
+    assert hidden(hs=508) == _lib.HOLO_ERR_INVALID_ARG                # hid row stride not a 16-byte multiple
+    # W1 read to the end of its last 256-row tile: 1024 * 2^20 * 2 bytes is 2 GiB
+    assert hidden(K=1 << 19, xs=1 << 19, w1s=1 << 20, nq=0, nh=1000, hs=1000, M=1, T=1) == _lib.HOLO_ERR_UNSUPPORTED
+    g = lib.holo_gemm_f32out_fwd
+
+    def out(M=512, K=512, N=120, as_=512, cs=120, a=16, w=16, c=16):
+        return g(M, K, N, a, as_, w, c, cs, None)
+    assert out(N=0) == _lib.HOLO_ERR_BAD_SHAPE
+    assert out(K=500, as_=504) == _lib.HOLO_ERR_UNSUPPORTED
+    assert out(N=126, cs=128) == _lib.HOLO_ERR_UNSUPPORTED            # width not a multiple of 4
+    assert out(w=None) == _lib.HOLO_ERR_INVALID_ARG
+    assert out(c=4) == _lib.HOLO_ERR_INVALID_ARG
+    assert out(cs=118) == _lib.HOLO_ERR_INVALID_ARG                   # c row stride below N
+    assert out(as_=508) == _lib.HOLO_ERR_INVALID_ARG                  # a row stride not a 16-byte multiple
+    assert out(M=1 << 22, as_=512) == _lib.HOLO_ERR_UNSUPPORTED       # a above 2 GiB
+
+
 def test_workspace_status_validation(lib):
     st = lib.holo_workspace_status
     assert st(None, 1024, 16, None) == _lib.HOLO_ERR_INVALID_ARG

@@ -16,26 +16,47 @@ def test_multi_gpu_request_exits_with_message():
     assert r.stdout == ""
 
 
-def test_traffic_is_reported_only_for_the_profiled_build(monkeypatch):
-    """roofline.traffic comes from the committed counter profile only when the
-    profile's sources digest equals the loaded library's build stamp; a
-    different or missing stamp gives None, and the line names the profile and
-    both digests either way."""
+def test_traffic_is_reported_only_for_the_profiled_machine_code(monkeypatch):
+    """roofline.traffic comes from the committed counter profile only when
+    every profiled kernel it sums has, in the loaded library, the instruction
+    fingerprint the profile recorded; a changed kernel, a kernel the profile
+    holds no fingerprint for, or no disassembler gives None, and the line
+    names the profile and its kernels either way."""
     sys.path.insert(0, REPO)
     import bench
-    from holonomyawareattention_amd import build
     prof = bench.json.load(open(os.path.join(REPO, "profiles", "pmc_traffic_cfg2.json")))
-    sha = prof["sources_sha"]
-    monkeypatch.setattr(build, "library_digest", lambda: sha)
+    code = {n: e["code_sha256"] for n, e in prof["kernels"].items() if "code_sha256" in e}
+    monkeypatch.setattr(bench, "library_code", lambda: code)
     t, src = bench.traffic_from_profile("cfg2", ["scan_reset", "chunk_apply"])
-    assert t is not None and t > 9e8 and src["same_build"] and src["profile"] == "profiles/pmc_traffic_cfg2.json"
-    assert not src["measured_in_this_run"]
-    monkeypatch.setattr(build, "library_digest", lambda: "0" * 64)
+    assert t is not None and t > 9e8 and src["same_code"] and src["profile"] == "profiles/pmc_traffic_cfg2.json"
+    assert len(src["kernels"]) == 2 and not src["measured_in_this_run"]
+    assert bench.traffic_from_profile("cfg2", ["attn_fwd_h16"])[0] > 1e8
+    changed = dict(code)
+    changed[next(n for n in code if "chunk_apply" in n)] = "0" * 64
+    monkeypatch.setattr(bench, "library_code", lambda: changed)
     t, src = bench.traffic_from_profile("cfg2", ["scan_reset", "chunk_apply"])
-    assert t is None and not src["same_build"] and src["measured_sources_sha"] == sha
-    monkeypatch.setattr(build, "library_digest", lambda: None)
+    assert t is None and not src["same_code"]
+    assert bench.traffic_from_profile("cfg2", ["attn_fwd_h16"])[0] is not None   # unchanged kernel keeps its figure
+    monkeypatch.setattr(bench, "library_code", lambda: None)
     assert bench.traffic_from_profile("cfg2", ["attn_fwd_h16"])[0] is None
-    assert bench.traffic_from_profile("cfg9", ["attn_fwd_h16"]) == (None, {"profile": None, "library_sources_sha": None})
+    monkeypatch.setattr(bench, "library_code", lambda: code)
+    assert bench.traffic_from_profile("cfg2", ["rocclr_copyBuffer"])[0] is None   # no fingerprint recorded
+    assert bench.traffic_from_profile("cfg9", ["attn_fwd_h16"])[0] is None
+
+
+def test_profiled_kernels_match_the_library_as_built():
+    """The library as built now holds the profiled attention and scan kernels
+    with the fingerprints the profile recorded, so the bench line carries
+    their traffic."""
+    sys.path.insert(0, REPO)
+    import bench
+    from holonomyawareattention_amd import _lib, kernel_code
+    if not (os.path.exists(_lib.LIB_PATH) and kernel_code.tools_present()):
+        import pytest
+        pytest.skip("library not built or ROCm's disassembler absent")
+    for prefix in (["attn_fwd_h16"], ["scan_reset", "chunk_apply"]):
+        t, src = bench.traffic_from_profile("cfg2", prefix)
+        assert t is not None and src["same_code"], src
 
 
 def test_library_stamp_is_the_sources_digest():

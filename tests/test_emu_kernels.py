@@ -25,6 +25,10 @@ Tolerances (written per case below):
                  bf16 bar); bf16 o within 2.5e-2 * max(1, max|o| / 4).
   GEMM        -- every element within the rounding bounds of
                  tests/test_gpu_gemm.py (err / bound <= 1).
+  edge MLP    -- hidden values, q/k/v and the fp32 second layer within the
+                 rounding bounds of tests/test_gpu_edge_mlp.py (err / bound
+                 <= 1); the hidden-only launch bit-identical to the combined
+                 one; the chained interaction layer's per-head o within 2e-3.
   exact path  -- fp32 max-abs 2e-5; bf16 max-abs 2.5e-2 and relative
                  Frobenius 1e-2; NaN rows exactly where the oracle's are.
   backward    -- fp32: each gradient within 2e-5 of its largest entry; bf16:
@@ -222,6 +226,39 @@ def emu_results():
 def test_emulated_kernel(emu_results, cid):
     check = next(c[3] for c in CASES if c[0] == cid)
     r = emu_results[cid]
+    assert r["stats"]["launches"] > 0
+    ok = check(r)
+    assert ok is None or ok, r
+
+
+# ---- fused interaction generator (tests/test_gpu_edge_mlp.py; off in the module) ----
+def _edge(r):
+    assert r["hid_only_identical"], r
+    assert r["hid_err_over_bound"] <= 1.0 and r["qkv_err_over_bound"] <= 1.0 and r["g_err_over_bound"] <= 1.0, r
+
+
+EDGE = [(f"edge_B{B}_T{T}_D{D}_H{H}", "edge", dict(B=B, T=T, K=D, H=H), _edge)
+        for (B, T, D, H) in [(3, 100, 128, 4), (5, 1, 128, 4), (2, 257, 192, 4), (1, 300, 384, 4)]]
+EDGE += [(f"layer_interaction_B{B}_T{T}_D{D}_H{H}", "layer_interaction", dict(B=B, T=T, D=D, H=H),
+          lambda r: r["status"] == 0 and r["o_err"] <= 2e-3)
+         for (B, T, D, H) in [(2, 300, 128, 4), (1, 129, 192, 4)]]
+jobs.register("edge_mlp", [(name, params) for _, name, params, _ in EDGE], timeout=900)
+
+
+@pytest.fixture(scope="module")
+def edge_results():
+    rc, out, res = jobs.result("edge_mlp")
+    if rc != 0 or res is None:
+        pytest.fail(f"emulated run failed (status {rc}):\n{out[-12000:]}")
+    assert len(res["cases"]) == len(EDGE)
+    return {cid: r for (cid, *_), r in zip(EDGE, res["cases"])}
+
+
+@pytest.mark.emu_jobs("edge_mlp")
+@pytest.mark.parametrize("cid", [c[0] for c in EDGE])
+def test_emulated_edge_mlp(edge_results, cid):
+    check = next(c[3] for c in EDGE if c[0] == cid)
+    r = edge_results[cid]
     assert r["stats"]["launches"] > 0
     ok = check(r)
     assert ok is None or ok, r

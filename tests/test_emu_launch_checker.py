@@ -19,7 +19,8 @@ Config 5's prefill scan runs at B = 2 (its launches at B = 64 differ only in
 the batch offset, which config 2's B = 16 run and the B = 64 GEMM and
 attention exercise); the exact-path and interaction layouts run at B = 4 of
 config 2, the training step's backward at one batch row and two heads of
-config 2's head size.
+config 2's head size. The fused interaction generator's two GEMMs (off in
+the module) run at config 2's shape with sampled workgroups.
 """
 from __future__ import annotations
 
@@ -42,6 +43,9 @@ CHECKS = [
     ("cfg2_exact_ring_inert", "layer_paths", dict(B=4, **CFG2, path="exact", mask="ring", mode="inert",
                                                   sample_attn=S)),
     ("cfg2_train_backward_bf16", "bwd", dict(B=1, T=1024, H=2, d=96, io=1, es=0.05)),
+    # the fused interaction generator (off in the module): first and last
+    # four and every 997th workgroup of both GEMMs, written entries checked
+    ("cfg2_fused_interaction_gemms", "edge", dict(B=16, T=2048, K=1536, H=16, sample=[4, 4, 997])),
     ("cfg3_layer", "layer", dict(B=2, T=32768, D=1536, H=16, sample_gemm=[1, 1, 0], sample_attn=[1, 1, 0],
                                  fill=False)),
     ("cfg4_layer", "layer", dict(B=8, T=4096, D=1536, H=16, sample_gemm=S, sample_attn=S, fill=False)),
@@ -55,15 +59,18 @@ CHECKS = [
 ]
 
 
-# three child processes of similar length, run at the same time
+# four child processes of similar length, run at the same time
 GROUPS = {"cfg1": 0, "cfg2": 1, "cfg3": 0, "cfg4": 2, "cfg5": 2}
+N_GROUPS = 4
 
 
 def _group(cid):
+    if "interaction_gemms" in cid:
+        return 3
     return 2 if "backward" in cid else GROUPS[cid.split("_")[0]]
 
 
-for g in range(3):
+for g in range(N_GROUPS):
     jobs.register(f"launch_checker_{g}", [(name, params) for cid, name, params in CHECKS if _group(cid) == g],
                   timeout=1800)
 
@@ -71,7 +78,7 @@ for g in range(3):
 @pytest.fixture(scope="module")
 def checked():
     out_all = {}
-    for g in range(3):
+    for g in range(N_GROUPS):
         rc, out, res = jobs.result(f"launch_checker_{g}")
         if rc != 0 or res is None:
             pytest.fail(f"emulated launch check failed (status {rc}):\n{out[-12000:]}")
@@ -80,7 +87,7 @@ def checked():
     return out_all
 
 
-@pytest.mark.emu_jobs("launch_checker_0", "launch_checker_1", "launch_checker_2")
+@pytest.mark.emu_jobs(*[f"launch_checker_{g}" for g in range(N_GROUPS)])
 @pytest.mark.parametrize("cid", [c[0] for c in CHECKS])
 def test_launch_in_bounds(checked, cid):
     r = checked[cid]
@@ -91,5 +98,8 @@ def test_launch_in_bounds(checked, cid):
         assert r["h_err"] == 0.0 and r["y_err"] <= 2.0 ** -8 * r["y_max"] + 1e-5, r
     if cid == "cfg2_train_backward_bf16":
         assert all(v <= 3e-2 for k, v in r.items() if k.endswith("_fro")), r
+    if cid == "cfg2_fused_interaction_gemms":
+        assert r["hid_err_over_bound"] <= 1.0 and r["qkv_err_over_bound"] <= 1.0 and r["g_err_over_bound"] <= 1.0, r
+        assert r["written_hid"] > 0 and r["written_qkv"] > 0 and r["written_g"] > 0, r
     if cid.startswith("cfg5_decode"):
         assert all(v for k, v in r.items() if k.startswith("finite_")), r

@@ -121,6 +121,71 @@ def test_fused_projection_predicate_follows_the_abi_limits():
     assert not m32._fused_projection_ok(torch.empty(2, 8, D))
 
 
+def test_fused_interaction_predicate_follows_the_abi_limits():
+    """fused_interaction is off by default; on, the interaction generator
+    takes holo_edge_hidden_fwd / holo_gemm_f32out_fwd only where their
+    conditions hold (bf16, exact GELU with a first-layer bias, widths
+    multiples of 4, the hidden activations within 2 GiB); every other input
+    keeps the library GEMMs. Metadata only: the large inputs are never
+    written."""
+    D, H = 1536, 16
+    m = PathOrderedGeometricMHA(D, n_heads=H, edge_scale=0.05).to(torch.bfloat16)
+    x = torch.empty(2, 8, D, dtype=torch.bfloat16)
+    assert m.fused_interaction is False and not m._fused_interaction_ok(x)
+    m.fused_interaction = True
+    assert m._fused_interaction_ok(x)
+    big = lambda B, T: torch.empty(B, T, D, dtype=torch.bfloat16)
+    assert m._fused_interaction_ok(big(16, 8192))             # hidden (131072, 6144) bf16: 1.61e9 bytes
+    assert not m._fused_interaction_ok(big(32, 8192))         # 3.2e9 bytes: beyond 2 GiB
+    assert not m._fused_interaction_ok(torch.empty(2, 8, D + 4, dtype=torch.bfloat16)[..., :D])
+    m.link_mode = "additive"
+    assert not m._fused_interaction_ok(x)
+    m.link_mode = "interaction"
+    m.edge_mlp[1] = torch.nn.GELU(approximate="tanh")
+    assert not m._fused_interaction_ok(x)
+    m.edge_mlp[1] = torch.nn.GELU()
+    assert m._fused_interaction_ok(x)
+    assert not m._fused_interaction_ok(x.float())
+    m2 = PathOrderedGeometricMHA(128, n_heads=2).to(torch.bfloat16)      # H*m = 2*63: not a multiple of 4
+    m2.fused_interaction = True
+    assert not m2._fused_interaction_ok(torch.empty(2, 8, 128, dtype=torch.bfloat16))
+    m4 = PathOrderedGeometricMHA(128, n_heads=4).to(torch.bfloat16)      # H*m = 4*30
+    m4.fused_interaction = True
+    assert m4._fused_interaction_ok(torch.empty(2, 8, 128, dtype=torch.bfloat16))
+
+
+def test_fused_interaction_reaches_the_edge_gemms(monkeypatch):
+    """With fused_interaction on, the kernel path's link inputs come from
+    kernels.edge_hidden (q/k/v + hidden layer) and kernels.edge_out (g, fp32),
+    with the second layer's bias handed to the scan as a per-head constant
+    (gk with row stride 0). Stand-ins record the calls (no GPU here)."""
+    from holonomyawareattention_amd import attention_kernel as AK
+    B, T, D, H = 2, 6, 128, 4
+    calls = []
+
+    def fake_hidden(x, w_qkv, w1, b1):
+        calls.append(("hidden", w_qkv is m.qkv.weight, w1 is m.edge_mlp[0].weight, b1 is m.edge_mlp[0].bias))
+        return (torch.arange(B * T * 3 * D, dtype=torch.float32).reshape(B, T, 3 * D).to(torch.bfloat16),
+                torch.zeros(B, T, 4 * D, dtype=torch.bfloat16))
+
+    def fake_out(hid, w2):
+        calls.append(("out", tuple(hid.shape), w2 is m.edge_mlp[2].weight))
+        return torch.ones(B, T, H * m.m_dim)
+
+    monkeypatch.setattr(AK.kernels, "edge_hidden", fake_hidden)
+    monkeypatch.setattr(AK.kernels, "edge_out", fake_out)
+    m = PathOrderedGeometricMHA(D, n_heads=H).to(torch.bfloat16)
+    m.fused_interaction = True
+    x = torch.randn(B, T, D).to(torch.bfloat16)
+    q, k, v, gq, gk = m._link_inputs(x, fused=True)
+    assert calls == [("hidden", True, True, True), ("out", (B, T, 4 * D), True)]
+    d = D // H
+    qkv = torch.arange(B * T * 3 * D, dtype=torch.float32).reshape(B, T, H, 3 * d).to(torch.bfloat16)
+    assert torch.equal(q, qkv[..., :d]) and torch.equal(k, qkv[..., d:2 * d]) and torch.equal(v, qkv[..., 2 * d:])
+    assert gq.dtype == torch.float32 and tuple(gq.shape) == (B, T, H, m.m_dim)
+    assert gk.stride()[:2] == (0, 0) and torch.equal(gk[0, 0], m.edge_mlp[2].bias.float().view(H, m.m_dim))
+
+
 def test_status_word_and_operand_options_reach_the_scan(monkeypatch):
     """check_status passes a status word to the scan and raises on any bit
     the scan set (carry time-out, fp16 overflow); off, no word is passed.

@@ -1,6 +1,7 @@
 """Every kernel of the GPU-validated build compiles to the same gfx950
-instructions in the library as built now (tests/kernel_code.py fingerprints
-against tests/validated_kernels.json), so changes made without a GPU run --
+instructions in the library as built now (the fingerprints of
+holonomyawareattention_amd/kernel_code.py against
+tests/validated_kernels.json), so changes made without a GPU run --
 new kernels, new template modes -- provably leave the validated kernels as
 they were. A kernel may change its symbol (e.g. a new template parameter
 with the old behaviour as one value); it is matched by its instructions.
@@ -12,7 +13,7 @@ import os
 
 import pytest
 
-from tests import kernel_code
+from holonomyawareattention_amd import kernel_code
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB = os.path.join(REPO, "holonomyawareattention_amd", "libholo_mi355x.so")
