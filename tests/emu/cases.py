@@ -405,7 +405,9 @@ def case_bwd(emu: Emu, p):
     """holo_attn_bwd after holo_geom_scan_fwd (fp32 quaternions) and
     holo_attn_fwd (with lse): dq, dk, dv, dgq, dgk against the float64
     backward of the same forward (oracle.attention_backward64 and
-    link_grad_from_cross), each relative to its largest entry."""
+    link_grad_from_cross), each relative to its largest entry. "check":
+    False runs the launches only (bounds at sizes the float64 oracle's
+    T x T arrays would not fit)."""
     B, T, H, d = p["B"], p["T"], p["H"], p["d"]
     io = p.get("io", F32)
     gen_mode = p.get("gen", GEN_ADD)
@@ -436,6 +438,11 @@ def case_bwd(emu: Emu, p):
         dq.ptr, H * d, d, dk.ptr, H * d, d, dv.ptr, H * d, d,
         dgq.ptr, H * m, m, dgk.ptr if dgk else None, H * m if dgk else 0, m if dgk else 0,
         ws.ptr, n, None), "holo_attn_bwd")
+    if not p.get("check", True):
+        st = emu.empty((1,), np.uint32)
+        emu.check(emu.lib.holo_workspace_status(ws.ptr, ws.nbytes, st.ptr, None), "holo_workspace_status")
+        finite = all(bool(np.isfinite(emu.host(b, _dtype(io))).all()) for b in (dq, dk, dv))
+        return {"status": int(st.a[0]), "finite": finite and bool(np.isfinite(dgq.a).all())}
     bh = lambda u: u.transpose(0, 2, 1, 3)
     a = L.a(gen_mode)
     Pr, _ = R.geometry_blocks(a)
