@@ -25,6 +25,14 @@
 // Generator tiles do twice the work of q/k/v tiles and come first in the
 // grid; each XCD takes a contiguous range of M-blocks, in groups of 8 that
 // stay in its L2 while the N-blocks sweep the weights.
+//
+// The same kernel, by a compile-time mode, serves the interaction
+// generator's edge MLP (core/attention_fast_chunked.py:56-60,73-76):
+//   hid = GELU([x_t ; x_{t+1}] W1^T + b1)    the shifted-row K segment is the
+//                                             pair's second half (MODE 1)
+//   g   = hid W2^T                            one K segment, fp32 (MODE 2)
+// MODE 0 is the projection GEMM above and compiles to the same instructions
+// as before the modes existed.
 #include "holo_attn_common.h"
 
 namespace holo {
