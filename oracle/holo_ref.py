@@ -47,6 +47,11 @@ Pinning (every function has at least one independent check in tests/):
   forward_blocks -> forward_chunked (fp64), flat-connection reduction
            (edge_scale = 0 gives torch's causal scaled_dot_product_attention),
            gauge invariance, causal prefix consistency, forward_arc_walk.
+  exact_backward64 / link_grad_closed -> central differences of
+           exact_attention64 through geometry_blocks (causal and inert, no
+           mask, random and ring masks, the closing edge included); under
+           tril the tril backward oracle (pinned to torch autograd);
+           planted mistakes fail (tests/test_oracle_exact_backward.py).
   decoder_forward -> at edge_scale = 0 (P = I) a stack of torch's own pre-LN
            nn.TransformerEncoderLayer (GELU, causal mask, zero attention
            biases, the per-head interleaved qkv rows reordered into torch's
@@ -572,6 +577,120 @@ def link_grad_from_cross(a: np.ndarray, P: np.ndarray, c: np.ndarray) -> np.ndar
     da = np.stack([-dphi[..., 2], dphi[..., 1], -dphi[..., 0]], -1)
     da[..., -1, :, :] = 0.0
     return da
+
+
+def link_grad_closed(a: np.ndarray, P: np.ndarray, c: np.ndarray, c_hol: np.ndarray) -> np.ndarray:
+    """dL/da_t (B,H,T,nb,3) when the loss also depends on the holonomy
+    Hol = G_{T-1} P_{T-1} (the exact path's wrap branch): Hol is P_T of the
+    same recursion, so its cross-product sum c_hol (B,H,nb,3) is a virtual
+    token T's. Every suffix m_t gains c_hol, and the closing edge t = T-1
+    gets P_{T-1} c_hol (in link_grad_from_cross it has no later token)."""
+    cc = np.concatenate([c, c_hol[..., None, :, :]], axis=-3)            # tokens 0..T
+    suf = np.cumsum(cc[..., ::-1, :, :], axis=-3)[..., ::-1, :, :]      # m_t = sum_{s>=t} c_s, t = 0..T
+    m_next = suf[..., 1:, :, :]                                          # m_{t+1}, t = 0..T-1
+    g = np.einsum("...bij,...bj->...bi", P, m_next)
+    return _link_param_grad(a, g)
+
+
+def _link_param_grad(a: np.ndarray, g: np.ndarray) -> np.ndarray:
+    """dL/da from g = P_t m_{t+1} (the SO(3) right Jacobian step of
+    link_grad_from_cross)."""
+    phi = np.stack([-a[..., 2], a[..., 1], -a[..., 0]], -1)
+    th2 = (phi * phi).sum(-1)
+    th = np.sqrt(th2)
+    small = th < 1e-3
+    ths = np.where(small, 1.0, th)
+    al = np.where(small, 0.5 - th2 / 24.0 + th2 * th2 / 720.0, (1.0 - np.cos(ths)) / (ths * ths))
+    be = np.where(small, 1.0 / 6.0 - th2 / 120.0 + th2 * th2 / 5040.0, (ths - np.sin(ths)) / (ths ** 3))
+    pxg = np.cross(phi, g)
+    dphi = g + al[..., None] * pxg + be[..., None] * np.cross(phi, pxg)
+    return np.stack([-dphi[..., 2], dphi[..., 1], -dphi[..., 0]], -1)
+
+
+def exact_backward64(q: np.ndarray, k: np.ndarray, v: np.ndarray, a: np.ndarray, do: np.ndarray, scale: float,
+                     mask: Optional[np.ndarray] = None, mode: str = "causal", plant: str = "") -> Dict[str, np.ndarray]:
+    """Gradients of <do, exact_attention64(q, k, v, P(a), Hol(a), ...)>
+    (the exact path for any mask and mode) with respect to q, k, v (B,H,T,d)
+    and the link parameters a (B,H,T,m) of all T edges, in float64. Rows
+    must allow at least one key.
+
+    Causal mode, in the path frame (u^ = P^T u), with qw = Hol^T q^ and
+    dow = Hol^T do^ the wrap branch's operands (pairs i < j):
+      dS = p (dA - delta), dA_ij = do^_i . v^_j (i >= j) or dow_i . v^_j,
+      delta_i = do^_i . u_i (u_i = P_i^T o_i),
+      dq^ = scale (dS_base k^ + Hol dS_wrap k^),
+      dk^ = scale (dS_base^T q^ + dS_wrap^T qw) = dk_base + dkw,
+      dv^ = p_base^T do^ + p_wrap^T dow = dv_base + dvw.
+    The per-token cross sums c_t = u x do^ + dq^ x q^ + dk^ x k^ + dv^ x v^
+    are those of the tril path; the holonomy adds the virtual token
+    c_hol = sum_j k^_j x dkw_j + v^_j x dvw_j (Hol^T dL/dHol, antisymmetric
+    part), see link_grad_closed.
+    Inert mode is the same algebra with P replaced by Q = P^T (u' = P u): the
+    cross sums c'_t in the primed frame give c_t = -P_t^T c'_t, and there is
+    no holonomy (the closing edge's gradient is zero).
+    `plant` (tests only) introduces one named mistake, so that the tests can
+    show their checks detect it."""
+    T = q.shape[-2]
+    nb = a.shape[-1] // 3
+    P, Hol = geometry_blocks(a)
+    allowed = np.ones((T, T), dtype=bool) if mask is None else np.asarray(mask, dtype=bool)
+    b3 = lambda u: _blocks3(u, nb)
+    mm = lambda x, y: np.einsum("...ij,...jd->...id", x, y)
+    mmT = lambda x, y: np.einsum("...ij,...id->...jd", x, y)
+    dot = lambda x, y: np.einsum("...id,...jd->...ij", x, y)
+    if mode == "causal":
+        qh, kh, vh, doh = (apply_blocks_T(P, u) for u in (q, k, v, do))
+        Hb = Hol[:, :, None]
+        qw, dow = apply_blocks_T(Hb, qh), apply_blocks_T(Hb, doh)
+        if plant == "hol_not_transposed":
+            qw = apply_blocks(Hb, qh)
+        base = np.arange(T)[:, None] >= np.arange(T)[None, :]
+        s = np.where(base, dot(qh, kh), dot(qw, kh)) * scale
+    elif mode == "inert":
+        qh, kh, vh, doh = (apply_blocks(P, u) for u in (q, k, v, do))
+        base = np.ones((T, T), dtype=bool)
+        s = dot(qh, kh) * scale
+    else:
+        raise ValueError(mode)
+    s = np.where(allowed, s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    pb, pw = np.where(base, p, 0.0), np.where(base, 0.0, p)
+    if mode == "causal":
+        dA = np.where(base, dot(doh, vh), dot(dow, vh))
+        u = mm(pb, vh) + apply_blocks(Hb, mm(pw, vh))
+    else:
+        dA = dot(doh, vh)
+        u = mm(p, vh)
+    delta = (doh * u).sum(-1, keepdims=True)
+    dS = p * (dA - delta)
+    dSb, dSw = np.where(base, dS, 0.0), np.where(base, 0.0, dS)
+    dqh = scale * mm(dSb, kh)
+    dkh = scale * mmT(dSb, qh)
+    dvh = mmT(pb, doh)
+    if mode == "causal":
+        dqh = dqh + apply_blocks(Hb, scale * mm(dSw, kh))
+        dkw, dvw = scale * mmT(dSw, qw), mmT(pw, dow)
+        dkh, dvh = dkh + dkw, dvh + dvw
+    c = (np.cross(b3(u), b3(doh)) + np.cross(b3(dqh), b3(qh)) + np.cross(b3(dkh), b3(kh))
+         + np.cross(b3(dvh), b3(vh)))
+    ab = a.reshape(*a.shape[:-1], nb, 3)
+    if mode == "causal":
+        c_hol = (np.cross(b3(kh), b3(dkw)) + np.cross(b3(vh), b3(dvw))).sum(-3)
+        if plant == "no_holonomy_torque":
+            c_hol = 0.0 * c_hol
+        da = link_grad_closed(ab, P, c, c_hol)
+        back = apply_blocks
+    else:
+        c = -np.einsum("...bji,...bj->...bi", P, c)                       # c_t = -P_t^T c'_t
+        if plant == "inert_torque_sign":
+            c = -c
+        elif plant == "inert_torque_frame":
+            c = np.einsum("...bij,...bj->...bi", P, np.einsum("...bij,...bj->...bi", P, c))
+        da = link_grad_from_cross(ab, P, c)
+        back = apply_blocks_T
+    return {"dq": back(P, dqh), "dk": back(P, dkh), "dv": back(P, dvh), "da": da.reshape(a.shape),
+            "dqh": dqh, "dkh": dkh, "dvh": dvh, "delta": delta[..., 0]}
 
 
 def attention_backward64(qh, kh, vh, oh, doh, scale):
