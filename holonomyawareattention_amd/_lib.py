@@ -63,6 +63,8 @@ SIGNATURES = [
     ("holo_attn_masked_workspace_size", _S, [_I, _L, _I, _I, _I, _I, _I]),
     ("holo_attn_masked_fwd", _I, [_I, _L, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _L,
                                   _P, _L, _L, _P, _S, _P]),
+    ("holo_attn_masked_train_fwd", _I, [_I, _L, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _L,
+                                        _P, _L, _L, _P, _P, _S, _P]),
     ("holo_attn_bwd_workspace_size", _S, [_I, _L, _I, _I, _I]),
     ("holo_attn_bwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _F,
                            _P, _L, _L, _P, _L, _L,
@@ -71,6 +73,14 @@ SIGNATURES = [
                            _P, _L, _L, _P, _L, _L, _P, _L, _L,
                            _P, _L, _L, _P, _L, _L,
                            _P, _S, _P]),
+    ("holo_attn_masked_bwd_workspace_size", _S, [_I, _L, _I, _I, _I, _I, _I]),
+    ("holo_attn_masked_bwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I, _F,
+                                  _P, _L, _L, _P, _L, _L,
+                                  _P, _P, _P, _P, _P, _P, _P, _L,
+                                  _P, _L, _L, _P, _L, _L,
+                                  _P, _L, _L, _P, _L, _L, _P, _L, _L,
+                                  _P, _L, _L, _P, _L, _L,
+                                  _P, _S, _P]),
     ("holo_quat_to_dense", _I, [_L, _I, _P, _P, _P]),
     ("holo_add_layernorm_fwd", _I, [_L, _I, _I, _F, _P, _L, _P, _L, _P, _P, _P, _L, _P, _L, _P]),
     ("holo_decode_geom_fwd", _I, [_I, _I, _I, _L, _L, _I, _F, _I, _I,

@@ -32,8 +32,9 @@ backward (holo_attn_bwd; the reference recomputes its forward under autograd,
 kernel/attention_kernel.py:174-187); that backward covers the causal + tril
 path. Other calls under autograd (any other mask, inert mode, return_geometry)
 run their forward as with gradients off and return outputs whose backward
-raises NotImplementedError: the exact path and the geometry output have no
-gfx950 backward.
+raises NotImplementedError, unless exact_backward is on: then any mask and
+inert mode run the exact path's differentiable pair (holo_attn_masked_train_fwd,
+holo_attn_masked_bwd); the geometry output has no gfx950 backward.
 """
 from __future__ import annotations
 
@@ -152,6 +153,41 @@ class _PathAttention(torch.autograd.Function):
         return dqkv, dg, None, None, None, None
 
 
+class _ExactPathAttention(torch.autograd.Function):
+    """o (B,L,H,d) of the exact path (any mask, causal mode with the wrap
+    branch through the holonomy, or inert mode) from the q, k, v views of qkv
+    and the fp32 generator output g (layouts of _PathAttention): geom_scan in
+    the call's mode + holo_attn_masked_train_fwd. Backward:
+    holo_attn_masked_bwd, returning dqkv and dg (the closing edge's share of
+    dg included in causal mode)."""
+
+    @staticmethod
+    def forward(ctx, qkv, g, edge_scale, scale, additive, d, mask, mode):
+        B, L, H, _ = qkv.shape
+        m = 3 * (d // 3)
+        gq, gk = _PathAttention._gviews(g, B, L, H, m, additive)
+        qh, kh, vh_t, P, hol = kernels.geom_scan(qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], gq, gk,
+                                                 edge_scale, want_hol=mode == "causal", p_format="f32", mode=mode)
+        o, lse = kernels.attention_masked_train(qh, kh, vh_t, P, hol, d, scale, mode=mode, mask=mask)
+        ctx.save_for_backward(g, qh, kh, vh_t, P, hol, lse, o, mask)
+        ctx.cfg = (edge_scale, scale, additive, d, H, m, tuple(qkv.shape), mode)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        g, qh, kh, vh_t, P, hol, lse, o, mask = ctx.saved_tensors
+        es, scale, additive, d, H, m, shp, mode = ctx.cfg
+        B, L = shp[0], shp[1]
+        dqkv = torch.empty(shp, dtype=o.dtype, device=o.device)
+        dg = torch.empty_like(g)
+        gq, gk = _PathAttention._gviews(g, B, L, H, m, additive)
+        dgq, dgk = _PathAttention._gviews(dg, B, L, H, m, additive)
+        kernels.attention_masked_backward(gq, gk, es, qh, kh, vh_t, P, hol, lse, o, do.contiguous(), d, scale,
+                                          dqkv[..., :d], dqkv[..., d:2 * d], dqkv[..., 2 * d:], dgq, dgk,
+                                          mode=mode, mask=mask)
+        return dqkv, dg, None, None, None, None, None, None
+
+
 class PathOrderedGeometricMHA(nn.Module):
     def __init__(self, d_model: int, n_heads: int = 4, dropout: float = 0.0,
                  edge_scale: float = 0.1, mode: str = "causal"):
@@ -190,10 +226,15 @@ class PathOrderedGeometricMHA(nn.Module):
         # (holo_edge_hidden_fwd with q/k/v in the same launch, then
         # holo_gemm_f32out_fwd) instead of torch's GEMMs and GELU; off by
         # default: these two entry points have been executed on the CPU
-        # only, never on a GPU.
+        # only, never on a GPU. exact_backward: under autograd, calls off the
+        # causal + tril path (any other mask, inert mode) run a
+        # differentiable exact path (holo_attn_masked_train_fwd and
+        # holo_attn_masked_bwd) instead of a forward whose backward raises;
+        # off by default for the same reason.
         self.fp16_operands = True
         self.check_status = False
         self.fused_interaction = False
+        self.exact_backward = False
         self._wcat_src = None          # _Verified of each weight behind _wcat
         self._wcat = None
         self._mask_ok = None           # _Verified of the last mask found to be tril(L)
@@ -374,9 +415,12 @@ class PathOrderedGeometricMHA(nn.Module):
             g = g + lin2.bias.float()
         return g
 
-    def _forward_autograd(self, x: torch.Tensor) -> torch.Tensor:
+    def _forward_autograd(self, x: torch.Tensor, exact_mask: Optional[Tuple[Optional[torch.Tensor]]] = None
+                          ) -> torch.Tensor:
         """Differentiable forward: torch GEMMs for the projections and the
-        generator, _PathAttention for the core."""
+        generator, _PathAttention for the core (causal + tril) or, with
+        exact_mask = (attn_mask,), _ExactPathAttention (the exact path in the
+        module's mode, attn_mask None = every pair)."""
         B, L, D = x.shape
         H, d, m = self.h, self.d, self.m_dim
         qkv = F.linear(x, self.qkv.weight).view(B, L, H, 3 * d)
@@ -387,7 +431,12 @@ class PathOrderedGeometricMHA(nn.Module):
         else:
             pair = torch.cat([x, torch.roll(x, shifts=-1, dims=1)], dim=-1)
             g = self._edge_params(pair).view(B, L, H * m)
-        o = _PathAttention.apply(qkv, g, self.edge_scale, self.scale, additive, d)
+        if exact_mask is not None:
+            mask = exact_mask[0]
+            mask = None if mask is None else mask.detach().to(torch.bool)
+            o = _ExactPathAttention.apply(qkv, g, self.edge_scale, self.scale, additive, d, mask, self.mode)
+        else:
+            o = _PathAttention.apply(qkv, g, self.edge_scale, self.scale, additive, d)
         return F.linear(o.reshape(B, L, D), self.out.weight)
 
     def _op_dtype(self, x: torch.Tensor) -> torch.dtype:
@@ -445,6 +494,8 @@ class PathOrderedGeometricMHA(nn.Module):
         if track:
             if tril and not return_geometry:
                 return self._forward_autograd(x), None
+            if not tril and not return_geometry and getattr(self, "exact_backward", False):
+                return self._forward_autograd(x, exact_mask=(attn_mask,)), None
             with torch.no_grad():
                 y, geo = self._forward_exact(x, attn_mask, return_geometry) if not tril else \
                     self._forward_kernels(x, True)

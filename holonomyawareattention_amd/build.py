@@ -20,7 +20,7 @@ CSRC = os.path.join(PKG, "csrc")
 LIB_NAME = "libholo_mi355x.so"
 LIB_PATH = os.path.join(PKG, LIB_NAME)
 SOURCES = ["holo_abi.hip", "holo_scan.hip", "holo_attn.hip", "holo_decode.hip", "holo_bwd.hip", "holo_norm.hip",
-           "holo_attn_masked.hip", "holo_gemm.hip"]
+           "holo_attn_masked.hip", "holo_gemm.hip", "holo_bwd_masked.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -86,7 +86,7 @@ extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (6 << 16) | 1; }
+int holo_abi_version(void) { return (6 << 16) | 2; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -354,11 +354,16 @@ size_t holo_attn_masked_workspace_size(int B, int64_t T, int H, int d, int dtype
   return n;
 }
 
-int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, int mode, float scale,
-                         const void* qh, const void* kh, const void* vh_t, const void* P, const float* hol,
-                         const uint8_t* mask, int64_t mask_rs,
-                         void* o, int64_t o_rs, int64_t o_hs,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// holo_attn_masked_fwd's checks and launch; lse non-null selects the
+// training forward (fp32 quaternions, the per-row LSE written)
+int masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, int mode, float scale,
+               const void* qh, const void* kh, const void* vh_t, const void* P, const float* hol,
+               const uint8_t* mask, int64_t mask_rs, void* o, int64_t o_rs, int64_t o_hs, float* lse,
+               void* workspace, size_t workspace_bytes, void* stream) {
   g_last_error.clear();
   int rc = check_common(B, T, H, d);
   if (rc) return rc;
@@ -376,8 +381,9 @@ int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format
   if (mask && mask_rs < T)
     return fail(HOLO_ERR_INVALID_ARG, "mask row stride %lld is below T = %lld", (long long)mask_rs, (long long)T);
   if ((rc = check_layout("o", o_rs, o_hs, H, d))) return rc;
-  if (!aligned16(qh) || !aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)) || (hol && !aligned16(hol)))
-    return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t, P and hol must be 16-byte aligned");
+  if (!aligned16(qh) || !aligned16(kh) || !aligned16(vh_t) || (P && !aligned16(P)) || (hol && !aligned16(hol)) ||
+      (lse && !aligned16(lse)))
+    return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t, P, hol and lse must be 16-byte aligned");
   if (!(scale > 0.f) || !(scale < 1e30f))
     return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
   const size_t need = holo_attn_masked_workspace_size(B, T, H, d, dtype, mode, mask != nullptr);
@@ -385,7 +391,7 @@ int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format
     return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
                 need, workspace ? workspace_bytes : (size_t)0);
 
-  holo::MaskedArgs a;
+  holo::MaskedLseArgs a;
   a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d); a.mode = mode;
   a.T = T; a.Tp = holo::padded_seq(T);
   a.scale_log2 = scale * 1.4426950408889634f;
@@ -394,6 +400,7 @@ int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format
   a.tile_act = nullptr;
   a.o = o; a.o_rs = o_rs; a.o_hs = o_hs;
   a.p_format = p_format;
+  a.lse = lse;
   char* ws = static_cast<char*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
@@ -404,9 +411,39 @@ int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format
                                const_cast<uint8_t*>(a.tile_act), s);
     if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "mask packing launch: %s", hipGetErrorString(e));
   }
-  e = dtype == HOLO_F32 ? holo::launch_attn_masked<float>(a, s) : holo::launch_attn_masked<holo::bf16>(a, s);
+  const holo::MaskedArgs& base = a;
+  if (lse)
+    e = dtype == HOLO_F32 ? holo::launch_attn_masked_lse<float>(a, s) : holo::launch_attn_masked_lse<holo::bf16>(a, s);
+  else
+    e = dtype == HOLO_F32 ? holo::launch_attn_masked<float>(base, s) : holo::launch_attn_masked<holo::bf16>(base, s);
   if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "attention launch: %s", hipGetErrorString(e));
   return HOLO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, int mode, float scale,
+                         const void* qh, const void* kh, const void* vh_t, const void* P, const float* hol,
+                         const uint8_t* mask, int64_t mask_rs,
+                         void* o, int64_t o_rs, int64_t o_hs,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  return masked_fwd(B, T, H, d, dtype, p_format, mode, scale, qh, kh, vh_t, P, hol, mask, mask_rs, o, o_rs, o_hs,
+                    nullptr, workspace, workspace_bytes, stream);
+}
+
+int holo_attn_masked_train_fwd(int B, int64_t T, int H, int d, int dtype, int mode, float scale,
+                               const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
+                               const uint8_t* mask, int64_t mask_rs,
+                               void* o, int64_t o_rs, int64_t o_hs, float* lse,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (!lse) {
+    g_last_error.clear();
+    return fail(HOLO_ERR_INVALID_ARG, "null lse");
+  }
+  return masked_fwd(B, T, H, d, dtype, HOLO_QUAT_F32, mode, scale, qh, kh, vh_t, P, hol, mask, mask_rs, o, o_rs,
+                    o_hs, lse, workspace, workspace_bytes, stream);
 }
 
 size_t holo_attn_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype) {
@@ -414,15 +451,20 @@ size_t holo_attn_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype) {
   return bwd_layout(B, T, H, d, dtype == HOLO_F32 ? 4 : 2, nullptr, nullptr);
 }
 
-int holo_attn_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
-                  float scale,
-                  const void* gq, int64_t gq_rs, int64_t gq_hs, const void* gk, int64_t gk_rs, int64_t gk_hs,
-                  const void* qh, const void* kh, const void* vh_t, const float* P, const float* lse,
-                  const void* o, int64_t o_rs, int64_t o_hs, const void* dout, int64_t do_rs, int64_t do_hs,
-                  void* dq, int64_t dq_rs, int64_t dq_hs, void* dk, int64_t dk_rs, int64_t dk_hs,
-                  void* dv, int64_t dv_rs, int64_t dv_hs,
-                  float* dgq, int64_t dgq_rs, int64_t dgq_hs, float* dgk, int64_t dgk_rs, int64_t dgk_hs,
-                  void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// holo_attn_bwd's argument checks; on success every field of `a` but the
+// workspace's is set
+int bwd_args(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype, int gen_dtype, float scale,
+             const void* gq, int64_t gq_rs, int64_t gq_hs, const void* gk, int64_t gk_rs, int64_t gk_hs,
+             const void* qh, const void* kh, const void* vh_t, const float* P, const float* lse,
+             const void* o, int64_t o_rs, int64_t o_hs, const void* dout, int64_t do_rs, int64_t do_hs,
+             void* dq, int64_t dq_rs, int64_t dq_hs, void* dk, int64_t dk_rs, int64_t dk_hs,
+             void* dv, int64_t dv_rs, int64_t dv_hs,
+             float* dgq, int64_t dgq_rs, int64_t dgq_hs, float* dgk, int64_t dgk_rs, int64_t dgk_hs,
+             holo::BwdArgs& a) {
   g_last_error.clear();
   int rc = check_common(B, T, H, d);
   if (rc) return rc;
@@ -454,13 +496,6 @@ int holo_attn_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale
     return fail(HOLO_ERR_INVALID_ARG, "qh, kh, vh_t, P and lse must be 16-byte aligned");
   if (!(scale > 0.f) || !(scale < 1e30f))
     return fail(HOLO_ERR_INVALID_ARG, "scale must be positive and finite");
-  const size_t es = io_dtype == HOLO_F32 ? 4 : 2;
-  const size_t need = bwd_layout(B, T, H, d, es, nullptr, nullptr);
-  if (!workspace || workspace_bytes < need || !aligned16(workspace))
-    return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
-                need, workspace ? workspace_bytes : (size_t)0);
-
-  holo::BwdArgs a;
   a.B = B; a.H = H; a.d = d; a.nb = nb; a.Dp = holo::padded_head_dim(d); a.gen_mode = gen_mode;
   a.T = T; a.Tp = holo::padded_seq(T); a.nch = a.Tp / holo::kChunk;
   a.scale = scale; a.scale_log2 = scale * 1.4426950408889634f; a.edge_scale = edge_scale;
@@ -470,10 +505,123 @@ int holo_attn_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale
   a.dq = dq; a.dq_rs = dq_rs; a.dq_hs = dq_hs; a.dk = dk; a.dk_rs = dk_rs; a.dk_hs = dk_hs;
   a.dv = dv; a.dv_rs = dv_rs; a.dv_hs = dv_hs;
   a.dgq = dgq; a.dgq_rs = dgq_rs; a.dgq_hs = dgq_hs; a.dgk = dgk; a.dgk_rs = dgk_rs; a.dgk_hs = dgk_hs;
+  return HOLO_OK;
+}
+
+// The exact path's backward workspace: holo_attn_bwd's (bwd_layout), then
+// each region 256-byte aligned: the mask bits and the map of open tiles (with
+// a mask), and in causal mode qw, dow (io dtype; fp32 also qw_t, dow_t),
+// dqw, dkw, dvw (fp32, B*H*Tp*Dp each) and the holonomy's cross sums
+// (fp32, B*H*nb*4).
+size_t masked_bwd_layout(int B, int64_t T, int H, int d, size_t es, int mode, bool has_mask, void* base,
+                         holo::MaskedBwdArgs* a) {
+  size_t off = bwd_layout(B, T, H, d, es, base, a);
+  const int64_t Tp = holo::padded_seq(T);
+  const size_t n = (size_t)B * H * Tp * holo::padded_head_dim(d);
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return base ? static_cast<char*>(base) + at : nullptr;
+  };
+  char* bits = nullptr;
+  char* act = nullptr;
+  if (has_mask) {
+    bits = take((size_t)Tp * (Tp / 64) * 8);
+    act = take((size_t)((T + 127) / 128) * (Tp / 64));
+  }
+  void* r[4] = {nullptr, nullptr, nullptr, nullptr};
+  float* g[4] = {nullptr, nullptr, nullptr, nullptr};
+  if (mode == HOLO_MODE_CAUSAL) {
+    for (int i = 0; i < 4; ++i) r[i] = (es == 2 && i >= 2) ? nullptr : take(n * es);
+    for (int i = 0; i < 3; ++i) g[i] = reinterpret_cast<float*>(take(n * 4));
+    g[3] = reinterpret_cast<float*>(take((size_t)B * H * (d / 3) * 16));
+  }
+  if (a) {
+    a->mask_bits = reinterpret_cast<const uint64_t*>(bits);
+    a->qw = r[0]; a->dow = r[1]; a->qw_t = r[2]; a->dow_t = r[3];
+    a->dqw = g[0]; a->dkw = g[1]; a->dvw = g[2]; a->hol_torque = g[3];
+  }
+  (void)act;
+  return off;
+}
+
+}  // namespace
+
+extern "C" {
+
+int holo_attn_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                  float scale,
+                  const void* gq, int64_t gq_rs, int64_t gq_hs, const void* gk, int64_t gk_rs, int64_t gk_hs,
+                  const void* qh, const void* kh, const void* vh_t, const float* P, const float* lse,
+                  const void* o, int64_t o_rs, int64_t o_hs, const void* dout, int64_t do_rs, int64_t do_hs,
+                  void* dq, int64_t dq_rs, int64_t dq_hs, void* dk, int64_t dk_rs, int64_t dk_hs,
+                  void* dv, int64_t dv_rs, int64_t dv_hs,
+                  float* dgq, int64_t dgq_rs, int64_t dgq_hs, float* dgk, int64_t dgk_rs, int64_t dgk_hs,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  holo::BwdArgs a;
+  int rc = bwd_args(B, T, H, d, gen_mode, edge_scale, io_dtype, gen_dtype, scale, gq, gq_rs, gq_hs, gk, gk_rs,
+                    gk_hs, qh, kh, vh_t, P, lse, o, o_rs, o_hs, dout, do_rs, do_hs, dq, dq_rs, dq_hs, dk, dk_rs,
+                    dk_hs, dv, dv_rs, dv_hs, dgq, dgq_rs, dgq_hs, dgk, dgk_rs, dgk_hs, a);
+  if (rc) return rc;
+  const size_t es = io_dtype == HOLO_F32 ? 4 : 2;
+  const size_t need = bwd_layout(B, T, H, d, es, nullptr, nullptr);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
+                need, workspace ? workspace_bytes : (size_t)0);
   bwd_layout(B, T, H, d, es, workspace, &a);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = io_dtype == HOLO_F32 ? holo::launch_bwd<float, float>(a, s)
                                       : holo::launch_bwd<holo::bf16, float>(a, s);
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "backward launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
+}
+
+size_t holo_attn_masked_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype, int mode, int has_mask) {
+  if (B <= 0 || T <= 0 || H <= 0 || d <= 0 || (dtype != HOLO_F32 && dtype != HOLO_BF16) ||
+      (mode != HOLO_MODE_CAUSAL && mode != HOLO_MODE_INERT))
+    return 0;
+  return masked_bwd_layout(B, T, H, d, dtype == HOLO_F32 ? 4 : 2, mode, has_mask != 0, nullptr, nullptr);
+}
+
+int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                         int mode, float scale,
+                         const void* gq, int64_t gq_rs, int64_t gq_hs, const void* gk, int64_t gk_rs, int64_t gk_hs,
+                         const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
+                         const float* lse, const uint8_t* mask, int64_t mask_rs,
+                         const void* o, int64_t o_rs, int64_t o_hs, const void* dout, int64_t do_rs, int64_t do_hs,
+                         void* dq, int64_t dq_rs, int64_t dq_hs, void* dk, int64_t dk_rs, int64_t dk_hs,
+                         void* dv, int64_t dv_rs, int64_t dv_hs,
+                         float* dgq, int64_t dgq_rs, int64_t dgq_hs, float* dgk, int64_t dgk_rs, int64_t dgk_hs,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  holo::MaskedBwdArgs a;
+  int rc = bwd_args(B, T, H, d, gen_mode, edge_scale, io_dtype, gen_dtype, scale, gq, gq_rs, gq_hs, gk, gk_rs,
+                    gk_hs, qh, kh, vh_t, P, lse, o, o_rs, o_hs, dout, do_rs, do_hs, dq, dq_rs, dq_hs, dk, dk_rs,
+                    dk_hs, dv, dv_rs, dv_hs, dgq, dgq_rs, dgq_hs, dgk, dgk_rs, dgk_hs, a);
+  if (rc) return rc;
+  if (mode != HOLO_MODE_CAUSAL && mode != HOLO_MODE_INERT)
+    return fail(HOLO_ERR_INVALID_ARG, "mode %d is not HOLO_MODE_CAUSAL or HOLO_MODE_INERT", mode);
+  if (mode == HOLO_MODE_CAUSAL && a.nb > 0 && (!hol || !aligned16(hol)))
+    return fail(HOLO_ERR_INVALID_ARG, "causal mode needs the holonomy (hol, 16-byte aligned)");
+  if (mask && mask_rs < T)
+    return fail(HOLO_ERR_INVALID_ARG, "mask row stride %lld is below T = %lld", (long long)mask_rs, (long long)T);
+  const size_t es = io_dtype == HOLO_F32 ? 4 : 2;
+  const size_t need = masked_bwd_layout(B, T, H, d, es, mode, mask != nullptr, nullptr, nullptr);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(HOLO_ERR_WORKSPACE, "workspace of %zu bytes (16-byte aligned) required, got %zu",
+                need, workspace ? workspace_bytes : (size_t)0);
+  masked_bwd_layout(B, T, H, d, es, mode, mask != nullptr, workspace, &a);
+  a.mode = mode == HOLO_MODE_CAUSAL ? 0 : 1;
+  a.hol = hol;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  if (mask) {
+    uint64_t* bits = const_cast<uint64_t*>(a.mask_bits);
+    uint8_t* act = reinterpret_cast<uint8_t*>(bits) + ((size_t)a.Tp * (a.Tp / 64) * 8 + 255) / 256 * 256;
+    e = holo::launch_pack_mask(mask, mask_rs, T, a.Tp, bits, act, s);
+    if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "mask packing launch: %s", hipGetErrorString(e));
+  }
+  e = io_dtype == HOLO_F32 ? holo::launch_masked_bwd<float, float>(a, s)
+                           : holo::launch_masked_bwd<holo::bf16, float>(a, s);
   if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "backward launch: %s", hipGetErrorString(e));
   return HOLO_OK;
 }

@@ -100,9 +100,11 @@ template <typename T, int DP> struct MaskedCfg {
 // in registers and the epilogue merges the two softmax states: with
 // m = max(m_b, m_w) the output is
 //   P_i (2^(m_b-m) O_b + Hol 2^(m_w-m) O_w) / (2^(m_b-m) l_b + 2^(m_w-m) l_w).
-template <typename T, int DP, bool PQ16, bool WRAP>
+// LSE (the training forward) also writes each row's m + log2 l over both
+// branches, for the backward.
+template <typename T, int DP, bool PQ16, bool WRAP, bool LSE = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && PQ16 ? 2 : 1)))
-attn_masked(MaskedArgs a) {
+attn_masked(typename MaskedArgsOf<LSE>::type a) {
   using C = AttnCfg<T, DP>;
   using M = MaskedCfg<T, DP>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -369,6 +371,12 @@ attn_masked(MaskedArgs a) {
     const float inv = 1.f / (ab * l_b + aw * l_w);
     sb = ab * inv;
     sw = aw * inv;
+    if constexpr (LSE) {
+      if (g == 0 && qi < a.T) a.lse[(int64_t)bh * a.Tp + qi] = m_use + __log2f(ab * l_b + aw * l_w);
+    }
+  } else if constexpr (LSE) {
+    const float lt = pair_sum(l_run);       // cross-lane: every lane takes part
+    if (g == 0 && qi < a.T) a.lse[(int64_t)bh * a.Tp + qi] = m_run + __log2f(lt);
   }
 
   // ---- epilogue: normalise (a row that allowed no key has l = 0: 0 * inf =
@@ -430,25 +438,25 @@ attn_masked(MaskedArgs a) {
   });
 }
 
-template <typename T, int DP, bool PQ16, bool WRAP>
-static hipError_t launch_masked_dp(const MaskedArgs& a, hipStream_t s) {
+template <typename T, int DP, bool PQ16, bool WRAP, bool LSE = false>
+static hipError_t launch_masked_dp(const typename MaskedArgsOf<LSE>::type& a, hipStream_t s) {
   using M = MaskedCfg<T, DP>;
   const size_t lds = M::lds(a.Tp / kBN);
   if (lds > (size_t)kMaxDynamicLds) return hipErrorInvalidValue;
-  const hipError_t attr = allow_dynamic_lds<&attn_masked<T, DP, PQ16, WRAP>>();
+  const hipError_t attr = allow_dynamic_lds<&attn_masked<T, DP, PQ16, WRAP, LSE>>();
   if (attr != hipSuccess) return attr;
   const int64_t ntile = (a.T + kBM - 1) / kBM;
-  hipLaunchKernelGGL((attn_masked<T, DP, PQ16, WRAP>), dim3((unsigned)(a.B * a.H * ntile)), dim3(kThreads),
+  hipLaunchKernelGGL((attn_masked<T, DP, PQ16, WRAP, LSE>), dim3((unsigned)(a.B * a.H * ntile)), dim3(kThreads),
                      lds, s, a);
   return hipGetLastError();
 }
 
-template <typename T, bool PQ16, bool WRAP>
-static hipError_t launch_masked_pf(const MaskedArgs& a, hipStream_t s) {
+template <typename T, bool PQ16, bool WRAP, bool LSE = false>
+static hipError_t launch_masked_pf(const typename MaskedArgsOf<LSE>::type& a, hipStream_t s) {
   switch (a.Dp) {
-    case 32: return launch_masked_dp<T, 32, PQ16, WRAP>(a, s);
-    case 64: return launch_masked_dp<T, 64, PQ16, WRAP>(a, s);
-    case 96: return launch_masked_dp<T, 96, PQ16, WRAP>(a, s);
+    case 32: return launch_masked_dp<T, 32, PQ16, WRAP, LSE>(a, s);
+    case 64: return launch_masked_dp<T, 64, PQ16, WRAP, LSE>(a, s);
+    case 96: return launch_masked_dp<T, 96, PQ16, WRAP, LSE>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -460,7 +468,16 @@ hipError_t launch_attn_masked(const MaskedArgs& a, hipStream_t s) {
   return wrap ? launch_masked_pf<T, false, true>(a, s) : launch_masked_pf<T, false, false>(a, s);
 }
 
+// the training forward: fp32 quaternions (the backward's format) and the LSE
+template <typename T>
+hipError_t launch_attn_masked_lse(const MaskedLseArgs& a, hipStream_t s) {
+  if (a.p_format) return hipErrorInvalidValue;
+  return a.mode == 0 ? launch_masked_pf<T, false, true, true>(a, s) : launch_masked_pf<T, false, false, true>(a, s);
+}
+
 template hipError_t launch_attn_masked<float>(const MaskedArgs&, hipStream_t);
 template hipError_t launch_attn_masked<bf16>(const MaskedArgs&, hipStream_t);
+template hipError_t launch_attn_masked_lse<float>(const MaskedLseArgs&, hipStream_t);
+template hipError_t launch_attn_masked_lse<bf16>(const MaskedLseArgs&, hipStream_t);
 
 }  // namespace holo

@@ -76,6 +76,32 @@ struct BwdArgs {
   float* dgk; int64_t dgk_rs, dgk_hs;
 };
 
+// The exact path's forward for training: MaskedArgs and the per-row
+// log2-domain log-sum-exp of the scaled scores (m + log2 l over both
+// branches), which its backward recomputes the probabilities from.
+struct MaskedLseArgs : MaskedArgs {
+  float* lse;                            // (B, H, Tp)
+};
+template <bool LSE> struct MaskedArgsOf { typedef MaskedLseArgs type; };
+template <> struct MaskedArgsOf<false> { typedef MaskedArgs type; };
+
+// Backward of the exact path (any mask; causal mode with the wrap branch
+// through the holonomy, or inert mode). The base fields keep their meaning;
+// in inert mode qh, kh, vh_t, doh hold the primed values u' = P u.
+struct MaskedBwdArgs : BwdArgs {
+  int mode;                              // 0 causal (wrap through hol), 1 inert
+  const float* hol;                      // (B, H, nb, 4) holonomy quaternions (causal)
+  const uint64_t* mask_bits;             // (Tp, Tp/64) as for MaskedArgs; null = every pair
+  void* qw; void* dow;                   // Hol^T qh, Hol^T doh (io dtype, (B, H, Tp, Dp); causal)
+  void* qw_t; void* dow_t;               // their transposed tiles (fp32 only)
+  float* dqw; float* dkw; float* dvw;    // wrap-branch gradients, path frame (fp32, causal)
+  float* hol_torque;                     // (B, H, nb, 4): the holonomy's cross sum (causal)
+};
+// kernel variants of the backward: 0 the causal + tril path, 1 the exact
+// path in causal mode, 2 the exact path in inert mode
+template <int EX> struct BwdArgsOf { typedef MaskedBwdArgs type; };
+template <> struct BwdArgsOf<0> { typedef BwdArgs type; };
+
 struct DecodeGeomArgs {
   int B, H, d, nb, Dp, gen_mode;
   int64_t t, cap;                  // new token's position, cache capacity (multiple of 64)
@@ -147,6 +173,7 @@ template <typename T> hipError_t launch_add_layernorm(const AddNormArgs& a, hipS
 hipError_t launch_pack_mask(const uint8_t* mask, int64_t mask_rs, int64_t T, int64_t Tp, uint64_t* bits,
                             uint8_t* tile_act, hipStream_t s);
 template <typename T> hipError_t launch_attn_masked(const MaskedArgs& a, hipStream_t s);
+template <typename T> hipError_t launch_attn_masked_lse(const MaskedLseArgs& a, hipStream_t s);
 template <typename IO, typename GT> hipError_t launch_decode_geom(const DecodeGeomArgs& a, hipStream_t s);
 template <typename T> hipError_t launch_decode_attn(const DecodeAttnArgs& a, hipStream_t s);
 int64_t decode_splits(int64_t t);
@@ -155,5 +182,6 @@ template <typename OPT, typename OT> hipError_t launch_attn(const AttnArgs& a, h
 hipError_t launch_quat_to_dense(int64_t n, int d, const float* q, float* out, hipStream_t s);
 hipError_t launch_chain_reset(void* state, int64_t n_pairs, unsigned* ticket, hipStream_t s);
 template <typename IO, typename GT> hipError_t launch_bwd(const BwdArgs& a, hipStream_t s);
+template <typename IO, typename GT> hipError_t launch_masked_bwd(const MaskedBwdArgs& a, hipStream_t s);
 
 }  // namespace holo

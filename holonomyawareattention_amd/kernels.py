@@ -4,6 +4,8 @@
 ``attention``  -> holo_attn_fwd      : causal attention, back-rotation
 ``attention_masked`` -> holo_attn_masked_fwd : any mask, causal (wrap through Hol) or inert mode
 ``attention_backward`` -> holo_attn_bwd : gradients of both wrt q, k, v and the generator
+``attention_masked_train`` / ``attention_masked_backward`` -> holo_attn_masked_train_fwd /
+    holo_attn_masked_bwd : the exact path's training forward (with its LSE) and gradient
 ``quat_to_dense`` -> holo_quat_to_dense
 ``add_layernorm`` -> holo_add_layernorm_fwd : residual add + LayerNorm of the decoder stack
 ``edge_hidden`` -> holo_edge_hidden_fwd : q/k/v and the interaction edge MLP's first layer
@@ -334,6 +336,40 @@ def attention(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.T
     return out
 
 
+def _masked_inputs(what: str, qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
+                   hol: Optional[torch.Tensor], d: int, mode: str, mask: Optional[torch.Tensor]):
+    """Checks shared by the exact path's calls; returns (B, H, T, nb, device,
+    dtype, holo_quat_format, uint8 mask or None, mask row stride)."""
+    if mode not in _MODE:
+        raise ValueError(f"{what}: mode must be one of {sorted(_MODE)}")
+    if P.dim() != 5:
+        raise ValueError(f"{what}: P must be (B, H, T, nb, 4)")
+    B, H, T = (int(n) for n in P.shape[:3])
+    nb = d // 3
+    dev, dt = qh.device, qh.dtype
+    if dev.type != "cuda" or dt not in _DT:
+        raise ValueError(f"{what}: qh must be a float32/bfloat16 GPU tensor (got {dt} on {dev})")
+    Dp, Tp = padded_head_dim(d), padded_seq_len(T)
+    for name, t, shape in (("qh", qh, (B, H, Tp, Dp)), ("kh", kh, (B, H, Tp, Dp)),
+                           ("vh_t", vh_t, (B, H, Tp // 64, Dp, 64))):
+        if tuple(t.shape) != shape or not t.is_contiguous() or t.dtype != dt or t.device != dev:
+            raise ValueError(f"{what}: {name} does not match the geom_scan layout")
+    pf = {torch.float32: _lib.HOLO_QUAT_F32, torch.int16: _lib.HOLO_QUAT_SNORM16}.get(P.dtype)
+    if tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous() or pf is None or P.device != dev:
+        raise ValueError(f"{what}: P does not match the geom_scan layout")
+    if mode == "causal" and nb:
+        if hol is None or tuple(hol.shape) != (B, H, nb, 4) or hol.dtype != torch.float32 \
+                or not hol.is_contiguous() or hol.device != dev:
+            raise ValueError(f"{what}: causal mode needs hol, a contiguous fp32 (B, H, nb, 4) tensor")
+    m8, m_rs = None, 0
+    if mask is not None:
+        if tuple(mask.shape) != (T, T) or mask.device != dev:
+            raise ValueError(f"{what}: mask must be ({T}, {T}) on {dev}")
+        m8 = mask.to(torch.bool).contiguous().view(torch.uint8)
+        m_rs = T
+    return B, H, T, nb, dev, dt, pf, m8, m_rs
+
+
 def attention_masked(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
                      hol: Optional[torch.Tensor], d: int, scale: float, mode: str = "causal",
                      mask: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -344,33 +380,7 @@ def attention_masked(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: 
     Returns o as a (B,T,H,d) tensor, or writes `out`."""
     _one_gpu("attention_masked", qh, kh, vh_t, P, hol, mask, out)
     lib = _lib.load()
-    if mode not in _MODE:
-        raise ValueError(f"attention_masked: mode must be one of {sorted(_MODE)}")
-    if P.dim() != 5:
-        raise ValueError("attention_masked: P must be (B, H, T, nb, 4)")
-    B, H, T = (int(n) for n in P.shape[:3])
-    nb = d // 3
-    dev, dt = qh.device, qh.dtype
-    if dev.type != "cuda" or dt not in _DT:
-        raise ValueError(f"attention_masked: qh must be a float32/bfloat16 GPU tensor (got {dt} on {dev})")
-    Dp, Tp = padded_head_dim(d), padded_seq_len(T)
-    for name, t, shape in (("qh", qh, (B, H, Tp, Dp)), ("kh", kh, (B, H, Tp, Dp)),
-                           ("vh_t", vh_t, (B, H, Tp // 64, Dp, 64))):
-        if tuple(t.shape) != shape or not t.is_contiguous() or t.dtype != dt or t.device != dev:
-            raise ValueError(f"attention_masked: {name} does not match the geom_scan layout")
-    pf = {torch.float32: _lib.HOLO_QUAT_F32, torch.int16: _lib.HOLO_QUAT_SNORM16}.get(P.dtype)
-    if tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous() or pf is None or P.device != dev:
-        raise ValueError("attention_masked: P does not match the geom_scan layout")
-    if mode == "causal" and nb:
-        if hol is None or tuple(hol.shape) != (B, H, nb, 4) or hol.dtype != torch.float32 \
-                or not hol.is_contiguous() or hol.device != dev:
-            raise ValueError("attention_masked: causal mode needs hol, a contiguous fp32 (B, H, nb, 4) tensor")
-    m8, m_rs = None, 0
-    if mask is not None:
-        if tuple(mask.shape) != (T, T) or mask.device != dev:
-            raise ValueError(f"attention_masked: mask must be ({T}, {T}) on {dev}")
-        m8 = mask.to(torch.bool).contiguous().view(torch.uint8)
-        m_rs = T
+    B, H, T, nb, dev, dt, pf, m8, m_rs = _masked_inputs("attention_masked", qh, kh, vh_t, P, hol, d, mode, mask)
     if out is None:
         out = torch.empty((B, T, H, d), dtype=dt, device=dev)
     elif out.dtype != dt or out.device != dev:
@@ -386,6 +396,75 @@ def attention_masked(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: 
     return out
 
 
+def attention_masked_train(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
+                           hol: Optional[torch.Tensor], d: int, scale: float, mode: str = "causal",
+                           mask: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """holo_attn_masked_train_fwd: attention_masked for training (P in fp32
+    quaternions) that also returns each row's log2-domain log-sum-exp
+    (B, H, Tp) fp32, which attention_masked_backward reads. Returns (o, lse)."""
+    _one_gpu("attention_masked_train", qh, kh, vh_t, P, hol, mask)
+    lib = _lib.load()
+    B, H, T, nb, dev, dt, pf, m8, m_rs = _masked_inputs("attention_masked_train", qh, kh, vh_t, P, hol, d, mode,
+                                                        mask)
+    if pf != _lib.HOLO_QUAT_F32:
+        raise ValueError("attention_masked_train: P must be the fp32 quaternions")
+    out = torch.empty((B, T, H, d), dtype=dt, device=dev)
+    lse = torch.empty((B, H, padded_seq_len(T)), dtype=torch.float32, device=dev)
+    o_rs, o_hs = _token_view(out, B, T, H, d, "out")
+    ws_bytes = int(lib.holo_attn_masked_workspace_size(B, T, H, d, _DT[dt], _MODE[mode], int(mask is not None)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    rc = lib.holo_attn_masked_train_fwd(B, T, H, d, _DT[dt], _MODE[mode], float(scale),
+                                        _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
+                                        _ptr(hol) if mode == "causal" else None, _ptr(m8), m_rs,
+                                        _ptr(out), o_rs, o_hs, _ptr(lse), _ptr(ws), ws_bytes, _stream(dev))
+    _lib.check(rc, "holo_attn_masked_train_fwd")
+    return out, lse
+
+
+def _bwd_inputs(what: str, gq, gk, qh, kh, vh_t, P, lse, o, dout, d, dq, dk, dv, dgq, dgk):
+    """Checks shared by the backward calls; returns (B, H, T, nb, device,
+    dtype, the five (row, head) strides of o, dout, dq, dk, dv, and those of
+    gq, gk, dgq, dgk)."""
+    B, H, T = (int(n) for n in P.shape[:3])
+    dev, dt = qh.device, qh.dtype
+    nb = d // 3
+    m = 3 * nb
+    Dp, Tp = padded_head_dim(d), padded_seq_len(T)
+    if P.dtype != torch.float32 or tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous():
+        raise ValueError(f"{what}: P must be the fp32 (B, H, T, nb, 4) quaternions")
+    if tuple(qh.shape) != (B, H, Tp, Dp) or not qh.is_contiguous():
+        raise ValueError(f"{what}: qh does not match the geom_scan layout")
+    if tuple(kh.shape) != (B, H, Tp, Dp) or not kh.is_contiguous() or kh.dtype != dt:
+        raise ValueError(f"{what}: kh does not match the geom_scan layout")
+    if tuple(vh_t.shape) != (B, H, Tp // 64, Dp, 64) or not vh_t.is_contiguous() or vh_t.dtype != dt:
+        raise ValueError(f"{what}: vh_t does not match the geom_scan layout")
+    if tuple(lse.shape) != (B, H, Tp) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError(f"{what}: lse must be a contiguous fp32 (B, H, Tp) tensor")
+    for t in (kh, vh_t, P, lse, o, dout, dq, dk, dv, gq, dgq) + tuple(x for x in (gk, dgk) if x is not None):
+        if t.device != dev:
+            raise ValueError(f"{what}: all tensors must be on one device")
+    for name, t in (("o", o), ("dout", dout), ("dq", dq), ("dk", dk), ("dv", dv)):
+        if t.dtype != dt:
+            raise ValueError(f"{what}: {name} must be {dt}")
+    for name, t in (("gq", gq), ("gk", gk), ("dgq", dgq), ("dgk", dgk)):
+        if t is not None and t.dtype != torch.float32:
+            raise ValueError(f"{what}: {name} must be float32")
+    if (gk is None) != (dgk is None):
+        raise ValueError(f"{what}: gk and dgk go together (additive generator)")
+    views = [_token_view(t, B, T, H, d, n) for n, t in (("o", o), ("dout", dout), ("dq", dq), ("dk", dk), ("dv", dv))]
+    gv = [(0, 0) if t is None else _token_view(t, B, T, H, m, n)
+          for n, t in (("gq", gq), ("gk", gk), ("dgq", dgq), ("dgk", dgk))]
+    return B, H, T, nb, dev, dt, views, gv
+
+
+def _workspace(what: str, workspace: Optional[torch.Tensor], need: int, dev: torch.device) -> torch.Tensor:
+    if workspace is not None and not workspace.is_contiguous():
+        raise ValueError(f"{what}: workspace must be contiguous")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    return workspace
+
+
 def attention_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge_scale: float,
                        qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
                        lse: torch.Tensor, o: torch.Tensor, dout: torch.Tensor, d: int, scale: float,
@@ -398,40 +477,10 @@ def attention_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge_scale:
     quaternions of the same forward, lse the normalisers its attention wrote."""
     _one_gpu("attention_backward", qh, kh, vh_t, P, lse, o, dout, dq, dk, dv, gq, gk, dgq, dgk, workspace)
     lib = _lib.load()
-    B, H, T = (int(n) for n in P.shape[:3])
-    dev, dt = qh.device, qh.dtype
-    nb = d // 3
-    m = 3 * nb
-    Dp, Tp = padded_head_dim(d), padded_seq_len(T)
-    if P.dtype != torch.float32 or tuple(P.shape) != (B, H, T, nb, 4) or not P.is_contiguous():
-        raise ValueError("attention_backward: P must be the fp32 (B, H, T, nb, 4) quaternions")
-    if tuple(qh.shape) != (B, H, Tp, Dp) or not qh.is_contiguous():
-        raise ValueError("attention_backward: qh does not match the geom_scan layout")
-    if tuple(kh.shape) != (B, H, Tp, Dp) or not kh.is_contiguous() or kh.dtype != dt:
-        raise ValueError("attention_backward: kh does not match the geom_scan layout")
-    if tuple(vh_t.shape) != (B, H, Tp // 64, Dp, 64) or not vh_t.is_contiguous() or vh_t.dtype != dt:
-        raise ValueError("attention_backward: vh_t does not match the geom_scan layout")
-    if tuple(lse.shape) != (B, H, Tp) or lse.dtype != torch.float32 or not lse.is_contiguous():
-        raise ValueError("attention_backward: lse must be a contiguous fp32 (B, H, Tp) tensor")
-    for t in (kh, vh_t, P, lse, o, dout, dq, dk, dv, gq, dgq) + tuple(x for x in (gk, dgk) if x is not None):
-        if t.device != dev:
-            raise ValueError("attention_backward: all tensors must be on one device")
-    for name, t in (("o", o), ("dout", dout), ("dq", dq), ("dk", dk), ("dv", dv)):
-        if t.dtype != dt:
-            raise ValueError(f"attention_backward: {name} must be {dt}")
-    for name, t in (("gq", gq), ("gk", gk), ("dgq", dgq), ("dgk", dgk)):
-        if t is not None and t.dtype != torch.float32:
-            raise ValueError(f"attention_backward: {name} must be float32")
-    if (gk is None) != (dgk is None):
-        raise ValueError("attention_backward: gk and dgk go together (additive generator)")
-    views = [_token_view(t, B, T, H, d, n) for n, t in (("o", o), ("dout", dout), ("dq", dq), ("dk", dk), ("dv", dv))]
-    gv = [(0, 0) if t is None else _token_view(t, B, T, H, m, n)
-          for n, t in (("gq", gq), ("gk", gk), ("dgq", dgq), ("dgk", dgk))]
+    B, H, T, nb, dev, dt, views, gv = _bwd_inputs("attention_backward", gq, gk, qh, kh, vh_t, P, lse, o, dout, d,
+                                                  dq, dk, dv, dgq, dgk)
     need = int(lib.holo_attn_bwd_workspace_size(B, T, H, d, _DT[dt]))
-    if workspace is not None and not workspace.is_contiguous():
-        raise ValueError("attention_backward: workspace must be contiguous")
-    if workspace is None or workspace.numel() * workspace.element_size() < need:
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    workspace = _workspace("attention_backward", workspace, need, dev)
     mode = _lib.HOLO_GEN_ADDITIVE if gk is not None else _lib.HOLO_GEN_DIRECT
     rc = lib.holo_attn_bwd(B, T, H, d, mode, float(edge_scale), _DT[dt], _lib.HOLO_F32, float(scale),
                            _ptr(gq), *gv[0], _ptr(gk), *gv[1],
@@ -441,6 +490,37 @@ def attention_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge_scale:
                            _ptr(dgq), *gv[2], _ptr(dgk), *gv[3],
                            _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(dev))
     _lib.check(rc, "holo_attn_bwd")
+
+
+def attention_masked_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge_scale: float,
+                              qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
+                              hol: Optional[torch.Tensor], lse: torch.Tensor, o: torch.Tensor, dout: torch.Tensor,
+                              d: int, scale: float, dq: torch.Tensor, dk: torch.Tensor, dv: torch.Tensor,
+                              dgq: torch.Tensor, dgk: Optional[torch.Tensor], mode: str = "causal",
+                              mask: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> None:
+    """holo_attn_masked_bwd: gradients of the exact path (any mask, either
+    mode) given dout; arguments as attention_backward's, plus the mode, the
+    holonomy hol (causal mode) and the mask of the forward; o and lse from
+    attention_masked_train. In causal mode the closing edge (gq_{T-1}, gk_0)
+    gets its gradient through the holonomy."""
+    _one_gpu("attention_masked_backward", qh, kh, vh_t, P, hol, lse, o, dout, dq, dk, dv, gq, gk, dgq, dgk, mask,
+             workspace)
+    lib = _lib.load()
+    what = "attention_masked_backward"
+    *_, m8, m_rs = _masked_inputs(what, qh, kh, vh_t, P, hol, d, mode, mask)
+    B, H, T, nb, dev, dt, views, gv = _bwd_inputs(what, gq, gk, qh, kh, vh_t, P, lse, o, dout, d, dq, dk, dv, dgq, dgk)
+    need = int(lib.holo_attn_masked_bwd_workspace_size(B, T, H, d, _DT[dt], _MODE[mode], int(mask is not None)))
+    workspace = _workspace(what, workspace, need, dev)
+    gm = _lib.HOLO_GEN_ADDITIVE if gk is not None else _lib.HOLO_GEN_DIRECT
+    rc = lib.holo_attn_masked_bwd(B, T, H, d, gm, float(edge_scale), _DT[dt], _lib.HOLO_F32, _MODE[mode],
+                                  float(scale), _ptr(gq), *gv[0], _ptr(gk), *gv[1],
+                                  _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
+                                  _ptr(hol) if mode == "causal" else None, _ptr(lse), _ptr(m8), m_rs,
+                                  _ptr(o), *views[0], _ptr(dout), *views[1],
+                                  _ptr(dq), *views[2], _ptr(dk), *views[3], _ptr(dv), *views[4],
+                                  _ptr(dgq), *gv[2], _ptr(dgk), *gv[3],
+                                  _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(dev))
+    _lib.check(rc, "holo_attn_masked_bwd")
 
 
 def quat_to_dense(quat: torch.Tensor, d: int) -> torch.Tensor:

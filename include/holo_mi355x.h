@@ -23,7 +23,11 @@
  *   holo_attn_bwd       replaces HoloAttnFn.backward (kernel/attention_kernel.py:
  *                       174-187, which recomputes the reference forward under
  *                       autograd): gradients of the attention output with
- *                       respect to q, k, v and the link generator outputs.
+ *                       respect to q, k, v and the link generator outputs;
+ *   holo_attn_masked_train_fwd, holo_attn_masked_bwd
+ *                       the exact path's forward with its log-sum-exp and its
+ *                       backward (torch autograd through kernel/attention_fast.py:
+ *                       78-166 in the reference).
  *
  * Conventions
  *   - Every pointer is a device pointer owned by the caller; no entry point
@@ -307,6 +311,20 @@ HOLO_API int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int
                          void* o, int64_t o_row_stride, int64_t o_head_stride,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * holo_attn_masked_train_fwd: holo_attn_masked_fwd for training (the forward
+ * whose gradient holo_attn_masked_bwd computes; in the reference, torch
+ * autograd records kernel/attention_fast.py:78-166): P in fp32 quaternions
+ * (HOLO_QUAT_F32), and lse (B, H, Tp) fp32 receives each row's log2-domain
+ * log-sum-exp of the scaled scores over both branches (-inf for a row that
+ * allows no key). Same workspace as holo_attn_masked_fwd.
+ */
+HOLO_API int holo_attn_masked_train_fwd(int B, int64_t T, int H, int d, int dtype, int mode, float scale,
+                         const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
+                         const uint8_t* mask, int64_t mask_row_stride,
+                         void* o, int64_t o_row_stride, int64_t o_head_stride, float* lse,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes of holo_attn_bwd. */
 HOLO_API size_t holo_attn_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype);
 
@@ -328,6 +346,38 @@ HOLO_API int holo_attn_bwd(int B, int64_t T, int H, int d, int gen_mode, float e
                   const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
                   const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
                   const void* qh, const void* kh, const void* vh_t, const float* P, const float* lse,
+                  const void* o, int64_t o_row_stride, int64_t o_head_stride,
+                  const void* dout, int64_t dout_row_stride, int64_t dout_head_stride,
+                  void* dq, int64_t dq_row_stride, int64_t dq_head_stride,
+                  void* dk, int64_t dk_row_stride, int64_t dk_head_stride,
+                  void* dv, int64_t dv_row_stride, int64_t dv_head_stride,
+                  float* dgq, int64_t dgq_row_stride, int64_t dgq_head_stride,
+                  float* dgk, int64_t dgk_row_stride, int64_t dgk_head_stride,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of holo_attn_masked_bwd (mode and has_mask as the call's). */
+HOLO_API size_t holo_attn_masked_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype, int mode,
+                                                    int has_mask);
+
+/*
+ * holo_attn_masked_bwd: the gradient of the exact path (any mask, either
+ * mode), as torch autograd takes it through kernel/attention_fast.py:78-166
+ * in the reference. Arguments as holo_attn_bwd's, plus the call's mode, the
+ * holonomy hol (causal mode) and the mask; qh, kh, vh_t, P, hol from
+ * holo_geom_scan_fwd in that mode, o and lse from holo_attn_masked_train_fwd.
+ * In causal mode the holonomy Hol = G_{T-1} P_{T-1} carries the wrap branch,
+ * so the closing edge (a_{T-1} = edge_scale (gq_{T-1} + gk_0)) gets a
+ * gradient; in inert mode it does not. A row that allows no key has a NaN
+ * output; its NaN reaches the link gradients of that token and every
+ * earlier one, and contributes nothing to dq, dk, dv. Calls sharing a
+ * workspace must not overlap in time.
+ */
+HOLO_API int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale,
+                  int io_dtype, int gen_dtype, int mode, float scale,
+                  const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
+                  const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
+                  const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
+                  const float* lse, const uint8_t* mask, int64_t mask_row_stride,
                   const void* o, int64_t o_row_stride, int64_t o_head_stride,
                   const void* dout, int64_t dout_row_stride, int64_t dout_head_stride,
                   void* dq, int64_t dq_row_stride, int64_t dq_head_stride,

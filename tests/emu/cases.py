@@ -401,6 +401,118 @@ def case_masked(emu: Emu, p):
     return res
 
 
+
+def _mask_of(kind, T, seed=5):
+    if kind == "ring":
+        return R.ring_mask(T)
+    if kind == "tril":
+        return np.tril(np.ones((T, T), bool))
+    if kind == "random":
+        mask = np.random.default_rng(seed).random((T, T)) < 0.3
+        mask[np.arange(T), np.arange(T)] = True
+        return mask
+    return None
+
+
+def case_masked_bwd(emu: Emu, p):
+    """The exact path's training pair: holo_geom_scan_fwd (fp32 quaternions)
+    -> holo_attn_masked_train_fwd (o and lse; o bit-identical to
+    holo_attn_masked_fwd's) -> holo_attn_masked_bwd, against
+    oracle.exact_backward64 on the same q, k, v and generator: dq, dk, dv and
+    the generator gradients dgq, dgk (the closing edge's included), each
+    relative to its largest entry, and lse against the float64 value."""
+    B, T, H, d = p["B"], p["T"], p["H"], p["d"]
+    io = p.get("io", F32)
+    mode = MODE_INERT if p.get("mode") == "inert" else MODE_CAUSAL
+    es = p.get("es", 0.9)
+    L = Layer(p.get("seed", 8), B, T, H, d, io, es)
+    s = scan(emu, L, io, io, QUAT_F32, GEN_ADD, mode=mode)
+    mask = _mask_of(p.get("mask", "none"), T)
+    nb, m, Tp = L.nb, L.m, padded_seq(T)
+    md = emu.to_dev(mask.astype(np.uint8), np.uint8) if mask is not None else None
+    scale = 1.0 / math.sqrt(d)
+    hol = s["hol"].ptr if (mode == MODE_CAUSAL and nb) else None
+    n = int(emu.lib.holo_attn_masked_workspace_size(B, T, H, d, io, mode, int(mask is not None)))
+    wsf = emu.empty((max(n, 1),), np.uint8)
+    o = emu.empty((B, T, H, d), _dtype(io))
+    o_ref_kernel = emu.empty((B, T, H, d), _dtype(io))
+    lse = emu.empty((B, H, Tp), np.float32)
+    args = (s["qh"].ptr, s["kh"].ptr, s["vh"].ptr, s["P"].ptr if nb else None, hol,
+            md.ptr if md else None, T if md else 0)
+    emu.check(emu.lib.holo_attn_masked_train_fwd(B, T, H, d, io, mode, scale, *args, o.ptr, H * d, d, lse.ptr,
+                                                 wsf.ptr, n, None), "holo_attn_masked_train_fwd")
+    emu.check(emu.lib.holo_attn_masked_fwd(B, T, H, d, io, QUAT_F32, mode, scale, *args, o_ref_kernel.ptr, H * d, d,
+                                           wsf.ptr, n, None), "holo_attn_masked_fwd")
+    rng = np.random.default_rng(p.get("seed", 8) + 100)
+    do_h = rng.standard_normal((B, T, H, d))
+    do_h = round_bf16(do_h) if io == BF16 else do_h.astype(np.float32).astype(np.float64)
+    dout = emu.to_dev(do_h, _dtype(io))
+    dq, dk, dv = (emu.empty((B, T, H, d), _dtype(io)) for _ in range(3))
+    dgq = emu.empty((B, T, H, m), np.float32)
+    dgk = emu.empty((B, T, H, m), np.float32)
+    nw = int(emu.lib.holo_attn_masked_bwd_workspace_size(B, T, H, d, io, mode, int(mask is not None)))
+    ws = emu.empty((max(nw, 1),), np.uint8)
+    emu.check(emu.lib.holo_attn_masked_bwd(
+        B, T, H, d, GEN_ADD, float(es), io, F32, mode, scale,
+        s["gq"].ptr, H * m, m, s["gk"].ptr, H * m, m,
+        s["qh"].ptr, s["kh"].ptr, s["vh"].ptr, s["P"].ptr if nb else None, hol, lse.ptr,
+        md.ptr if md else None, T if md else 0,
+        o.ptr, H * d, d, dout.ptr, H * d, d,
+        dq.ptr, H * d, d, dk.ptr, H * d, d, dv.ptr, H * d, d,
+        dgq.ptr, H * m, m, dgk.ptr, H * m, m, ws.ptr, nw, None), "holo_attn_masked_bwd")
+    st = emu.empty((1,), np.uint32)
+    emu.check(emu.lib.holo_workspace_status(ws.ptr, ws.nbytes, st.ptr, None), "holo_workspace_status")
+    bh = lambda u: u.transpose(0, 2, 1, 3)
+    mname = "inert" if mode == MODE_INERT else "causal"
+    a = L.a(GEN_ADD)
+    g = R.exact_backward64(bh(L.q), bh(L.k), bh(L.v), a, bh(do_h), scale, mask, mname)
+    Pr, Holr = R.geometry_blocks(a)
+    # lse (log2 domain of the scaled scores) from the float64 scores
+    if mname == "causal":
+        qh_, kh_ = R.apply_blocks_T(Pr, bh(L.q)), R.apply_blocks_T(Pr, bh(L.k))
+        qw_ = R.apply_blocks_T(Holr[:, :, None], qh_)
+        base = np.arange(T)[:, None] >= np.arange(T)[None, :]
+        sc = np.where(base, np.einsum("...id,...jd->...ij", qh_, kh_), np.einsum("...id,...jd->...ij", qw_, kh_))
+    else:
+        qh_, kh_ = R.apply_blocks(Pr, bh(L.q)), R.apply_blocks(Pr, bh(L.k))
+        sc = np.einsum("...id,...jd->...ij", qh_, kh_)
+    sc = sc * scale / math.log(2.0)
+    if mask is not None:
+        sc = np.where(mask, sc, -np.inf)
+    mx = sc.max(-1)
+    lse_ref = mx + np.log2(np.exp2(sc - mx[..., None]).sum(-1))
+    ref = {"dq": g["dq"], "dk": g["dk"], "dv": g["dv"], "dgq": es * g["da"],
+           "dgk": np.roll(es * g["da"], 1, axis=2)}
+    got = {"dq": bh(emu.host(dq, _dtype(io))), "dk": bh(emu.host(dk, _dtype(io))), "dv": bh(emu.host(dv, _dtype(io))),
+           "dgq": bh(dgq.a.astype(np.float64)), "dgk": bh(dgk.a.astype(np.float64))}
+    res = {"status": int(st.a[0]), "o_identical": bool(np.array_equal(o.a, o_ref_kernel.a)),
+           "lse_err": float(np.abs(lse.a[:, :, :T] - lse_ref).max()),
+           "closing_edge_max": float(np.abs(ref["dgq"][:, :, -1]).max())}
+    # errors over each gradient's scale: its largest entry, at least 5% of
+    # the largest entry of any of the five (a gradient that is 0 exactly,
+    # e.g. dq at T = 1, where dS = dA - delta cancels, is then held to the
+    # others' scale)
+    scale_all = max(np.abs(r_).max() for r_ in ref.values())
+    for k_, r_ in ref.items():
+        den = max(np.abs(r_).max(), 0.05 * scale_all)
+        res[k_ + "_rel"] = float(np.abs(got[k_] - r_).max() / den)
+        res[k_ + "_fro"] = float(np.linalg.norm(got[k_] - r_) / max(np.linalg.norm(r_), 0.05 * scale_all))
+    if io == BF16:
+        # the oracle fed the kernel's own transported operands (rounded to
+        # bf16 by the scan): what is left is the backward's own arithmetic
+        Dp = padded_head_dim(d)
+        own = []
+        for buf, tr in ((s["qh"], False), (s["kh"], False), (s["vh"], True)):
+            u = emu.host(buf, "bf16")
+            u = unpack_vh(u.reshape(B, H, Tp // 64, Dp, 64), T) if tr else u.reshape(B, H, Tp, Dp)[:, :, :T]
+            u = u[..., :d]
+            own.append(R.apply_blocks(Pr, u) if mname == "causal" else R.apply_blocks_T(Pr, u))
+        g2 = R.exact_backward64(*own, a, bh(do_h), scale, mask, mname)
+        ref2 = {"dq": g2["dq"], "dk": g2["dk"], "dv": g2["dv"], "dgq": es * g2["da"]}
+        for k_, r_ in ref2.items():
+            res[k_ + "_fro_own"] = float(np.linalg.norm(got[k_] - r_) / max(np.linalg.norm(r_), 0.05 * scale_all))
+    return res
+
 def case_bwd(emu: Emu, p):
     """holo_attn_bwd after holo_geom_scan_fwd (fp32 quaternions) and
     holo_attn_fwd (with lse): dq, dk, dv, dgq, dgk against the float64
@@ -861,7 +973,7 @@ def case_planted(emu: Emu, p):
     return {"completed": True}
 
 
-CASES = {"edge": case_edge, "layer_interaction": case_layer_interaction, "planted": case_planted, "layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
+CASES = {"masked_bwd": case_masked_bwd, "edge": case_edge, "layer_interaction": case_layer_interaction, "planted": case_planted, "layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
          "decode": case_decode, "norm": case_norm, "quat_dense": case_quat_dense, "status": case_status}
 
 

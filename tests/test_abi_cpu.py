@@ -288,3 +288,47 @@ def test_masked_attention_argument_validation(lib):
     assert _masked(lib, wsb=64) == _lib.HOLO_ERR_WORKSPACE
     assert _masked(lib, ws=None) == _lib.HOLO_ERR_WORKSPACE
     assert _masked(lib, mask=None, ws=None, wsb=0, T=0) == _lib.HOLO_ERR_BAD_SHAPE   # no mask: no workspace
+
+
+def _mbwd(lib, **kw):
+    a = dict(B=1, T=8, H=2, d=12, gen=0, es=0.1, io=_lib.HOLO_F32, gdt=_lib.HOLO_F32, mode=_lib.HOLO_MODE_CAUSAL,
+             sc=0.3, gq=16, gk=16, qh=16, kh=16, vh=16, P=16, hol=16, lse=16, mask=16, mrs=8, o=16, do=16, dq=16,
+             dk=16, dv=16, dgq=16, dgk=16, ws=16, wsb=1 << 30, rs=64, hs=24, grs=64, ghs=24)
+    a.update(kw)
+    return lib.holo_attn_masked_bwd(a["B"], a["T"], a["H"], a["d"], a["gen"], a["es"], a["io"], a["gdt"], a["mode"],
+                                    a["sc"], a["gq"], a["grs"], a["ghs"], a["gk"], a["grs"], a["ghs"],
+                                    a["qh"], a["kh"], a["vh"], a["P"], a["hol"], a["lse"], a["mask"], a["mrs"],
+                                    a["o"], a["rs"], a["hs"], a["do"], a["rs"], a["hs"],
+                                    a["dq"], a["rs"], a["hs"], a["dk"], a["rs"], a["hs"], a["dv"], a["rs"], a["hs"],
+                                    a["dgq"], a["grs"], a["ghs"], a["dgk"], a["grs"], a["ghs"],
+                                    a["ws"], a["wsb"], None)
+
+
+def test_exact_path_training_argument_validation(lib):
+    ws = lib.holo_attn_masked_bwd_workspace_size
+    base = lib.holo_attn_bwd_workspace_size(2, 300, 3, 48, _lib.HOLO_BF16)
+    r = lambda x: (x + 255) // 256 * 256
+    n = 2 * 3 * 320 * 64
+    # inert mode, no mask: the tril backward's workspace; a mask adds its bits
+    # and tile map; causal mode adds qw, dow (bf16), dqw, dkw, dvw and the
+    # holonomy's cross sums
+    assert ws(2, 300, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_INERT, 0) == base
+    assert ws(2, 300, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_INERT, 1) == base + r(320 * 5 * 8) + r(3 * 5)
+    assert ws(2, 300, 3, 48, _lib.HOLO_BF16, _lib.HOLO_MODE_CAUSAL, 0) == \
+        base + 2 * r(2 * n) + 3 * r(4 * n) + r(2 * 3 * 16 * 16)
+    assert ws(2, 300, 3, 48, _lib.HOLO_F32, _lib.HOLO_MODE_CAUSAL, 0) == \
+        lib.holo_attn_bwd_workspace_size(2, 300, 3, 48, _lib.HOLO_F32) + 4 * r(4 * n) + 3 * r(4 * n) + r(2 * 3 * 16 * 16)
+    assert ws(2, 300, 3, 48, _lib.HOLO_BF16, 7, 0) == 0
+    assert _mbwd(lib, B=0) == _lib.HOLO_ERR_BAD_SHAPE
+    assert _mbwd(lib, mode=3) == _lib.HOLO_ERR_INVALID_ARG
+    assert _mbwd(lib, hol=None) == _lib.HOLO_ERR_INVALID_ARG             # causal mode needs the holonomy
+    assert _mbwd(lib, hol=8) == _lib.HOLO_ERR_INVALID_ARG                # misaligned
+    assert _mbwd(lib, mrs=7) == _lib.HOLO_ERR_INVALID_ARG                # mask rows shorter than T
+    assert _mbwd(lib, lse=None) == _lib.HOLO_ERR_INVALID_ARG
+    assert _mbwd(lib, gdt=_lib.HOLO_BF16) == _lib.HOLO_ERR_UNSUPPORTED
+    assert _mbwd(lib, wsb=1024) == _lib.HOLO_ERR_WORKSPACE
+    t = lib.holo_attn_masked_train_fwd
+    args = lambda lse: (1, 8, 2, 12, _lib.HOLO_F32, _lib.HOLO_MODE_CAUSAL, 0.3, 16, 16, 16, 16, 16, 16, 8,
+                        16, 24, 12, lse, 16, 1 << 20, None)
+    assert t(*args(None)) == _lib.HOLO_ERR_INVALID_ARG                    # the LSE is the point of this call
+    assert t(*args(8)) == _lib.HOLO_ERR_INVALID_ARG                       # misaligned LSE

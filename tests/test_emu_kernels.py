@@ -25,6 +25,11 @@ Tolerances (written per case below):
                  bf16 bar); bf16 o within 2.5e-2 * max(1, max|o| / 4).
   GEMM        -- every element within the rounding bounds of
                  tests/test_gpu_gemm.py (err / bound <= 1).
+  exact-path backward -- fp32: every gradient within 2e-5 of its scale (its
+                 largest entry, at least 5% of the largest of the five), lse
+                 1e-5; bf16: dq, dk, dv relative Frobenius 1.5e-2, the
+                 generator gradients 3e-2 (the backward's bf16 bar); the
+                 training forward's o bit-identical to holo_attn_masked_fwd's.
   edge MLP    -- hidden values, q/k/v and the fp32 second layer within the
                  rounding bounds of tests/test_gpu_edge_mlp.py (err / bound
                  <= 1); the hidden-only launch bit-identical to the combined
@@ -262,6 +267,56 @@ def test_emulated_edge_mlp(edge_results, cid):
     assert r["stats"]["launches"] > 0
     ok = check(r)
     assert ok is None or ok, r
+
+
+# ---- exact path's backward (holo_attn_masked_train_fwd + holo_attn_masked_bwd; off in the module) ----
+def _mbwd(io, wrap_pairs):
+    def check(r):
+        assert r["status"] == 0 and r["o_identical"], r
+        if io == F32:
+            assert r["lse_err"] <= 1e-5, r
+            assert all(v <= 2e-5 for k, v in r.items() if k.endswith("_rel")), r
+        else:
+            assert r["lse_err"] <= 2e-2, r
+            assert all(r[k + "_fro"] <= 1.5e-2 for k in ("dq", "dk", "dv")), r
+            assert r["dgq_fro"] <= 3e-2 and r["dgk_fro"] <= 3e-2, r
+        # the closing edge has a gradient exactly when wrap pairs are open
+        assert (r["closing_edge_max"] > 1e-3) == wrap_pairs, r
+    return check
+
+
+MBWD = []
+for (B, T, H, d, mode, mask, io, es) in [
+        (1, 70, 2, 12, "causal", "none", F32, 0.9), (1, 70, 2, 12, "inert", "none", F32, 0.9),
+        (2, 130, 3, 16, "causal", "ring", F32, 0.9), (2, 130, 3, 16, "inert", "random", F32, 0.9),
+        (1, 65, 2, 48, "causal", "random", F32, 0.9), (1, 65, 2, 48, "causal", "tril", F32, 0.9),
+        (1, 1, 2, 12, "causal", "none", F32, 0.9), (1, 129, 2, 96, "causal", "none", F32, 0.9),
+        (1, 129, 2, 96, "inert", "ring", F32, 0.9), (1, 100, 2, 34, "causal", "random", F32, 0.9),
+        (2, 64, 1, 5, "inert", "none", F32, 0.9),
+        (1, 300, 2, 96, "causal", "none", BF16, 0.05), (1, 300, 2, 96, "inert", "ring", BF16, 0.05),
+        (2, 200, 2, 64, "causal", "random", BF16, 0.9), (1, 300, 2, 96, "causal", "tril", BF16, 0.05)]:
+    wrap_pairs = mode == "causal" and mask != "tril" and T > 1
+    MBWD.append((f"masked_bwd_{mode}_{mask}_{'bf16' if io == BF16 else 'f32'}_B{B}_T{T}_H{H}_d{d}", "masked_bwd",
+                 dict(B=B, T=T, H=H, d=d, mode=mode, mask=mask, io=io, es=es), _mbwd(io, wrap_pairs)))
+jobs.register("masked_bwd", [(name, params) for _, name, params, _ in MBWD], timeout=900)
+
+
+@pytest.fixture(scope="module")
+def mbwd_results():
+    rc, out, res = jobs.result("masked_bwd")
+    if rc != 0 or res is None:
+        pytest.fail(f"emulated run failed (status {rc}):\n{out[-12000:]}")
+    assert len(res["cases"]) == len(MBWD)
+    return {cid: r for (cid, *_), r in zip(MBWD, res["cases"])}
+
+
+@pytest.mark.emu_jobs("masked_bwd")
+@pytest.mark.parametrize("cid", [c[0] for c in MBWD])
+def test_emulated_exact_path_backward(mbwd_results, cid):
+    check = next(c[3] for c in MBWD if c[0] == cid)
+    r = mbwd_results[cid]
+    assert r["stats"]["launches"] > 0
+    check(r)
 
 
 # ---- the checker fires: mistakes planted in the caller's buffers (CPU only) ----

@@ -19,8 +19,9 @@ Config 5's prefill scan runs at B = 2 (its launches at B = 64 differ only in
 the batch offset, which config 2's B = 16 run and the B = 64 GEMM and
 attention exercise); the exact-path and interaction layouts run at B = 4 of
 config 2, the training step's backward at one batch row and two heads of
-config 2's head size. The fused interaction generator's two GEMMs (off in
-the module) run at config 2's shape with sampled workgroups.
+config 2's head size (also the exact path's training pair, off in the
+module). The fused interaction generator's two GEMMs (off in the module) run
+at config 2's shape with sampled workgroups.
 """
 from __future__ import annotations
 
@@ -43,6 +44,12 @@ CHECKS = [
     ("cfg2_exact_ring_inert", "layer_paths", dict(B=4, **CFG2, path="exact", mask="ring", mode="inert",
                                                   sample_attn=S)),
     ("cfg2_train_backward_bf16", "bwd", dict(B=1, T=1024, H=2, d=96, io=1, es=0.05)),
+    # the exact path's training pair (off in the module) at the same head
+    # shape: causal mode with the ring mask (wrap pairs open), inert mode
+    ("cfg2_exact_train_backward_ring_bf16", "masked_bwd", dict(B=1, T=1024, H=2, d=96, io=1, es=0.05,
+                                                               mode="causal", mask="ring")),
+    ("cfg2_exact_train_backward_inert_bf16", "masked_bwd", dict(B=1, T=1024, H=2, d=96, io=1, es=0.05,
+                                                                mode="inert")),
     # the fused interaction generator (off in the module): first and last
     # four and every 997th workgroup of both GEMMs, written entries checked
     ("cfg2_fused_interaction_gemms", "edge", dict(B=16, T=2048, K=1536, H=16, sample=[4, 4, 997])),
@@ -98,6 +105,9 @@ def test_launch_in_bounds(checked, cid):
         assert r["h_err"] == 0.0 and r["y_err"] <= 2.0 ** -8 * r["y_max"] + 1e-5, r
     if cid == "cfg2_train_backward_bf16":
         assert all(v <= 3e-2 for k, v in r.items() if k.endswith("_fro")), r
+    if cid.startswith("cfg2_exact_train_backward"):
+        assert r["o_identical"] and all(v <= 3e-2 for k, v in r.items() if "_fro" in k), r
+        assert (r["closing_edge_max"] > 1e-3) == ("ring" in cid), r
     if cid == "cfg2_fused_interaction_gemms":
         assert r["hid_err_over_bound"] <= 1.0 and r["qkv_err_over_bound"] <= 1.0 and r["g_err_over_bound"] <= 1.0, r
         assert r["written_hid"] > 0 and r["written_qkv"] > 0 and r["written_g"] > 0, r

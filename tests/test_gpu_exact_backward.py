@@ -1,0 +1,81 @@
+"""The exact path's training pair on the GPU (holo_attn_masked_train_fwd +
+holo_attn_masked_bwd, through kernels.attention_masked_train and
+kernels.attention_masked_backward): every gradient against the float64
+oracle (oracle.holo_ref.exact_backward64, pinned by central differences of
+the exact-path forward) for causal mode with the wrap branch through the
+holonomy and for inert mode, with no mask, the ring mask and a random mask.
+
+Bars (written in the tests): fp32 every gradient within 2e-5 of its scale
+(its largest entry); bf16 relative Frobenius 1.5e-2 for dq, dk, dv and 3e-2
+for the generator gradients (the tril backward's bf16 bar); the training
+forward's o equal to attention_masked's.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from holonomyawareattention_amd import kernels
+from oracle import holo_ref as R
+
+pytestmark = [
+    pytest.mark.gpu,
+    # Built and checked on the CPU emulation of the kernels only
+    # (tests/test_emu_kernels.py, tests/test_emu_launch_checker.py): GPU use
+    # for the repository was closed before these kernels could run on a GPU.
+    # The module keeps the path off (exact_backward = False) until they have.
+    pytest.mark.skip(reason="exact-path backward not yet run on a GPU (executed on the CPU emulation only)"),
+]
+DEV = torch.device("cuda:0")
+
+
+def _inputs(seed, B, T, H, d, dtype, es):
+    rng = np.random.default_rng(seed)
+    m = 3 * (d // 3)
+    f = lambda a: torch.as_tensor(a, dtype=torch.float32).to(dtype)
+    q, k, v, do = (f(rng.standard_normal((B, T, H, d))) for _ in range(4))
+    gq, gk = (torch.as_tensor(rng.standard_normal((B, T, H, m)), dtype=torch.float32) for _ in range(2))
+    return q, k, v, gq, gk, do
+
+
+@pytest.mark.parametrize("mode", ["causal", "inert"])
+@pytest.mark.parametrize("mask_kind", ["none", "ring", "random"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_exact_path_gradients_against_the_oracle(mode, mask_kind, dtype):
+    B, T, H, d, es = 2, 300, 2, 96, 0.05
+    q, k, v, gq, gk, do = _inputs(7, B, T, H, d, dtype, es)
+    mask = None
+    if mask_kind == "ring":
+        mask = torch.as_tensor(R.ring_mask(T))
+    elif mask_kind == "random":
+        mask = torch.as_tensor(np.random.default_rng(3).random((T, T)) < 0.3)
+        mask[torch.arange(T), torch.arange(T)] = True
+    dv_ = lambda t: t.to(DEV)
+    qd, kd, vd, gqd, gkd, dod = (dv_(t) for t in (q, k, v, gq, gk, do))
+    md = None if mask is None else mask.to(DEV)
+    scale = 1.0 / math.sqrt(d)
+    qh, kh, vh_t, P, hol = kernels.geom_scan(qd, kd, vd, gqd, gkd, es, want_hol=mode == "causal", p_format="f32",
+                                             mode=mode)
+    o, lse = kernels.attention_masked_train(qh, kh, vh_t, P, hol, d, scale, mode=mode, mask=md)
+    o2 = kernels.attention_masked(qh, kh, vh_t, P, hol, d, scale, mode=mode, mask=md)
+    dq, dk, dv = (torch.empty_like(qd) for _ in range(3))
+    dgq, dgk = torch.empty_like(gqd), torch.empty_like(gkd)
+    kernels.attention_masked_backward(gqd, gkd, es, qh, kh, vh_t, P, hol, lse, o, dod, d, scale, dq, dk, dv, dgq, dgk,
+                                      mode=mode, mask=md)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2)
+    bh = lambda t: t.double().cpu().numpy().transpose(0, 2, 1, 3)
+    a = es * (bh(gq) + np.roll(bh(gk), -1, axis=2))
+    g = R.exact_backward64(bh(q), bh(k), bh(v), a, bh(do), scale, None if mask is None else mask.numpy(), mode)
+    ref = {"dq": g["dq"], "dk": g["dk"], "dv": g["dv"], "dgq": es * g["da"], "dgk": np.roll(es * g["da"], 1, axis=2)}
+    got = {"dq": bh(dq), "dk": bh(dk), "dv": bh(dv), "dgq": bh(dgq), "dgk": bh(dgk)}
+    for name, r in ref.items():
+        err = got[name] - r
+        if dtype == torch.float32:
+            assert np.abs(err).max() <= 2e-5 * np.abs(r).max(), name
+        else:
+            bar = 3e-2 if name.startswith("dg") else 1.5e-2
+            assert np.linalg.norm(err) <= bar * np.linalg.norm(r), name

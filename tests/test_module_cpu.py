@@ -224,3 +224,65 @@ def test_status_word_and_operand_options_reach_the_scan(monkeypatch):
     assert m._op_dtype(xb) == torch.float16
     m.fp16_operands = False
     assert m._op_dtype(xb) == torch.bfloat16 and m._op_dtype(x) == torch.float32
+
+
+def test_exact_backward_option_routes_autograd_through_the_exact_path(monkeypatch):
+    """exact_backward on: a call off the causal + tril path under autograd
+    runs _ExactPathAttention, whose forward takes the scan in the module's
+    mode and holo_attn_masked_train_fwd, and whose backward takes
+    holo_attn_masked_bwd with the same mode, mask and saved state; gradients
+    then reach the weights. Off (the default): the forward-only outputs'
+    backward raises. Stand-ins for the kernel wrappers (no GPU here)."""
+    from holonomyawareattention_amd import attention_kernel as AK
+    B, T, D, H = 1, 6, 24, 2
+    d = D // H
+    seen = {}
+
+    def fake_scan(q, k, v, gq, gk, es, want_hol=False, p_format="f32", mode="causal", op_dtype=None,
+                  status=None, static_scratch=False):
+        seen["scan"] = (mode, want_hol, p_format, gk is None)
+        P = torch.zeros(B, H, T, d // 3, 4)
+        hol = torch.zeros(B, H, d // 3, 4) if want_hol else None
+        return torch.zeros(1), torch.zeros(1), torch.zeros(1), P, hol
+
+    def fake_train(qh, kh, vh_t, P, hol, d_, scale, mode="causal", mask=None):
+        seen["train"] = (mode, None if mask is None else mask.clone(), hol is not None)
+        return torch.ones(B, T, H, d_), torch.zeros(B, H, 64)
+
+    def fake_bwd(gq, gk, es, qh, kh, vh_t, P, hol, lse, o, dout, d_, scale, dq, dk, dv, dgq, dgk, mode="causal",
+                 mask=None, workspace=None):
+        seen["bwd"] = (mode, None if mask is None else mask.clone(), tuple(dout.shape))
+        for t in (dq, dk, dv, dgq) + ((dgk,) if dgk is not None else ()):
+            t.fill_(1.0)
+
+    monkeypatch.setattr(AK.kernels, "geom_scan", fake_scan)
+    monkeypatch.setattr(AK.kernels, "attention_masked_train", fake_train)
+    monkeypatch.setattr(AK.kernels, "attention_masked_backward", fake_bwd)
+    ring = torch.zeros(T, T, dtype=torch.bool)
+    for i in range(T):
+        ring[i, [i, (i - 1) % T, (i + 1) % T]] = True
+    for mode, link in (("causal", "additive"), ("inert", "interaction")):
+        seen.clear()
+        m = PathOrderedGeometricMHA(D, n_heads=H, mode=mode)
+        m.link_mode = link
+        m.exact_backward = True
+        x = torch.randn(B, T, D, requires_grad=True)
+        y = m._forward_autograd(x, exact_mask=(ring,))
+        assert seen["scan"] == (mode, mode == "causal", "f32", link == "interaction")
+        assert seen["train"][0] == mode and torch.equal(seen["train"][1], ring) and seen["train"][2] == (mode == "causal")
+        y.sum().backward()
+        assert seen["bwd"][0] == mode and torch.equal(seen["bwd"][1], ring) and seen["bwd"][2] == (B, T, H, d)
+        assert x.grad is not None and m.qkv.weight.grad is not None
+        assert (m.gqproj.weight.grad if link == "additive" else m.edge_mlp[0].weight.grad) is not None
+    m = PathOrderedGeometricMHA(D, n_heads=H)
+    assert m.exact_backward is False
+
+
+def test_forward_only_outputs_without_exact_backward():
+    """With exact_backward off, the module's forward under autograd for a
+    non-tril call keeps returning outputs whose backward raises."""
+    from holonomyawareattention_amd.attention_kernel import _ForwardOnly
+    x = torch.randn(2, 3, requires_grad=True)
+    y = _ForwardOnly.apply("an attention mask other than tril(L)", 1, x * 2, x)
+    with pytest.raises(NotImplementedError, match="tril"):
+        y.sum().backward()
