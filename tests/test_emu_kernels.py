@@ -279,7 +279,7 @@ def _mbwd(io, wrap_pairs):
         else:
             assert r["lse_err"] <= 2e-2, r
             assert all(r[k + "_fro"] <= 1.5e-2 for k in ("dq", "dk", "dv")), r
-            assert r["dgq_fro"] <= 3e-2 and r["dgk_fro"] <= 3e-2, r
+            assert r["dgq_fro"] <= 3e-2 and r.get("dgk_fro", 0.0) <= 3e-2, r
         # the closing edge has a gradient exactly when wrap pairs are open
         assert (r["closing_edge_max"] > 1e-3) == wrap_pairs, r
     return check
@@ -298,6 +298,12 @@ for (B, T, H, d, mode, mask, io, es) in [
     wrap_pairs = mode == "causal" and mask != "tril" and T > 1
     MBWD.append((f"masked_bwd_{mode}_{mask}_{'bf16' if io == BF16 else 'f32'}_B{B}_T{T}_H{H}_d{d}", "masked_bwd",
                  dict(B=B, T=T, H=H, d=d, mode=mode, mask=mask, io=io, es=es), _mbwd(io, wrap_pairs)))
+# the direct generator (the interaction MLP's output g: a_t = es g_t, the
+# closing edge's g_{T-1} from the pair (x_{T-1}, x_0))
+for (mode, mask, io) in [("causal", "random", F32), ("inert", "ring", F32), ("causal", "none", BF16)]:
+    MBWD.append((f"masked_bwd_direct_{mode}_{mask}_{'bf16' if io == BF16 else 'f32'}", "masked_bwd",
+                 dict(B=2, T=100, H=2, d=24, mode=mode, mask=mask, io=io, es=0.5, gen=1),
+                 _mbwd(io, mode == "causal")))
 jobs.register("masked_bwd", [(name, params) for _, name, params, _ in MBWD], timeout=900)
 
 
