@@ -358,6 +358,112 @@ def case_layer_interaction(emu: Emu, p):
     return {"status": int(st.a[0]), "o_err": float(np.abs(og - o_ref).max()), "o_max": float(np.abs(o_ref).max())}
 
 
+
+def case_stage_bound(emu: Emu, p):
+    """tests/test_gpu_parity_bar.py::test_attention_stage_rounding_bound on
+    the emulation, with the same seeded layer (tests._util.layer(22, ...)):
+    the projections as float64 products rounded once (bf16 q/k/v, fp32 gq,
+    gk; on the GPU hipBLASLt made them, so a few values may differ in their
+    last bit), holo_geom_scan_fwd with `op` operands, holo_attn_fwd with an
+    fp32 o, then the test's measure: the error against the float64 oracle fed
+    the kernel's own qh, kh, vh, P, and that error over the test's rounding
+    bound. The GPU run recorded both figures for each shape."""
+    import torch
+    from tests._util import layer
+    B, T, D, H, op = p["B"], p["T"], p["D"], p["H"], p["op"]
+    es, d = 0.5, D // H
+    nb, m = d // 3, 3 * (d // 3)
+    M, Dp, Tp = B * T, padded_head_dim(d), padded_seq(T)
+    x, W = layer(22, B, T, D, H, dtype=torch.bfloat16)
+    x2 = x.reshape(M, D)
+    qkv = emu.to_dev(round_bf16(x2 @ W["qkv.weight"].T), "bf16")
+    gq = emu.to_dev((x2 @ W["gqproj.weight"].T).astype(np.float32), np.float32)
+    gk = emu.to_dev((x2 @ W["gkproj.weight"].T).astype(np.float32), np.float32)
+    qh = emu.empty((B, H, Tp, Dp), _dtype(op))
+    kh = emu.empty((B, H, Tp, Dp), _dtype(op))
+    vh = emu.empty((B, H, Tp // 64, Dp, 64), _dtype(op))
+    P = emu.empty((B, H, T, nb, 4), np.float32)
+    n = int(emu.lib.holo_geom_scan_workspace_size(B, T, H, d))
+    ws = emu.empty((max(n, 1),), np.uint8)
+    E = 2
+    emu.check(emu.lib.holo_geom_scan_fwd(B, T, H, d, GEN_ADD, float(es), BF16, op, F32, QUAT_F32, MODE_CAUSAL,
+                                         gq.ptr, H * m, m, gk.ptr, H * m, m,
+                                         qkv.ptr, 3 * D, 3 * d, qkv.ptr + d * E, 3 * D, 3 * d,
+                                         qkv.ptr + 2 * d * E, 3 * D, 3 * d,
+                                         qh.ptr, kh.ptr, vh.ptr, P.ptr, None, ws.ptr, n, None), "holo_geom_scan_fwd")
+    o = emu.empty((B, T, H, d), np.float32)
+    scale = 1.0 / math.sqrt(d)
+    emu.check(emu.lib.holo_attn_fwd(B, T, H, d, op, F32, QUAT_F32, scale, qh.ptr, kh.ptr, vh.ptr, P.ptr,
+                                    o.ptr, H * d, d, None, None), "holo_attn_fwd")
+    qhr = emu.host(qh, _dtype(op))[:, :, :T, :d]
+    khr = emu.host(kh, _dtype(op))[:, :, :T, :d]
+    vhr = unpack_vh(emu.host(vh, _dtype(op)), T)[..., :d]
+    Pb = quat_to_mat(P.a.astype(np.float64))
+    oh = R.causal_attention64(qhr, khr, vhr, scale)
+    o_ref = R.apply_blocks(Pb, oh)
+    u = 2.0 ** -8 if op == BF16 else 2.0 ** -11
+    spread = R.causal_attention64(qhr, khr, np.abs(vhr), scale) * (2 * u / (1 - u))
+    blk = np.sqrt((spread[..., :3 * nb].reshape(*spread.shape[:-1], nb, 3) ** 2).sum(-1))
+    bound = np.concatenate([np.repeat(blk, 3, axis=-1), spread[..., 3 * nb:]], axis=-1)
+    bound = bound + (1e-5 + T * 2.0 ** -25) * np.abs(vhr).max()
+    err = np.abs(o.a.astype(np.float64).transpose(0, 2, 1, 3) - o_ref)
+    return {"max_err": float(err.max()), "max_err_over_bound": float((err / bound).max())}
+
+
+def case_cfg2_head_bar(emu: Emu, p):
+    """tests/test_gpu_parity_bar.py::test_cfg2_per_head_output_2e3's first
+    measure on the emulation: config 2's seeded layer (tests._util.layer(2,
+    16, 2048, 1536, 16)), every (b, h) at the first `tlen` positions, which
+    depend on tokens 0..tlen-1 only (P_t on links 0..t-1, query t on keys
+    0..t), so the sequences are cut to tlen tokens. The product's path as
+    the test runs it: holo_qkvg_proj_fwd (q/k/v and g), holo_geom_scan_fwd in
+    direct mode with fp16 operands and int16 quaternions, holo_attn_fwd with
+    an fp32 o; against the float64 oracle fed the kernels' own q, k, v, g.
+    Returns the max error, its (b, h, t, c), |o| there and the rms, the
+    figures the GPU run printed."""
+    import torch
+    from tests._util import layer
+    B, Tf, D, H, es = 16, 2048, 1536, 16, 0.05
+    T = p.get("tlen", 256)
+    d = D // H
+    nb, m = d // 3, 3 * (d // 3)
+    M, Dp, Tp = B * T, padded_head_dim(d), padded_seq(T)
+    x, W = layer(2, B, Tf, D, H, dtype=torch.bfloat16)
+    x = np.ascontiguousarray(x[:, :T]).reshape(M, D)
+    xd = emu.to_dev(x, "bf16")
+    wq, wg0, wg1 = (emu.to_dev(W[k], "bf16") for k in ("qkv.weight", "gqproj.weight", "gkproj.weight"))
+    qkv = emu.empty((M, 3 * D), "bf16")
+    g = emu.empty((M, H * m), np.float32)
+    emu.check(emu.lib.holo_qkvg_proj_fwd(M, T, D, 3 * D, H * m, xd.ptr, D, wq.ptr, wg0.ptr, wg1.ptr,
+                                         qkv.ptr, 3 * D, g.ptr, H * m, None), "holo_qkvg_proj_fwd")
+    qh = emu.empty((B, H, Tp, Dp), np.float16)
+    kh = emu.empty((B, H, Tp, Dp), np.float16)
+    vh = emu.empty((B, H, Tp // 64, Dp, 64), np.float16)
+    P = emu.empty((B, H, T, nb, 4), np.int16)
+    n = int(emu.lib.holo_geom_scan_workspace_size(B, T, H, d))
+    ws = emu.empty((max(n, 1),), np.uint8)
+    E = 2
+    emu.check(emu.lib.holo_geom_scan_fwd(B, T, H, d, GEN_DIRECT, float(es), BF16, F16, F32, QUAT_S16, MODE_CAUSAL,
+                                         g.ptr, H * m, m, None, 0, 0,
+                                         qkv.ptr, 3 * D, 3 * d, qkv.ptr + d * E, 3 * D, 3 * d,
+                                         qkv.ptr + 2 * d * E, 3 * D, 3 * d,
+                                         qh.ptr, kh.ptr, vh.ptr, P.ptr, None, ws.ptr, n, None), "holo_geom_scan_fwd")
+    o = emu.empty((B, T, H, d), np.float32)
+    emu.check(emu.lib.holo_attn_fwd(B, T, H, d, F16, F32, QUAT_S16, 1.0 / math.sqrt(d), qh.ptr, kh.ptr, vh.ptr,
+                                    P.ptr, o.ptr, H * d, d, None, None), "holo_attn_fwd")
+    bh = lambda u: u.transpose(0, 2, 1, 3)
+    qkvh = emu.host(qkv, "bf16").reshape(B, T, H, 3 * d)
+    qq, kk, vv = (bh(qkvh[..., i * d:(i + 1) * d]) for i in range(3))
+    a = es * bh(g.a.astype(np.float64).reshape(B, T, H, m))
+    Pr, _ = R.geometry_blocks(a)
+    rows = np.arange(T)
+    ref = R.apply_blocks(Pr, R.attention_rows64(*(R.apply_blocks_T(Pr, u) for u in (qq, kk, vv)),
+                                                1.0 / math.sqrt(d), rows))
+    err = np.abs(bh(o.a.astype(np.float64)) - ref)
+    i = np.unravel_index(err.argmax(), err.shape)
+    return {"max": float(err.max()), "at": [int(j) for j in i], "o_at": float(abs(ref[i])),
+            "rms": float(np.sqrt((err ** 2).mean()))}
+
 def case_masked(emu: Emu, p):
     """holo_attn_masked_fwd (exact path: any mask, causal mode's wrap branch
     through the holonomy, inert mode) against oracle.exact_attention64 on the
@@ -978,7 +1084,7 @@ def case_planted(emu: Emu, p):
     return {"completed": True}
 
 
-CASES = {"masked_bwd": case_masked_bwd, "edge": case_edge, "layer_interaction": case_layer_interaction, "planted": case_planted, "layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
+CASES = {"cfg2_head_bar": case_cfg2_head_bar, "stage_bound": case_stage_bound, "masked_bwd": case_masked_bwd, "edge": case_edge, "layer_interaction": case_layer_interaction, "planted": case_planted, "layer_paths": case_layer_paths, "decode_bounds": case_decode_bounds, "dma_modes": case_dma_modes, "static_scan": case_static_scan, "layer": case_layer, "scan_attn": case_scan_attn, "gemm": case_gemm, "masked": case_masked, "bwd": case_bwd,
          "decode": case_decode, "norm": case_norm, "quat_dense": case_quat_dense, "status": case_status}
 
 
