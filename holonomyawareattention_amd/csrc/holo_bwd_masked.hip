@@ -131,6 +131,16 @@ attn_bwd_masked_dkdv(MaskedBwdArgs a) {
         if (rel == kRelBase && qs0 + kBT - 1 < kw0) return;    // every query before every key of the wave
         if (rel == kRelWrap && qs0 >= kw0 + kBT - 1) return;   // no query before any key of the wave
         const int ro = kBT * sub;
+        if (a.mask_bits != nullptr) {
+          // a sub-tile the mask closes for every pair of the wave adds only
+          // zeros: skip it (uniform over the wave)
+          bool open = false;
+          static_for<16>([&](auto rr) {
+            const int qr = 8 * (rr >> 2) + 4 * g + (rr & 3);
+            open = open || ((mw_s[ro + qr][kword] >> kbit) & 1ull) != 0ull;
+          });
+          if (!__any(open)) return;
+        }
         f32x16 S = f32x16{}, dP = f32x16{};
         static_for<C::QF>([&](auto s) {
           if constexpr (kBF) {
@@ -271,6 +281,9 @@ attn_bwd_masked_dq(MaskedBwdArgs a) {
         if (rel == kRelBase && ks0 > qw0 + kBT - 1) return;    // every key after every query
         if (rel == kRelWrap && ks0 + kBT - 1 <= qw0) return;   // no key after any query
         const int ro = kBT * sub;
+        // a sub-tile whose 32 keys the mask closes for all of the wave's
+        // queries adds only zeros: skip it (uniform over the wave)
+        if (a.mask_bits != nullptr && !__any(((mw >> ro) & 0xffffffffull) != 0ull)) return;
         f32x16 S = f32x16{}, dP = f32x16{};
         static_for<C::QF>([&](auto s) {
           if constexpr (kBF) {

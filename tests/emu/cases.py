@@ -603,9 +603,14 @@ def case_masked_bwd(emu: Emu, p):
     if add:                               # gk_{t+1} enters edge t (gk_0 the closing edge)
         ref["dgk"] = np.roll(es * g["da"], 1, axis=2)
         got["dgk"] = bh(dgk.a.astype(np.float64))
+    import hashlib
+    digest = hashlib.sha256()
+    for b_ in (dq, dk, dv, dgq) + ((dgk,) if add else ()):
+        digest.update(b_.a.tobytes())
     res = {"status": int(st.a[0]), "o_identical": bool(np.array_equal(o.a, o_ref_kernel.a)),
            "lse_err": float(np.abs(lse.a[:, :, :T] - lse_ref).max()),
-           "closing_edge_max": float(np.abs(ref["dgq"][:, :, -1]).max())}
+           "closing_edge_max": float(np.abs(ref["dgq"][:, :, -1]).max()),
+           "grad_sha256": digest.hexdigest()}
     # errors over each gradient's scale: its largest entry, at least 5% of
     # the largest entry of any of the five (a gradient that is 0 exactly,
     # e.g. dq at T = 1, where dS = dA - delta cancels, is then held to the
