@@ -289,11 +289,28 @@ def decode_bench(args, torch, F, synth, kernels, Module):
             "prefill_s": round(prefill_s, 3), "cpu_baseline": None}
 
 
+def layer_mask(kind, T, torch, dev):
+    """(mask or None, allowed pairs) of --mask: tril, none (every pair) or the
+    ring mask of core/utils.py:59-75."""
+    if kind == "tril":
+        return torch.ones(T, T, dtype=torch.bool, device=dev).tril(), T * (T + 1) // 2
+    if kind == "ring":
+        i = torch.arange(T, device=dev)
+        mask = torch.zeros(T, T, dtype=torch.bool, device=dev)
+        for off in (-1, 0, 1):
+            mask[i, (i + off) % T] = True
+        return mask, int(mask.sum())
+    return None, T * T
+
+
 def train_bench(args, torch, F, synth, kernels, Module):
     """Forward + backward of one layer at a BASELINE config (default config 2)
-    through the module's autograd path, and the fused backward (holo_attn_bwd)
-    timed alone on the saved forward state. The backward attention's
-    algorithmic work is 2.5x the forward's (recomputed QK^T, dP, dV, dK, dQ)."""
+    through the module's autograd path, and the backward timed alone on the
+    saved forward state: the fused backward (holo_attn_bwd) for causal + tril,
+    or with --exact-backward the exact path's (holo_attn_masked_bwd) for
+    --mask none|ring or --mode inert. The backward attention's algorithmic
+    work is 2.5x the forward's (recomputed QK^T, dP, dV, dK, dQ) over the
+    pairs the mask allows."""
     cfg = CONFIGS[args.config]
     B, T, D, H, es = cfg["B"], cfg["T"], cfg["D"], cfg["H"], cfg["es"]
     d = D // H
@@ -301,14 +318,16 @@ def train_bench(args, torch, F, synth, kernels, Module):
     dev = torch.device("cuda:0")
     inp = synth.layer_inputs(2, B, T, D, H, "additive")
     x = torch.as_tensor(inp.pop("x")).to(dev, dt)
-    m = Module(D, n_heads=H, edge_scale=es)
+    m = Module(D, n_heads=H, edge_scale=es, mode=args.mode)
     m.link_mode = "additive"
+    m.exact_backward = args.exact_backward
     with torch.no_grad():
         for k, p in m.state_dict().items():
             if k in inp:
                 p.copy_(torch.as_tensor(inp[k]))
     m = m.to(device=dev, dtype=dt).train()
-    mask = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
+    mask, pairs = layer_mask(args.mask, T, torch, dev)
+    exact = args.exact_backward
     g = torch.Generator(device=dev).manual_seed(3)
     dy = torch.randn(B, T, D, device=dev, generator=g).to(dt)
 
@@ -325,20 +344,32 @@ def train_bench(args, torch, F, synth, kernels, Module):
         step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # the fused backward alone, on the state of one forward
+    # the backward alone, on the state of one forward
     with torch.no_grad():
         q, k, v, gq, gk = m._link_inputs(x)
-        qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, es, p_format="f32")
-        lse = torch.empty((B, H, qh.shape[2]), dtype=torch.float32, device=dev)
-        o = kernels.attention(qh, kh, vh_t, P, d, m.scale, lse=lse)
         do = torch.randn(B, T, H, d, device=dev, generator=g).to(dt)
         dqkv = torch.empty(B, T, H, 3 * d, dtype=dt, device=dev)
         dgq, dgk = torch.empty_like(gq), torch.empty_like(gk)
-        ws = torch.empty(int(kernels._lib.load().holo_attn_bwd_workspace_size(B, T, H, d, kernels._DT[dt])),
-                         dtype=torch.uint8, device=dev)
-        run = lambda: kernels.attention_backward(gq, gk, es, qh, kh, vh_t, P, lse, o, do, d, m.scale,
-                                                 dqkv[..., :d], dqkv[..., d:2 * d], dqkv[..., 2 * d:],
-                                                 dgq, dgk, workspace=ws)
+        lib = kernels._lib.load()
+        dqs = (dqkv[..., :d], dqkv[..., d:2 * d], dqkv[..., 2 * d:])
+        if exact:
+            qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, es, want_hol=args.mode == "causal",
+                                                     p_format="f32", mode=args.mode)
+            o, lse = kernels.attention_masked_train(qh, kh, vh_t, P, hol, d, m.scale, mode=args.mode, mask=mask)
+            ws = torch.empty(int(lib.holo_attn_masked_bwd_workspace_size(B, T, H, d, kernels._DT[dt],
+                                                                          kernels._MODE[args.mode],
+                                                                          int(mask is not None))),
+                             dtype=torch.uint8, device=dev)
+            run = lambda: kernels.attention_masked_backward(gq, gk, es, qh, kh, vh_t, P, hol, lse, o, do, d, m.scale,
+                                                            *dqs, dgq, dgk, mode=args.mode, mask=mask, workspace=ws)
+        else:
+            qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, es, p_format="f32")
+            lse = torch.empty((B, H, qh.shape[2]), dtype=torch.float32, device=dev)
+            o = kernels.attention(qh, kh, vh_t, P, d, m.scale, lse=lse)
+            ws = torch.empty(int(lib.holo_attn_bwd_workspace_size(B, T, H, d, kernels._DT[dt])),
+                             dtype=torch.uint8, device=dev)
+            run = lambda: kernels.attention_backward(gq, gk, es, qh, kh, vh_t, P, lse, o, do, d, m.scale,
+                                                     *dqs, dgq, dgk, workspace=ws)
         for _ in range(3):
             run()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -348,10 +379,14 @@ def train_bench(args, torch, F, synth, kernels, Module):
         e1.record()
         torch.cuda.synchronize()
         bwd_ms = e0.elapsed_time(e1) / args.steps
-    fl_bwd = 2.5 * attention_core_flops(B, T, H, d)
+    fl_bwd = 2.5 * 4 * d * pairs * B * H
     peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
     ach = fl_bwd / (bwd_ms * 1e-3) / 1e12
     ms = wall * 1e3 / args.steps
+    path = (f"{args.mode} mode, mask {args.mask}: exact path" if exact else "causal + tril")
+    kern = ("holo_attn_masked_bwd (bwd_prep + attn_bwd_masked_dkdv + attn_bwd_masked_dq"
+            + (" + hol_torque" if args.mode == "causal" else "") + " + link_bwd)") if exact else \
+        "holo_attn_bwd (bwd_prep + attn_bwd_dkdv + attn_bwd_dq + link_bwd)"
     return {"metric": f"training step tokens/s (forward + backward of one layer, {args.config})",
             "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
@@ -359,13 +394,14 @@ def train_bench(args, torch, F, synth, kernels, Module):
             "data": "synthetic (seeded SplitMix64/Box-Muller: x ~ N(0,1), weights ~ N(0,1/d_model); dy from "
                     "torch.randn seeded 3)",
             "config": {"workload": f"{args.config}: one layer forward + backward (all weight and input "
-                                   f"gradients)", "global_batch": B, "seq_len": T, "n_heads": H, "d_head": d,
-                       "d_model": D, "link_mode": "additive", "edge_scale": es, "parallelism": "single GPU"},
+                                   f"gradients), {path}", "global_batch": B, "seq_len": T, "n_heads": H,
+                       "d_head": d, "d_model": D, "link_mode": "additive", "edge_scale": es,
+                       "mode": args.mode, "mask": args.mask, "parallelism": "single GPU"},
             "fused_backward_ms": bwd_ms,
-            "roofline": {"kernel": "holo_attn_bwd (bwd_prep + attn_bwd_dkdv + attn_bwd_dq + link_bwd)",
-                         "bound": "mfma", "achieved": ach, "peak": peak, "unit": "TFLOP/s", "frac": ach / peak,
-                         "traffic": None,
-                         "work_per_launch": f"{fl_bwd:.4e} FLOP = 2.5 * 2*d*T*(T+1)*B*H"},
+            "roofline": {"kernel": kern, "bound": "mfma", "achieved": ach, "peak": peak, "unit": "TFLOP/s",
+                         "frac": ach / peak, "traffic": None,
+                         "work_per_launch": f"{fl_bwd:.4e} FLOP = 2.5 * 4*d*pairs*B*H ({pairs} allowed pairs "
+                                            f"per (b, h))"},
             "cpu_baseline": None}
 
 
@@ -509,9 +545,26 @@ def main():
                     help="attention mode (inert runs the exact-path kernels with any mask)")
     ap.add_argument("--train", action="store_true",
                     help="forward + backward of one layer at --config (one JSON line) and exit")
+    ap.add_argument("--fused-interaction", action="store_true",
+                    help="with --link interaction: the edge MLP on the hand-written GEMM (the module's "
+                         "fused_interaction option, off by default: run so far only on the CPU emulation)")
+    ap.add_argument("--exact-backward", action="store_true",
+                    help="with --train and --mask none|ring or --mode inert: the exact path's backward (the "
+                         "module's exact_backward option, off by default: run so far only on the CPU emulation)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSVs under DIR(s) as JSON and exit")
     args = ap.parse_args()
+    if args.fused_interaction and args.link != "interaction":
+        print("bench.py: --fused-interaction needs --link interaction", file=sys.stderr)
+        sys.exit(2)
+    off_tril = args.mask != "tril" or args.mode != "causal"
+    if args.train and off_tril and not args.exact_backward:
+        print("bench.py: --train with a mask other than tril or inert mode needs --exact-backward "
+              "(without it the module's backward for these calls raises)", file=sys.stderr)
+        sys.exit(2)
+    if args.exact_backward and not (args.train and off_tril):
+        print("bench.py: --exact-backward applies to --train with --mask none|ring or --mode inert", file=sys.stderr)
+        sys.exit(2)
     if args.pmc_summary:
         print(json.dumps(pmc_summary(args.pmc_summary), indent=1))
         return
@@ -547,6 +600,7 @@ def main():
     x_np = inp.pop("x")
     m = PathOrderedGeometricMHA(D, n_heads=H, edge_scale=es, mode=args.mode)
     m.link_mode = args.link
+    m.fused_interaction = args.fused_interaction
     with torch.no_grad():
         for k, p in m.state_dict().items():
             if k in inp:
@@ -556,17 +610,7 @@ def main():
     if args.ortho:
         print(json.dumps(orthogonality_report(m, x, args.config, kernels, torch)))
         return
-    if args.mask == "tril":
-        mask = torch.ones(T, T, dtype=torch.bool, device=dev).tril()
-        pairs = T * (T + 1) // 2
-    elif args.mask == "ring":
-        i = torch.arange(T, device=dev)
-        mask = torch.zeros(T, T, dtype=torch.bool, device=dev)
-        for off in (-1, 0, 1):
-            mask[i, (i + off) % T] = True
-        pairs = int(mask.sum())
-    else:
-        mask, pairs = None, T * T
+    mask, pairs = layer_mask(args.mask, T, torch, dev)
     exact = not m._tril_path(mask, T)
 
     pfmt = m._p_format(x, False)
@@ -645,7 +689,7 @@ def main():
         "config": {"workload": f"{args.config}: one path-ordered attention layer forward"
                                + (f" ({args.mode} mode, mask {args.mask}: exact-path kernels)" if exact else ""),
                    "global_batch": B, "seq_len": T, "n_heads": H, "d_head": d, "d_model": D,
-                   "rotation": f"{d // 3} SO(3) blocks per head", "link_mode": args.link,
+                   "rotation": f"{d // 3} SO(3) blocks per head", "link_mode": args.link, "fused_interaction": args.fused_interaction,
                    "mode": args.mode, "mask": args.mask,
                    "attention_operands": ("bf16" if exact else "fp16") if dt == torch.bfloat16 else "fp32",
                    "edge_scale": es, "parallelism": "single GPU"},

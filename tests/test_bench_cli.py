@@ -16,6 +16,18 @@ def test_multi_gpu_request_exits_with_message():
     assert r.stdout == ""
 
 
+def test_contradictory_options_exit_before_any_gpu_work():
+    """--fused-interaction needs the interaction generator; training off the
+    tril path needs --exact-backward, which applies to nothing else."""
+    for argv, needle in ((["--fused-interaction"], "--link interaction"),
+                         (["--train", "--mask", "ring"], "--exact-backward"),
+                         (["--train", "--mode", "inert"], "--exact-backward"),
+                         (["--exact-backward"], "applies to --train")):
+        r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), *argv],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 2 and needle in r.stderr and r.stdout == "", (argv, r.stderr)
+
+
 def test_traffic_is_reported_only_for_the_profiled_machine_code(monkeypatch):
     """roofline.traffic comes from the committed counter profile only when
     every profiled kernel it sums has, in the loaded library, the instruction
