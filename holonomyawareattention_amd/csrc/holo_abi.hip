@@ -538,10 +538,10 @@ size_t masked_bwd_layout(int B, int64_t T, int H, int d, size_t es, int mode, bo
   }
   if (a) {
     a->mask_bits = reinterpret_cast<const uint64_t*>(bits);
+    a->tile_act = reinterpret_cast<const uint8_t*>(act);
     a->qw = r[0]; a->dow = r[1]; a->qw_t = r[2]; a->dow_t = r[3];
     a->dqw = g[0]; a->dkw = g[1]; a->dvw = g[2]; a->hol_torque = g[3];
   }
-  (void)act;
   return off;
 }
 
@@ -615,9 +615,8 @@ int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edg
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
   if (mask) {
-    uint64_t* bits = const_cast<uint64_t*>(a.mask_bits);
-    uint8_t* act = reinterpret_cast<uint8_t*>(bits) + ((size_t)a.Tp * (a.Tp / 64) * 8 + 255) / 256 * 256;
-    e = holo::launch_pack_mask(mask, mask_rs, T, a.Tp, bits, act, s);
+    e = holo::launch_pack_mask(mask, mask_rs, T, a.Tp, const_cast<uint64_t*>(a.mask_bits),
+                               const_cast<uint8_t*>(a.tile_act), s);
     if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "mask packing launch: %s", hipGetErrorString(e));
   }
   e = io_dtype == HOLO_F32 ? holo::launch_masked_bwd<float, float>(a, s)

@@ -41,6 +41,7 @@ namespace holo {
 // torque) and its dQ (in the frame of qw, rotated back by Hol in link_bwd)
 // are also stored apart.
 enum : int { kRelBase = 0, kRelWrap = 1, kRelAll = 2 };
+constexpr int kMapRows = 128;        // query rows per tile of the open-tile map (mask_tiles)
 
 template <typename T, int DP, bool WRAP>
 __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1)))
@@ -118,13 +119,28 @@ attn_bwd_masked_dkdv(MaskedBwdArgs a) {
       if (tid < kFillKV) { lse_s[tid] = ls; del_s[tid] = dl; }
       if (tid < 2 * kFillKV) mw_s[tid >> 1][tid & 1] = mwr;
     };
+    // the first fill at or after qf that the mask opens for the workgroup's
+    // keys (the map of open (128-query, 64-key) tiles; every thread reads the
+    // same bytes, so the walk is uniform)
+    auto open_from = [&](int qf) {
+      if (a.tile_act == nullptr) return qf;
+      const int64_t kt0 = k0 / 64;
+      for (; qf < f1; ++qf) {
+        const int64_t row = (int64_t)qf * kFillKV / kMapRows * nw;
+        if (a.tile_act[row + kt0] != 0 || (kt0 + 1 < nw && a.tile_act[row + kt0 + 1] != 0)) break;
+      }
+      return qf;
+    };
+    const int first = open_from(f0);
+    if (first >= f1) return;                // uniform: no open pair in this sweep
     __syncthreads();                        // the previous sweep is done with the tiles
-    load_fill(f0);
+    load_fill(first);
     store_fill();
     __syncthreads();
-    for (int qf = f0; qf < f1; ++qf) {
+    for (int qf = first; qf < f1;) {
       const int64_t q0 = (int64_t)qf * kFillKV;
-      if (qf + 1 < f1) load_fill(qf + 1);
+      const int nxt = open_from(qf + 1);
+      if (nxt < f1) load_fill(nxt);
       static_for<kFillKV / kBT>([&](auto sub) {
         const int64_t qs0 = q0 + kBT * sub;
         if (!wave_in) return;
@@ -189,8 +205,9 @@ attn_bwd_masked_dkdv(MaskedBwdArgs a) {
         }
       });
       __syncthreads();                      // every wave is done with this fill
-      if (qf + 1 < f1) store_fill();
+      if (nxt < f1) store_fill();
       __syncthreads();
+      qf = nxt;
     }
   };
   auto store = [&](float* dk, float* dv) {
@@ -263,6 +280,9 @@ attn_bwd_masked_dq(MaskedBwdArgs a) {
     const int f0 = (int)(klo / kFill), f1 = (int)((khi + kFill - 1) / kFill);
     for (int kfi = f0; kfi < f1; ++kfi) {
       const int64_t k0 = (int64_t)kfi * kFill;
+      // a fill the mask closes for all of the workgroup's queries (the map of
+      // open (128-query, 64-key) tiles; the same byte for every thread)
+      if (a.tile_act != nullptr && a.tile_act[qb * nw + kfi] == 0) continue;
       {
         u32x4 r[M::IT];
         const T* const rows[2] = {reinterpret_cast<const T*>(a.kh) + (bh * a.Tp + k0) * DP,

@@ -92,6 +92,7 @@ struct MaskedBwdArgs : BwdArgs {
   int mode;                              // 0 causal (wrap through hol), 1 inert
   const float* hol;                      // (B, H, nb, 4) holonomy quaternions (causal)
   const uint64_t* mask_bits;             // (Tp, Tp/64) as for MaskedArgs; null = every pair
+  const uint8_t* tile_act;               // (ceil(T/128), Tp/64) open-tile map as for MaskedArgs; null = all
   void* qw; void* dow;                   // Hol^T qh, Hol^T doh (io dtype, (B, H, Tp, Dp); causal)
   void* qw_t; void* dow_t;               // their transposed tiles (fp32 only)
   float* dqw; float* dkw; float* dvw;    // wrap-branch gradients, path frame (fp32, causal)
