@@ -98,20 +98,23 @@ def build_library(verbose: bool = False) -> str:
 
 C_SMOKE_SRC = os.path.join(REPO, "tests", "c", "abi_smoke.c")
 C_EXAMPLE_SRC = os.path.join(REPO, "tests", "c", "integration_example.c")
+C_TRAIN_EXAMPLE_SRC = os.path.join(REPO, "tests", "c", "exact_train_example.c")
 C_SMOKE_BIN = os.path.join(PKG, "_build", "abi_smoke")
 
 
 def build_c_smoke() -> str:
     """Compile the C caller of the ABI (tests/c/abi_smoke.c, which also calls
-    the documented C binding example, tests/c/integration_example.c) with gcc
-    against the HIP runtime and this library (no PyTorch); returns the
-    binary's path. A stale signature in either fails here."""
+    the documented C binding example, tests/c/integration_example.c, and
+    links the exact path's training example, tests/c/exact_train_example.c)
+    with gcc against the HIP runtime and this library (no PyTorch); returns
+    the binary's path. A stale signature in any of them fails here."""
     os.makedirs(os.path.dirname(C_SMOKE_BIN), exist_ok=True)
     cc = shutil.which("gcc") or shutil.which("cc")
     if cc is None:
         raise RuntimeError("no C compiler found for the ABI smoke driver")
     cmd = [cc, "-std=c99", "-O2", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
-           "-I/opt/rocm/include", "-I", os.path.join(REPO, "include"), C_SMOKE_SRC, C_EXAMPLE_SRC, "-o", C_SMOKE_BIN,
+           "-I/opt/rocm/include", "-I", os.path.join(REPO, "include"), C_SMOKE_SRC, C_EXAMPLE_SRC,
+           C_TRAIN_EXAMPLE_SRC, "-o", C_SMOKE_BIN,
            "-L", PKG, "-lholo_mi355x", "-L/opt/rocm/lib", "-lamdhip64", "-lm", "-Wl,-rpath," + PKG,
            "-Wl,-rpath,$ORIGIN/.."]
     r = subprocess.run(cmd, capture_output=True, text=True)
