@@ -308,7 +308,10 @@ def train_bench(args, torch, F, synth, kernels, Module):
     through the module's autograd path, and the backward timed alone on the
     saved forward state: the fused backward (holo_attn_bwd) for causal + tril,
     or with --exact-backward the exact path's (holo_attn_masked_bwd) for
-    --mask none|ring or --mode inert. The backward attention's algorithmic
+    --mask none|ring or --mode inert; --dropout P (with --exact-backward, any
+    mask) trains with attention dropout on the exact path's dropout pair
+    (holo_attn_masked_dropout_fwd / _bwd), as the reference's kernel module
+    sends such steps to its exact path. The backward attention's algorithmic
     work is 2.5x the forward's (recomputed QK^T, dP, dV, dK, dQ) over the
     pairs the mask allows."""
     cfg = CONFIGS[args.config]
@@ -318,7 +321,7 @@ def train_bench(args, torch, F, synth, kernels, Module):
     dev = torch.device("cuda:0")
     inp = synth.layer_inputs(2, B, T, D, H, "additive")
     x = torch.as_tensor(inp.pop("x")).to(dev, dt)
-    m = Module(D, n_heads=H, edge_scale=es, mode=args.mode)
+    m = Module(D, n_heads=H, edge_scale=es, mode=args.mode, dropout=args.dropout)
     m.link_mode = "additive"
     m.exact_backward = args.exact_backward
     with torch.no_grad():
@@ -355,13 +358,16 @@ def train_bench(args, torch, F, synth, kernels, Module):
         if exact:
             qh, kh, vh_t, P, hol = kernels.geom_scan(q, k, v, gq, gk, es, want_hol=args.mode == "causal",
                                                      p_format="f32", mode=args.mode)
-            o, lse = kernels.attention_masked_train(qh, kh, vh_t, P, hol, d, m.scale, mode=args.mode, mask=mask)
+            drop = dict(dropout_p=args.dropout, seed=0x5EED, offset=0)
+            o, lse = kernels.attention_masked_train(qh, kh, vh_t, P, hol, d, m.scale, mode=args.mode, mask=mask,
+                                                    **drop)
             ws = torch.empty(int(lib.holo_attn_masked_bwd_workspace_size(B, T, H, d, kernels._DT[dt],
                                                                           kernels._MODE[args.mode],
                                                                           int(mask is not None))),
                              dtype=torch.uint8, device=dev)
             run = lambda: kernels.attention_masked_backward(gq, gk, es, qh, kh, vh_t, P, hol, lse, o, do, d, m.scale,
-                                                            *dqs, dgq, dgk, mode=args.mode, mask=mask, workspace=ws)
+                                                            *dqs, dgq, dgk, mode=args.mode, mask=mask, workspace=ws,
+                                                            **drop)
         else:
             qh, kh, vh_t, P, _ = kernels.geom_scan(q, k, v, gq, gk, es, p_format="f32")
             lse = torch.empty((B, H, qh.shape[2]), dtype=torch.float32, device=dev)
@@ -384,7 +390,10 @@ def train_bench(args, torch, F, synth, kernels, Module):
     ach = fl_bwd / (bwd_ms * 1e-3) / 1e12
     ms = wall * 1e3 / args.steps
     path = (f"{args.mode} mode, mask {args.mask}: exact path" if exact else "causal + tril")
-    kern = ("holo_attn_masked_bwd (bwd_prep + attn_bwd_masked_dkdv + attn_bwd_masked_dq"
+    if args.dropout > 0:
+        path += f", attention dropout p = {args.dropout}"
+    kern = (("holo_attn_masked_dropout_bwd" if args.dropout > 0 else "holo_attn_masked_bwd")
+            + " (bwd_prep + attn_bwd_masked_dkdv + attn_bwd_masked_dq"
             + (" + hol_torque" if args.mode == "causal" else "") + " + link_bwd)") if exact else \
         "holo_attn_bwd (bwd_prep + attn_bwd_dkdv + attn_bwd_dq + link_bwd)"
     return {"metric": f"training step tokens/s (forward + backward of one layer, {args.config})",
@@ -396,7 +405,8 @@ def train_bench(args, torch, F, synth, kernels, Module):
             "config": {"workload": f"{args.config}: one layer forward + backward (all weight and input "
                                    f"gradients), {path}", "global_batch": B, "seq_len": T, "n_heads": H,
                        "d_head": d, "d_model": D, "link_mode": "additive", "edge_scale": es,
-                       "mode": args.mode, "mask": args.mask, "parallelism": "single GPU"},
+                       "mode": args.mode, "mask": args.mask, "dropout": args.dropout,
+                       "parallelism": "single GPU"},
             "fused_backward_ms": bwd_ms,
             "roofline": {"kernel": kern, "bound": "mfma", "achieved": ach, "peak": peak, "unit": "TFLOP/s",
                          "frac": ach / peak, "traffic": None,
@@ -551,19 +561,26 @@ def main():
     ap.add_argument("--exact-backward", action="store_true",
                     help="with --train and --mask none|ring or --mode inert: the exact path's backward (the "
                          "module's exact_backward option, off by default: run so far only on the CPU emulation)")
+    ap.add_argument("--dropout", type=float, default=0.0,
+                    help="with --train and --exact-backward: attention dropout probability of the layer (the "
+                         "exact path's dropout kernels, run so far only on the CPU emulation; any --mask)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc CSVs under DIR(s) as JSON and exit")
     args = ap.parse_args()
     if args.fused_interaction and args.link != "interaction":
         print("bench.py: --fused-interaction needs --link interaction", file=sys.stderr)
         sys.exit(2)
-    off_tril = args.mask != "tril" or args.mode != "causal"
+    if not (0.0 <= args.dropout < 1.0) or (args.dropout > 0 and not (args.train and args.exact_backward)):
+        print("bench.py: --dropout takes 0 <= P < 1 and applies to --train with --exact-backward", file=sys.stderr)
+        sys.exit(2)
+    off_tril = args.mask != "tril" or args.mode != "causal" or args.dropout > 0
     if args.train and off_tril and not args.exact_backward:
         print("bench.py: --train with a mask other than tril or inert mode needs --exact-backward "
               "(without it the module's backward for these calls raises)", file=sys.stderr)
         sys.exit(2)
     if args.exact_backward and not (args.train and off_tril):
-        print("bench.py: --exact-backward applies to --train with --mask none|ring or --mode inert", file=sys.stderr)
+        print("bench.py: --exact-backward applies to --train with --mask none|ring, --mode inert or --dropout",
+              file=sys.stderr)
         sys.exit(2)
     if args.pmc_summary:
         print(json.dumps(pmc_summary(args.pmc_summary), indent=1))

@@ -43,6 +43,8 @@ _I = ctypes.c_int
 _L = ctypes.c_int64
 _F = ctypes.c_float
 _S = ctypes.c_size_t
+_U64 = ctypes.c_uint64
+_U32 = ctypes.c_uint32
 SIGNATURES = [
     ("holo_last_error", ctypes.c_char_p, []),
     ("holo_abi_version", _I, []),
@@ -81,6 +83,16 @@ SIGNATURES = [
                                   _P, _L, _L, _P, _L, _L, _P, _L, _L,
                                   _P, _L, _L, _P, _L, _L,
                                   _P, _S, _P]),
+    ("holo_attn_masked_dropout_fwd", _I, [_I, _L, _I, _I, _I, _I, _F, _F, _U64, _U32, _P, _P, _P, _P, _P, _P, _L,
+                                          _P, _L, _L, _P, _P, _S, _P]),
+    ("holo_attn_masked_dropout_bwd", _I, [_I, _L, _I, _I, _I, _F, _I, _I, _I, _F, _F, _U64, _U32,
+                                          _P, _L, _L, _P, _L, _L,
+                                          _P, _P, _P, _P, _P, _P, _P, _L,
+                                          _P, _L, _L, _P, _L, _L,
+                                          _P, _L, _L, _P, _L, _L, _P, _L, _L,
+                                          _P, _L, _L, _P, _L, _L,
+                                          _P, _S, _P]),
+    ("holo_dropout_keep_mask", _I, [_I, _L, _I, _F, _U64, _U32, _P, _P]),
     ("holo_quat_to_dense", _I, [_L, _I, _P, _P, _P]),
     ("holo_add_layernorm_fwd", _I, [_L, _I, _I, _F, _P, _L, _P, _L, _P, _P, _P, _L, _P, _L, _P]),
     ("holo_decode_geom_fwd", _I, [_I, _I, _I, _L, _L, _I, _F, _I, _I,

@@ -24,8 +24,10 @@ Dispatch follows the reference's kernel module (kernel/attention_kernel.py:
 kernels (holo_attn_fwd; return_geometry is also supported); every other call
 -- no mask, the ring mask or any (L, L) boolean mask, inert mode -- runs the
 exact-path kernels (holo_attn_masked_fwd), where the reference falls back to
-kernel/attention_fast.py. Both need x on the GPU and dropout inactive;
-anything else raises NotImplementedError (there is no CPU path).
+kernel/attention_fast.py. Both need x on the GPU; active attention dropout
+(training, dropout > 0) runs on the exact path's dropout kernels when
+exact_backward is on and raises otherwise; anything else unsupported raises
+NotImplementedError (there is no CPU path).
 Under autograd the projections are ordinary differentiable torch GEMMs and the
 scan + attention core is one autograd function whose backward is the gfx950
 backward (holo_attn_bwd; the reference recomputes its forward under autograd,
@@ -159,24 +161,28 @@ class _ExactPathAttention(torch.autograd.Function):
     and the fp32 generator output g (layouts of _PathAttention): geom_scan in
     the call's mode + holo_attn_masked_train_fwd. Backward:
     holo_attn_masked_bwd, returning dqkv and dg (the closing edge's share of
-    dg included in causal mode)."""
+    dg included in causal mode). drop = (p, seed) applies attention dropout
+    (holo_attn_masked_dropout_fwd / _bwd, the keep mask regenerated from the
+    seed in the backward); None = no dropout."""
 
     @staticmethod
-    def forward(ctx, qkv, g, edge_scale, scale, additive, d, mask, mode):
+    def forward(ctx, qkv, g, edge_scale, scale, additive, d, mask, mode, drop=None):
         B, L, H, _ = qkv.shape
         m = 3 * (d // 3)
+        p, seed = drop if drop is not None else (0.0, 0)
         gq, gk = _PathAttention._gviews(g, B, L, H, m, additive)
         qh, kh, vh_t, P, hol = kernels.geom_scan(qkv[..., :d], qkv[..., d:2 * d], qkv[..., 2 * d:], gq, gk,
                                                  edge_scale, want_hol=mode == "causal", p_format="f32", mode=mode)
-        o, lse = kernels.attention_masked_train(qh, kh, vh_t, P, hol, d, scale, mode=mode, mask=mask)
+        o, lse = kernels.attention_masked_train(qh, kh, vh_t, P, hol, d, scale, mode=mode, mask=mask,
+                                                dropout_p=p, seed=seed)
         ctx.save_for_backward(g, qh, kh, vh_t, P, hol, lse, o, mask)
-        ctx.cfg = (edge_scale, scale, additive, d, H, m, tuple(qkv.shape), mode)
+        ctx.cfg = (edge_scale, scale, additive, d, H, m, tuple(qkv.shape), mode, p, seed)
         return o
 
     @staticmethod
     def backward(ctx, do):
         g, qh, kh, vh_t, P, hol, lse, o, mask = ctx.saved_tensors
-        es, scale, additive, d, H, m, shp, mode = ctx.cfg
+        es, scale, additive, d, H, m, shp, mode, p, seed = ctx.cfg
         B, L = shp[0], shp[1]
         dqkv = torch.empty(shp, dtype=o.dtype, device=o.device)
         dg = torch.empty_like(g)
@@ -184,8 +190,8 @@ class _ExactPathAttention(torch.autograd.Function):
         dgq, dgk = _PathAttention._gviews(dg, B, L, H, m, additive)
         kernels.attention_masked_backward(gq, gk, es, qh, kh, vh_t, P, hol, lse, o, do.contiguous(), d, scale,
                                           dqkv[..., :d], dqkv[..., d:2 * d], dqkv[..., 2 * d:], dgq, dgk,
-                                          mode=mode, mask=mask)
-        return dqkv, dg, None, None, None, None, None, None
+                                          mode=mode, mask=mask, dropout_p=p, seed=seed)
+        return dqkv, dg, None, None, None, None, None, None, None
 
 
 class PathOrderedGeometricMHA(nn.Module):
@@ -229,8 +235,10 @@ class PathOrderedGeometricMHA(nn.Module):
         # only, never on a GPU. exact_backward: under autograd, calls off the
         # causal + tril path (any other mask, inert mode) run a
         # differentiable exact path (holo_attn_masked_train_fwd and
-        # holo_attn_masked_bwd) instead of a forward whose backward raises;
-        # off by default for the same reason.
+        # holo_attn_masked_bwd) instead of a forward whose backward raises,
+        # and active attention dropout (training, dropout.p > 0) runs there
+        # (holo_attn_masked_dropout_fwd / _bwd) as the reference's exact path
+        # applies it, instead of raising; off by default for the same reason.
         self.fp16_operands = True
         self.check_status = False
         self.fused_interaction = False
@@ -247,8 +255,9 @@ class PathOrderedGeometricMHA(nn.Module):
     def _unsupported_reason(self, x, attn_mask, causal_implied: bool = False) -> Optional[str]:
         if not x.is_cuda:
             return "input is not on the GPU"
-        if self.dropout.p != 0.0 and self.training:
-            return "attention dropout is active (the kernels apply none)"
+        if self._dropout_active() and not getattr(self, "exact_backward", False):
+            return ("attention dropout is active (the exact path's dropout kernels run it when exact_backward "
+                    "is on)")
         if x.dtype not in (torch.float32, torch.bfloat16):
             return f"dtype {x.dtype} (float32 and bfloat16 are supported)"
         if self.link_mode not in ("additive", "interaction"):
@@ -259,6 +268,10 @@ class PathOrderedGeometricMHA(nn.Module):
         if attn_mask is not None and (tuple(attn_mask.shape) != (L, L) or attn_mask.device != x.device):
             return f"attn_mask must be an ({L}, {L}) tensor on {x.device}"
         return None
+
+    def _dropout_active(self) -> bool:
+        """nn.Dropout(p) on the attention weights acts: training and p > 0."""
+        return self.training and self.dropout.p != 0.0
 
     def _tril_path(self, attn_mask, L: int) -> bool:
         """causal mode with attn_mask exactly tril(L): the reference's kernel
@@ -415,12 +428,13 @@ class PathOrderedGeometricMHA(nn.Module):
             g = g + lin2.bias.float()
         return g
 
-    def _forward_autograd(self, x: torch.Tensor, exact_mask: Optional[Tuple[Optional[torch.Tensor]]] = None
-                          ) -> torch.Tensor:
+    def _forward_autograd(self, x: torch.Tensor, exact_mask: Optional[Tuple[Optional[torch.Tensor]]] = None,
+                          drop: Optional[Tuple[float, int]] = None) -> torch.Tensor:
         """Differentiable forward: torch GEMMs for the projections and the
         generator, _PathAttention for the core (causal + tril) or, with
         exact_mask = (attn_mask,), _ExactPathAttention (the exact path in the
-        module's mode, attn_mask None = every pair)."""
+        module's mode, attn_mask None = every pair; drop = (p, seed): with
+        attention dropout)."""
         B, L, D = x.shape
         H, d, m = self.h, self.d, self.m_dim
         qkv = F.linear(x, self.qkv.weight).view(B, L, H, 3 * d)
@@ -434,7 +448,7 @@ class PathOrderedGeometricMHA(nn.Module):
         if exact_mask is not None:
             mask = exact_mask[0]
             mask = None if mask is None else mask.detach().to(torch.bool)
-            o = _ExactPathAttention.apply(qkv, g, self.edge_scale, self.scale, additive, d, mask, self.mode)
+            o = _ExactPathAttention.apply(qkv, g, self.edge_scale, self.scale, additive, d, mask, self.mode, drop)
         else:
             o = _PathAttention.apply(qkv, g, self.edge_scale, self.scale, additive, d)
         return F.linear(o.reshape(B, L, D), self.out.weight)
@@ -488,6 +502,8 @@ class PathOrderedGeometricMHA(nn.Module):
             raise NotImplementedError(
                 f"holonomyawareattention_amd kernel path does not support this call: {reason}")
         B, L, D = x.shape
+        if self._dropout_active():
+            return self._forward_dropout(x, attn_mask, return_geometry)
         tril = self._tril_path(attn_mask, L)
         params = [p for p in self.parameters() if p.requires_grad]
         track = torch.is_grad_enabled() and (x.requires_grad or bool(params))
@@ -509,6 +525,30 @@ class PathOrderedGeometricMHA(nn.Module):
         if not tril:
             return self._forward_exact(x, attn_mask, return_geometry)
         return self._forward_kernels(x, return_geometry)
+
+    def _forward_dropout(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor], return_geometry: bool
+                         ) -> Tuple[torch.Tensor, Optional[Dict[str, torch.Tensor]]]:
+        """Active attention dropout (exact_backward on): as the reference's
+        kernel module sends such calls to its exact path
+        (kernel/attention_kernel.py:203-213 -> kernel/attention_fast.py:160),
+        every mask -- tril(L) included -- runs the exact path's differentiable
+        pair with dropout (holo_attn_masked_dropout_fwd / _bwd). The keep mask
+        comes from a fresh 64-bit seed drawn from torch's default CPU
+        generator (so torch.manual_seed makes it repeatable) and is
+        regenerated by the backward. The geometry output (return_geometry)
+        does not depend on dropout; it comes from a separate forward without
+        gradients, as elsewhere."""
+        seed = int(torch.randint(0, 2 ** 63 - 1, (), dtype=torch.int64).item())
+        y = self._forward_autograd(x, exact_mask=(attn_mask,), drop=(float(self.dropout.p), seed))
+        if not return_geometry:
+            return y, None
+        with torch.no_grad():
+            _, geo = self._forward_exact(x, attn_mask, True)
+        params = [p for p in self.parameters() if p.requires_grad]
+        if torch.is_grad_enabled() and (x.requires_grad or bool(params)):
+            C, Hm = _ForwardOnly.apply("the geometry output", 2, geo["C"], geo["H"], x, *params)
+            geo = {"C": C, "H": Hm}
+        return y, geo
 
     def _forward_kernels(self, x: torch.Tensor, return_geometry: bool
                          ) -> Tuple[torch.Tensor, Optional[Dict[str, torch.Tensor]]]:

@@ -1,6 +1,7 @@
 // C ABI of the gfx950 path-ordered attention forward (include/holo_mi355x.h):
 // argument validation, status codes and kernel launches. Nothing here
 // allocates device memory or synchronises the host.
+#include <cmath>
 #include <cstdio>
 #include <cstdarg>
 #include <mutex>
@@ -86,7 +87,7 @@ extern "C" {
 
 const char* holo_last_error(void) { return g_last_error.c_str(); }
 
-int holo_abi_version(void) { return (6 << 16) | 2; }
+int holo_abi_version(void) { return (6 << 16) | 3; }
 
 int holo_padded_head_dim(int d) { return holo::padded_head_dim(d); }
 
@@ -358,13 +359,28 @@ size_t holo_attn_masked_workspace_size(int B, int64_t T, int H, int d, int dtype
 
 namespace {
 
+// Attention dropout's parameters from the drop probability p (0 <= p < 1),
+// the 64-bit seed and the counter offset: keep a pair when its Philox word
+// is >= round(p 2^32) (ties to even; capped at 2^32 - 1), scale kept weights
+// by 1 / (1 - p).
+int drop_params(float p, uint64_t seed, uint32_t offset, holo::DropParams& d) {
+  if (!(p >= 0.f && p < 1.f)) return fail(HOLO_ERR_INVALID_ARG, "dropout probability %g is not in [0, 1)", (double)p);
+  const double t = std::nearbyint((double)p * 4294967296.0);
+  d.thr = t >= 4294967295.0 ? 0xffffffffu : (uint32_t)t;
+  d.scale = 1.f / (1.f - p);
+  d.k0 = (uint32_t)seed;
+  d.k1 = (uint32_t)(seed >> 32);
+  d.offset = offset;
+  return HOLO_OK;
+}
+
 // holo_attn_masked_fwd's checks and launch; lse non-null selects the
-// training forward (fp32 quaternions, the per-row LSE written)
+// training forward (fp32 quaternions, the per-row LSE written), drop
+// non-null (with lse) its attention dropout
 int masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, int mode, float scale,
                const void* qh, const void* kh, const void* vh_t, const void* P, const float* hol,
                const uint8_t* mask, int64_t mask_rs, void* o, int64_t o_rs, int64_t o_hs, float* lse,
-               void* workspace, size_t workspace_bytes, void* stream) {
-  g_last_error.clear();
+               void* workspace, size_t workspace_bytes, void* stream, const holo::DropParams* drop = nullptr) {
   int rc = check_common(B, T, H, d);
   if (rc) return rc;
   if (dtype != HOLO_F32 && dtype != HOLO_BF16)
@@ -401,6 +417,8 @@ int masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format, int mode
   a.o = o; a.o_rs = o_rs; a.o_hs = o_hs;
   a.p_format = p_format;
   a.lse = lse;
+  a.dropout = drop != nullptr;
+  a.drop = drop ? *drop : holo::DropParams{0u, 1.f, 0u, 0u, 0u};
   char* ws = static_cast<char*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
@@ -429,6 +447,7 @@ int holo_attn_masked_fwd(int B, int64_t T, int H, int d, int dtype, int p_format
                          const uint8_t* mask, int64_t mask_rs,
                          void* o, int64_t o_rs, int64_t o_hs,
                          void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
   return masked_fwd(B, T, H, d, dtype, p_format, mode, scale, qh, kh, vh_t, P, hol, mask, mask_rs, o, o_rs, o_hs,
                     nullptr, workspace, workspace_bytes, stream);
 }
@@ -438,12 +457,38 @@ int holo_attn_masked_train_fwd(int B, int64_t T, int H, int d, int dtype, int mo
                                const uint8_t* mask, int64_t mask_rs,
                                void* o, int64_t o_rs, int64_t o_hs, float* lse,
                                void* workspace, size_t workspace_bytes, void* stream) {
-  if (!lse) {
-    g_last_error.clear();
-    return fail(HOLO_ERR_INVALID_ARG, "null lse");
-  }
+  g_last_error.clear();
+  if (!lse) return fail(HOLO_ERR_INVALID_ARG, "null lse");
   return masked_fwd(B, T, H, d, dtype, HOLO_QUAT_F32, mode, scale, qh, kh, vh_t, P, hol, mask, mask_rs, o, o_rs,
                     o_hs, lse, workspace, workspace_bytes, stream);
+}
+
+int holo_attn_masked_dropout_fwd(int B, int64_t T, int H, int d, int dtype, int mode, float scale,
+                                 float dropout_p, uint64_t seed, uint32_t offset,
+                                 const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
+                                 const uint8_t* mask, int64_t mask_rs,
+                                 void* o, int64_t o_rs, int64_t o_hs, float* lse,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (!lse) return fail(HOLO_ERR_INVALID_ARG, "null lse");
+  holo::DropParams dp;
+  const int rc = drop_params(dropout_p, seed, offset, dp);
+  if (rc) return rc;
+  return masked_fwd(B, T, H, d, dtype, HOLO_QUAT_F32, mode, scale, qh, kh, vh_t, P, hol, mask, mask_rs, o, o_rs,
+                    o_hs, lse, workspace, workspace_bytes, stream, &dp);
+}
+
+int holo_dropout_keep_mask(int B, int64_t T, int H, float dropout_p, uint64_t seed, uint32_t offset, uint8_t* keep,
+                           void* stream) {
+  g_last_error.clear();
+  int rc = check_common(B, T, H, 3);
+  if (rc) return rc;
+  if (!keep) return fail(HOLO_ERR_INVALID_ARG, "null keep");
+  holo::DropParams dp;
+  if ((rc = drop_params(dropout_p, seed, offset, dp))) return rc;
+  const hipError_t e = holo::launch_dropout_keep(B, H, T, dp, keep, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "dropout mask launch: %s", hipGetErrorString(e));
+  return HOLO_OK;
 }
 
 size_t holo_attn_bwd_workspace_size(int B, int64_t T, int H, int d, int dtype) {
@@ -583,8 +628,14 @@ size_t holo_attn_masked_bwd_workspace_size(int B, int64_t T, int H, int d, int d
   return masked_bwd_layout(B, T, H, d, dtype == HOLO_F32 ? 4 : 2, mode, has_mask != 0, nullptr, nullptr);
 }
 
-int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
-                         int mode, float scale,
+}  // extern "C"
+
+namespace {
+
+// holo_attn_masked_bwd's checks and launch; drop non-null: the forward's
+// attention dropout
+int masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+               int mode, float scale,
                          const void* gq, int64_t gq_rs, int64_t gq_hs, const void* gk, int64_t gk_rs, int64_t gk_hs,
                          const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
                          const float* lse, const uint8_t* mask, int64_t mask_rs,
@@ -592,7 +643,7 @@ int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edg
                          void* dq, int64_t dq_rs, int64_t dq_hs, void* dk, int64_t dk_rs, int64_t dk_hs,
                          void* dv, int64_t dv_rs, int64_t dv_hs,
                          float* dgq, int64_t dgq_rs, int64_t dgq_hs, float* dgk, int64_t dgk_rs, int64_t dgk_hs,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+                         void* workspace, size_t workspace_bytes, void* stream, const holo::DropParams* drop) {
   holo::MaskedBwdArgs a;
   int rc = bwd_args(B, T, H, d, gen_mode, edge_scale, io_dtype, gen_dtype, scale, gq, gq_rs, gq_hs, gk, gk_rs,
                     gk_hs, qh, kh, vh_t, P, lse, o, o_rs, o_hs, dout, do_rs, do_hs, dq, dq_rs, dq_hs, dk, dk_rs,
@@ -612,6 +663,8 @@ int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edg
   masked_bwd_layout(B, T, H, d, es, mode, mask != nullptr, workspace, &a);
   a.mode = mode == HOLO_MODE_CAUSAL ? 0 : 1;
   a.hol = hol;
+  a.dropout = drop != nullptr;
+  a.drop = drop ? *drop : holo::DropParams{0u, 1.f, 0u, 0u, 0u};
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
   if (mask) {
@@ -623,6 +676,46 @@ int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edg
                            : holo::launch_masked_bwd<holo::bf16, float>(a, s);
   if (e != hipSuccess) return fail(HOLO_ERR_LAUNCH, "backward launch: %s", hipGetErrorString(e));
   return HOLO_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype, int gen_dtype,
+                         int mode, float scale,
+                         const void* gq, int64_t gq_rs, int64_t gq_hs, const void* gk, int64_t gk_rs, int64_t gk_hs,
+                         const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
+                         const float* lse, const uint8_t* mask, int64_t mask_rs,
+                         const void* o, int64_t o_rs, int64_t o_hs, const void* dout, int64_t do_rs, int64_t do_hs,
+                         void* dq, int64_t dq_rs, int64_t dq_hs, void* dk, int64_t dk_rs, int64_t dk_hs,
+                         void* dv, int64_t dv_rs, int64_t dv_hs,
+                         float* dgq, int64_t dgq_rs, int64_t dgq_hs, float* dgk, int64_t dgk_rs, int64_t dgk_hs,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  return masked_bwd(B, T, H, d, gen_mode, edge_scale, io_dtype, gen_dtype, mode, scale, gq, gq_rs, gq_hs, gk, gk_rs,
+                    gk_hs, qh, kh, vh_t, P, hol, lse, mask, mask_rs, o, o_rs, o_hs, dout, do_rs, do_hs, dq, dq_rs,
+                    dq_hs, dk, dk_rs, dk_hs, dv, dv_rs, dv_hs, dgq, dgq_rs, dgq_hs, dgk, dgk_rs, dgk_hs, workspace,
+                    workspace_bytes, stream, nullptr);
+}
+
+int holo_attn_masked_dropout_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale, int io_dtype,
+                                 int gen_dtype, int mode, float scale, float dropout_p, uint64_t seed, uint32_t offset,
+                                 const void* gq, int64_t gq_rs, int64_t gq_hs, const void* gk, int64_t gk_rs,
+                                 int64_t gk_hs, const void* qh, const void* kh, const void* vh_t, const float* P,
+                                 const float* hol, const float* lse, const uint8_t* mask, int64_t mask_rs,
+                                 const void* o, int64_t o_rs, int64_t o_hs, const void* dout, int64_t do_rs,
+                                 int64_t do_hs, void* dq, int64_t dq_rs, int64_t dq_hs, void* dk, int64_t dk_rs,
+                                 int64_t dk_hs, void* dv, int64_t dv_rs, int64_t dv_hs,
+                                 float* dgq, int64_t dgq_rs, int64_t dgq_hs, float* dgk, int64_t dgk_rs,
+                                 int64_t dgk_hs, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  holo::DropParams dp;
+  const int rc = drop_params(dropout_p, seed, offset, dp);
+  if (rc) return rc;
+  return masked_bwd(B, T, H, d, gen_mode, edge_scale, io_dtype, gen_dtype, mode, scale, gq, gq_rs, gq_hs, gk, gk_rs,
+                    gk_hs, qh, kh, vh_t, P, hol, lse, mask, mask_rs, o, o_rs, o_hs, dout, do_rs, do_hs, dq, dq_rs,
+                    dq_hs, dk, dk_rs, dk_hs, dv, dv_rs, dv_hs, dgq, dgq_rs, dgq_hs, dgk, dgk_rs, dgk_hs, workspace,
+                    workspace_bytes, stream, &dp);
 }
 
 int holo_add_layernorm_fwd(int64_t n, int d, int dtype, float eps, const void* x, int64_t x_rs,

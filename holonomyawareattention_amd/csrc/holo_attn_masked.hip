@@ -29,6 +29,7 @@
 #include <type_traits>
 
 #include "holo_attn_common.h"
+#include "holo_dropout.h"
 
 namespace holo {
 
@@ -101,10 +102,13 @@ template <typename T, int DP> struct MaskedCfg {
 // m = max(m_b, m_w) the output is
 //   P_i (2^(m_b-m) O_b + Hol 2^(m_w-m) O_w) / (2^(m_b-m) l_b + 2^(m_w-m) l_w).
 // LSE (the training forward) also writes each row's m + log2 l over both
-// branches, for the backward.
-template <typename T, int DP, bool PQ16, bool WRAP, bool LSE = false>
+// branches, for the backward. DROP (with LSE) applies attention dropout: the
+// row sums l take every weight, the accumulators only the kept ones, and the
+// normalisation multiplies by 1 / (1 - p).
+template <typename T, int DP, bool PQ16, bool WRAP, bool LSE = false, bool DROP = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 && PQ16 ? 2 : 1)))
 attn_masked(typename MaskedArgsOf<LSE>::type a) {
+  static_assert(LSE || !DROP, "dropout runs in the training forward");
   using C = AttnCfg<T, DP>;
   using M = MaskedCfg<T, DP>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -266,6 +270,18 @@ attn_masked(typename MaskedArgsOf<LSE>::type a) {
         });
       });
       l_run += (ls[0][0] + ls[0][1]) + (ls[1][0] + ls[1][1]);
+      if constexpr (DROP) {
+        // elements 4 G .. 4 G + 3 of S[kb]: one query, four consecutive keys
+        static_for<2>([&](auto kb) {
+          static_for<4>([&](auto G) {
+            const u32x4 wd = keep_words(qi, (k0 + 32 * kb + 8 * G + 4 * g) >> 2, bh, a.drop);
+            static_for<4>([&](auto e) {
+              constexpr int r = 4 * G + e;
+              if (wd[(int)e] < a.drop.thr) pb[kb][r >> 3][r & 7] = (bf16)0.f;
+            });
+          });
+        });
+      }
       static_for<2>([&](auto kb) {
         static_for<2>([&](auto hh) {
           static_for<DP / 32>([&](auto db) {
@@ -284,6 +300,16 @@ attn_masked(typename MaskedArgsOf<LSE>::type a) {
       static_for<4>([&](auto r) { t[r] += t[r + 4]; });
       static_for<2>([&](auto r) { t[r] += t[r + 2]; });
       l_run += t[0] + t[1];
+      if constexpr (DROP) {
+        static_for<2>([&](auto kb) {
+          static_for<4>([&](auto G) {
+            const u32x4 wd = keep_words(qi, (k0 + 32 * kb + 8 * G + 4 * g) >> 2, bh, a.drop);
+            static_for<4>([&](auto e) {
+              if (wd[(int)e] < a.drop.thr) S[kb][4 * G + e] = 0.f;
+            });
+          });
+        });
+      }
       static_for<2>([&](auto kb) {
         static_for<16>([&](auto r) {
           static_for<DP / 32>([&](auto db) {
@@ -378,6 +404,10 @@ attn_masked(typename MaskedArgsOf<LSE>::type a) {
     const float lt = pair_sum(l_run);       // cross-lane: every lane takes part
     if (g == 0 && qi < a.T) a.lse[(int64_t)bh * a.Tp + qi] = m_run + __log2f(lt);
   }
+  if constexpr (DROP) {
+    sw *= a.drop.scale;
+    sb *= a.drop.scale;
+  }
 
   // ---- epilogue: normalise (a row that allowed no key has l = 0: 0 * inf =
   // NaN, as torch.softmax gives), stage, rotate, store. Item = (row, 3-dim
@@ -438,25 +468,25 @@ attn_masked(typename MaskedArgsOf<LSE>::type a) {
   });
 }
 
-template <typename T, int DP, bool PQ16, bool WRAP, bool LSE = false>
+template <typename T, int DP, bool PQ16, bool WRAP, bool LSE = false, bool DROP = false>
 static hipError_t launch_masked_dp(const typename MaskedArgsOf<LSE>::type& a, hipStream_t s) {
   using M = MaskedCfg<T, DP>;
   const size_t lds = M::lds(a.Tp / kBN);
   if (lds > (size_t)kMaxDynamicLds) return hipErrorInvalidValue;
-  const hipError_t attr = allow_dynamic_lds<&attn_masked<T, DP, PQ16, WRAP, LSE>>();
+  const hipError_t attr = allow_dynamic_lds<&attn_masked<T, DP, PQ16, WRAP, LSE, DROP>>();
   if (attr != hipSuccess) return attr;
   const int64_t ntile = (a.T + kBM - 1) / kBM;
-  hipLaunchKernelGGL((attn_masked<T, DP, PQ16, WRAP, LSE>), dim3((unsigned)(a.B * a.H * ntile)), dim3(kThreads),
-                     lds, s, a);
+  hipLaunchKernelGGL((attn_masked<T, DP, PQ16, WRAP, LSE, DROP>), dim3((unsigned)(a.B * a.H * ntile)),
+                     dim3(kThreads), lds, s, a);
   return hipGetLastError();
 }
 
-template <typename T, bool PQ16, bool WRAP, bool LSE = false>
+template <typename T, bool PQ16, bool WRAP, bool LSE = false, bool DROP = false>
 static hipError_t launch_masked_pf(const typename MaskedArgsOf<LSE>::type& a, hipStream_t s) {
   switch (a.Dp) {
-    case 32: return launch_masked_dp<T, 32, PQ16, WRAP, LSE>(a, s);
-    case 64: return launch_masked_dp<T, 64, PQ16, WRAP, LSE>(a, s);
-    case 96: return launch_masked_dp<T, 96, PQ16, WRAP, LSE>(a, s);
+    case 32: return launch_masked_dp<T, 32, PQ16, WRAP, LSE, DROP>(a, s);
+    case 64: return launch_masked_dp<T, 64, PQ16, WRAP, LSE, DROP>(a, s);
+    case 96: return launch_masked_dp<T, 96, PQ16, WRAP, LSE, DROP>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -468,10 +498,14 @@ hipError_t launch_attn_masked(const MaskedArgs& a, hipStream_t s) {
   return wrap ? launch_masked_pf<T, false, true>(a, s) : launch_masked_pf<T, false, false>(a, s);
 }
 
-// the training forward: fp32 quaternions (the backward's format) and the LSE
+// the training forward: fp32 quaternions (the backward's format) and the LSE;
+// with dropout, its own instantiations
 template <typename T>
 hipError_t launch_attn_masked_lse(const MaskedLseArgs& a, hipStream_t s) {
   if (a.p_format) return hipErrorInvalidValue;
+  if (a.dropout)
+    return a.mode == 0 ? launch_masked_pf<T, false, true, true, true>(a, s)
+                       : launch_masked_pf<T, false, false, true, true>(a, s);
   return a.mode == 0 ? launch_masked_pf<T, false, true, true>(a, s) : launch_masked_pf<T, false, false, true>(a, s);
 }
 

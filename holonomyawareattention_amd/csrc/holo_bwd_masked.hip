@@ -23,6 +23,7 @@
 // attn_bwd_masked_dq (per 128 queries: base sweep, then the wrap sweep with
 // qw, dow stored as dqw), hol_torque (causal), link_bwd.
 #include "holo_bwd_kernels.h"
+#include "holo_dropout.h"
 
 namespace holo {
 
@@ -39,11 +40,13 @@ namespace holo {
 // frame of k^ and v^) are the sums over its pairs, so one accumulator carries
 // both branches. The wrap branch's share of dK, dV (for the holonomy's
 // torque) and its dQ (in the frame of qw, rotated back by Hol in link_bwd)
-// are also stored apart.
+// are also stored apart. DROP: the forward's attention dropout (z = keep /
+// (1 - p) per pair, regenerated from its seed): dV takes p z, and
+// dS = p (z dP - delta) (delta = do . o already holds the dropped output).
 enum : int { kRelBase = 0, kRelWrap = 1, kRelAll = 2 };
 constexpr int kMapRows = 128;        // query rows per tile of the open-tile map (mask_tiles)
 
-template <typename T, int DP, bool WRAP>
+template <typename T, int DP, bool WRAP, bool DROP = false>
 __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1)))
 attn_bwd_masked_dkdv(MaskedBwdArgs a) {
   using C = BwdCfg<T, DP, kFillKV>;
@@ -170,6 +173,26 @@ attn_bwd_masked_dkdv(MaskedBwdArgs a) {
             dP = __builtin_amdgcn_mfma_f32_32x32x2f32(dOs[(ro + lr) * C::RS + 2 * s + g], vf[s], dP, 0, 0, 0);
           }
         });
+        // dropout: this lane's words for its key at the 16 queries. Philox
+        // call (query, key / 4) gives the words of four consecutive keys, held
+        // by the lanes of one quad; in group G each lane c = lane % 4 of a
+        // quad draws for query qs0 + 8 G + 4 g + c, and four rotations
+        // (step s: lane c sends word (c - s) % 4, receives from lane
+        // (c + s) % 4) give every lane its own key's word of each query.
+        float z[DROP ? 16 : 1];
+        if constexpr (DROP) {
+          const int c = lr & 3;
+          static_for<4>([&](auto G) {
+            const u32x4 wd = keep_words(qs0 + 8 * G + 4 * g + c, key >> 2, bh, a.drop);
+            u32x4 got;
+            static_for<4>([&](auto st) {
+              got[(int)st] = __shfl((int)pick4(wd, (c - (int)st) & 3), (lane & ~3) | ((c + (int)st) & 3));
+            });
+            static_for<4>([&](auto e) {          // query qs0 + 8 G + 4 g + e arrived at step (e - c) % 4
+              z[4 * G + e] = pick4(got, ((int)e - c) & 3) >= a.drop.thr ? a.drop.scale : 0.f;
+            });
+          });
+        }
         // element r: query qs0 + qr (row), this lane's key (column)
         static_for<16>([&](auto rr) {
           const int qr = 8 * (rr >> 2) + 4 * g + (rr & 3);
@@ -178,8 +201,13 @@ attn_bwd_masked_dkdv(MaskedBwdArgs a) {
           if constexpr (rel == kRelBase) ok = ok && key <= qi;
           if constexpr (rel == kRelWrap) ok = ok && key > qi;
           const float pm = ok ? exp2f(__builtin_fmaf(S[(int)rr], cl, -lse_s[ro + qr])) : 0.f;
-          S[(int)rr] = pm;
-          dP[(int)rr] = ok ? pm * (dP[(int)rr] - del_s[ro + qr]) : 0.f;
+          if constexpr (DROP) {
+            S[(int)rr] = pm * z[(int)rr];
+            dP[(int)rr] = ok ? pm * (z[(int)rr] * dP[(int)rr] - del_s[ro + qr]) : 0.f;
+          } else {
+            S[(int)rr] = pm;
+            dP[(int)rr] = ok ? pm * (dP[(int)rr] - del_s[ro + qr]) : 0.f;
+          }
         });
         if constexpr (kBF) {
           bf16x8 pb[2], sb[2];
@@ -231,7 +259,7 @@ attn_bwd_masked_dkdv(MaskedBwdArgs a) {
   store(a.dkh, a.dvh);
 }
 
-template <typename T, int DP, bool WRAP>
+template <typename T, int DP, bool WRAP, bool DROP = false>
 __global__ void __launch_bounds__(kBwdThreads) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1)))
 attn_bwd_masked_dq(MaskedBwdArgs a) {
   using C = BwdCfg<T, DP>;
@@ -316,6 +344,15 @@ attn_bwd_masked_dq(MaskedBwdArgs a) {
             dP = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[(ro + lr) * C::RS + 2 * s + g], df[s], dP, 0, 0, 0);
           }
         });
+        // dropout: elements 4 G .. 4 G + 3 are four consecutive keys of this
+        // lane's query, the four words of one Philox call
+        float z[DROP ? 16 : 1];
+        if constexpr (DROP) {
+          static_for<4>([&](auto G) {
+            const u32x4 wd = keep_words(q, (k0 + ro + 8 * G + 4 * g) >> 2, bh, a.drop);
+            static_for<4>([&](auto e) { z[4 * G + e] = wd[(int)e] >= a.drop.thr ? a.drop.scale : 0.f; });
+          });
+        }
         // element r: key ks0 + kr (row), this lane's query (column)
         static_for<16>([&](auto rr) {
           const int kr = ro + 8 * (rr >> 2) + 4 * g + (rr & 3);    // key offset in the fill
@@ -324,7 +361,8 @@ attn_bwd_masked_dq(MaskedBwdArgs a) {
           if constexpr (rel == kRelBase) ok = ok && kk <= q;
           if constexpr (rel == kRelWrap) ok = ok && kk > q;
           const float pm = ok ? exp2f(__builtin_fmaf(S[(int)rr], cl, -lse)) : 0.f;
-          dP[(int)rr] = ok ? pm * (dP[(int)rr] - del) : 0.f;
+          if constexpr (DROP) dP[(int)rr] = ok ? pm * (z[(int)rr] * dP[(int)rr] - del) : 0.f;
+          else dP[(int)rr] = ok ? pm * (dP[(int)rr] - del) : 0.f;
         });
         if constexpr (kBF) {
           bf16x8 sb[2];
@@ -434,9 +472,15 @@ static hipError_t launch_masked_bwd_ex(const MaskedBwdArgs& a, hipStream_t s) {
   constexpr bool WRAP = EX == 1;
   const int64_t nbh = (int64_t)a.B * a.H;
   const int64_t nblk = (a.Tp + 127) / 128;
+  const dim3 grid((unsigned)(nbh * nblk));
   hipLaunchKernelGGL((bwd_prep<IO, DP, EX>), dim3((unsigned)(nbh * a.nch)), dim3(kBwdThreads), 0, s, a);
-  hipLaunchKernelGGL((attn_bwd_masked_dkdv<IO, DP, WRAP>), dim3((unsigned)(nbh * nblk)), dim3(kBwdThreads), 0, s, a);
-  hipLaunchKernelGGL((attn_bwd_masked_dq<IO, DP, WRAP>), dim3((unsigned)(nbh * nblk)), dim3(kBwdThreads), 0, s, a);
+  if (a.dropout) {
+    hipLaunchKernelGGL((attn_bwd_masked_dkdv<IO, DP, WRAP, true>), grid, dim3(kBwdThreads), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_masked_dq<IO, DP, WRAP, true>), grid, dim3(kBwdThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_masked_dkdv<IO, DP, WRAP>), grid, dim3(kBwdThreads), 0, s, a);
+    hipLaunchKernelGGL((attn_bwd_masked_dq<IO, DP, WRAP>), grid, dim3(kBwdThreads), 0, s, a);
+  }
   if constexpr (WRAP)
     hipLaunchKernelGGL((hol_torque<IO, DP>), dim3((unsigned)nbh), dim3(kBwdThreads), 0, s, a);
   hipError_t e = launch_chain_reset(a.carry, nbh * a.nch * a.nb * 2, a.ticket, s);
@@ -458,5 +502,28 @@ hipError_t launch_masked_bwd(const MaskedBwdArgs& a, hipStream_t s) {
 
 template hipError_t launch_masked_bwd<float, float>(const MaskedBwdArgs&, hipStream_t);
 template hipError_t launch_masked_bwd<bf16, float>(const MaskedBwdArgs&, hipStream_t);
+
+// keep[(bh T + i) T + j] = 1 when attention dropout keeps pair (i, j) of
+// head bh: one thread per (bh, i, j / 4), the four words of one Philox call
+__global__ void __launch_bounds__(256) dropout_keep(int64_t nbh, int64_t T, DropParams d, uint8_t* keep) {
+  const int64_t nj4 = (T + 3) / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= nbh * T * nj4) return;
+  const int64_t j4 = idx % nj4, row = idx / nj4;           // row = bh T + i
+  const int64_t i = row % T, bh = row / T;
+  const u32x4 wd = keep_words(i, j4, bh, d);
+  uint8_t* dst = keep + row * T + 4 * j4;
+  static_for<4>([&](auto e) {
+    if (4 * j4 + e < T) dst[(int)e] = wd[(int)e] >= d.thr ? 1 : 0;
+  });
+}
+
+hipError_t launch_dropout_keep(int B, int H, int64_t T, const DropParams& d, uint8_t* keep, hipStream_t s) {
+  const int64_t nbh = (int64_t)B * H, n = nbh * T * ((T + 3) / 4);
+  if (n == 0) return hipSuccess;
+  if ((n + 255) / 256 > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(dropout_keep, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, nbh, T, d, keep);
+  return hipGetLastError();
+}
 
 }  // namespace holo

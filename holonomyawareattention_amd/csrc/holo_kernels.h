@@ -76,11 +76,25 @@ struct BwdArgs {
   float* dgk; int64_t dgk_rs, dgk_hs;
 };
 
+// Attention dropout of the exact path's training pair: pair (i, j) of head bh
+// is kept when word j % 4 of Philox4x32-10 at counter (i, j / 4, bh, offset)
+// under key (k0, k1) is >= thr; kept weights are multiplied by scale.
+struct DropParams {
+  uint32_t thr;                          // round(p 2^32), capped at 2^32 - 1
+  float scale;                           // 1 / (1 - p)
+  uint32_t k0, k1;                       // the seed's low and high words
+  uint32_t offset;                       // the counter's fourth word
+};
+
 // The exact path's forward for training: MaskedArgs and the per-row
 // log2-domain log-sum-exp of the scaled scores (m + log2 l over both
-// branches), which its backward recomputes the probabilities from.
+// branches), which its backward recomputes the probabilities from; with
+// dropout on, the output weights are the softmax weights times keep * scale
+// (the LSE stays that of the softmax).
 struct MaskedLseArgs : MaskedArgs {
   float* lse;                            // (B, H, Tp)
+  int dropout;                           // 1: apply `drop`
+  DropParams drop;
 };
 template <bool LSE> struct MaskedArgsOf { typedef MaskedLseArgs type; };
 template <> struct MaskedArgsOf<false> { typedef MaskedArgs type; };
@@ -97,6 +111,8 @@ struct MaskedBwdArgs : BwdArgs {
   void* qw_t; void* dow_t;               // their transposed tiles (fp32 only)
   float* dqw; float* dkw; float* dvw;    // wrap-branch gradients, path frame (fp32, causal)
   float* hol_torque;                     // (B, H, nb, 4): the holonomy's cross sum (causal)
+  int dropout;                           // 1: the forward applied `drop`
+  DropParams drop;
 };
 // kernel variants of the backward: 0 the causal + tril path, 1 the exact
 // path in causal mode, 2 the exact path in inert mode
@@ -184,5 +200,7 @@ hipError_t launch_quat_to_dense(int64_t n, int d, const float* q, float* out, hi
 hipError_t launch_chain_reset(void* state, int64_t n_pairs, unsigned* ticket, hipStream_t s);
 template <typename IO, typename GT> hipError_t launch_bwd(const BwdArgs& a, hipStream_t s);
 template <typename IO, typename GT> hipError_t launch_masked_bwd(const MaskedBwdArgs& a, hipStream_t s);
+// keep (B, H, T, T) uint8: 1 where attention dropout keeps pair (i, j)
+hipError_t launch_dropout_keep(int B, int H, int64_t T, const DropParams& d, uint8_t* keep, hipStream_t s);
 
 }  // namespace holo

@@ -5,7 +5,9 @@
 ``attention_masked`` -> holo_attn_masked_fwd : any mask, causal (wrap through Hol) or inert mode
 ``attention_backward`` -> holo_attn_bwd : gradients of both wrt q, k, v and the generator
 ``attention_masked_train`` / ``attention_masked_backward`` -> holo_attn_masked_train_fwd /
-    holo_attn_masked_bwd : the exact path's training forward (with its LSE) and gradient
+    holo_attn_masked_bwd : the exact path's training forward (with its LSE) and gradient;
+    with dropout_p > 0 holo_attn_masked_dropout_fwd / holo_attn_masked_dropout_bwd
+``dropout_keep_mask`` -> holo_dropout_keep_mask : attention dropout's keep mask
 ``quat_to_dense`` -> holo_quat_to_dense
 ``add_layernorm`` -> holo_add_layernorm_fwd : residual add + LayerNorm of the decoder stack
 ``edge_hidden`` -> holo_edge_hidden_fwd : q/k/v and the interaction edge MLP's first layer
@@ -396,13 +398,46 @@ def attention_masked(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: 
     return out
 
 
+def _dropout_args(what: str, dropout_p: float, seed: int, offset: int) -> Tuple[float, int, int]:
+    p = float(dropout_p)
+    if not (0.0 <= p < 1.0):
+        raise ValueError(f"{what}: dropout_p must be in [0, 1), got {dropout_p}")
+    seed, offset = int(seed), int(offset)
+    if not (0 <= seed < 2 ** 64 and 0 <= offset < 2 ** 32):
+        raise ValueError(f"{what}: seed must be a 64-bit and offset a 32-bit unsigned integer")
+    return p, seed, offset
+
+
+def dropout_keep_mask(B: int, T: int, H: int, dropout_p: float, seed: int, offset: int = 0,
+                      device: Optional[torch.device] = None) -> torch.Tensor:
+    """holo_dropout_keep_mask: (B, H, T, T) bool, True where attention dropout
+    with (dropout_p, seed, offset) keeps pair (i, j) -- the mask that
+    attention_masked_train and attention_masked_backward regenerate."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    if dev.type != "cuda":
+        raise ValueError("dropout_keep_mask: device must be a GPU")
+    p, seed, offset = _dropout_args("dropout_keep_mask", dropout_p, seed, offset)
+    keep = torch.empty((int(B), int(H), int(T), int(T)), dtype=torch.uint8, device=dev)
+    if keep.numel() == 0:
+        return keep.bool()
+    with torch.cuda.device(dev):
+        rc = _lib.load().holo_dropout_keep_mask(int(B), int(T), int(H), p, seed, offset, _ptr(keep), _stream(dev))
+    _lib.check(rc, "holo_dropout_keep_mask")
+    return keep.view(torch.bool)
+
+
 def attention_masked_train(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tensor, P: torch.Tensor,
                            hol: Optional[torch.Tensor], d: int, scale: float, mode: str = "causal",
-                           mask: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                           mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0, seed: int = 0,
+                           offset: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
     """holo_attn_masked_train_fwd: attention_masked for training (P in fp32
     quaternions) that also returns each row's log2-domain log-sum-exp
-    (B, H, Tp) fp32, which attention_masked_backward reads. Returns (o, lse)."""
+    (B, H, Tp) fp32, which attention_masked_backward reads. Returns (o, lse).
+    dropout_p > 0 runs holo_attn_masked_dropout_fwd: attention dropout on the
+    softmax weights with the keep mask of (seed, offset); the backward must be
+    given the same three values."""
     _one_gpu("attention_masked_train", qh, kh, vh_t, P, hol, mask)
+    dropout_p, seed, offset = _dropout_args("attention_masked_train", dropout_p, seed, offset)
     lib = _lib.load()
     B, H, T, nb, dev, dt, pf, m8, m_rs = _masked_inputs("attention_masked_train", qh, kh, vh_t, P, hol, d, mode,
                                                         mask)
@@ -413,11 +448,15 @@ def attention_masked_train(qh: torch.Tensor, kh: torch.Tensor, vh_t: torch.Tenso
     o_rs, o_hs = _token_view(out, B, T, H, d, "out")
     ws_bytes = int(lib.holo_attn_masked_workspace_size(B, T, H, d, _DT[dt], _MODE[mode], int(mask is not None)))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    rc = lib.holo_attn_masked_train_fwd(B, T, H, d, _DT[dt], _MODE[mode], float(scale),
-                                        _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
-                                        _ptr(hol) if mode == "causal" else None, _ptr(m8), m_rs,
-                                        _ptr(out), o_rs, o_hs, _ptr(lse), _ptr(ws), ws_bytes, _stream(dev))
-    _lib.check(rc, "holo_attn_masked_train_fwd")
+    tail = (_ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None, _ptr(hol) if mode == "causal" else None,
+            _ptr(m8), m_rs, _ptr(out), o_rs, o_hs, _ptr(lse), _ptr(ws), ws_bytes, _stream(dev))
+    if dropout_p > 0.0:
+        rc = lib.holo_attn_masked_dropout_fwd(B, T, H, d, _DT[dt], _MODE[mode], float(scale), dropout_p, seed, offset,
+                                              *tail)
+        _lib.check(rc, "holo_attn_masked_dropout_fwd")
+    else:
+        rc = lib.holo_attn_masked_train_fwd(B, T, H, d, _DT[dt], _MODE[mode], float(scale), *tail)
+        _lib.check(rc, "holo_attn_masked_train_fwd")
     return out, lse
 
 
@@ -497,30 +536,38 @@ def attention_masked_backward(gq: torch.Tensor, gk: Optional[torch.Tensor], edge
                               hol: Optional[torch.Tensor], lse: torch.Tensor, o: torch.Tensor, dout: torch.Tensor,
                               d: int, scale: float, dq: torch.Tensor, dk: torch.Tensor, dv: torch.Tensor,
                               dgq: torch.Tensor, dgk: Optional[torch.Tensor], mode: str = "causal",
-                              mask: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> None:
+                              mask: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                              dropout_p: float = 0.0, seed: int = 0, offset: int = 0) -> None:
     """holo_attn_masked_bwd: gradients of the exact path (any mask, either
     mode) given dout; arguments as attention_backward's, plus the mode, the
     holonomy hol (causal mode) and the mask of the forward; o and lse from
     attention_masked_train. In causal mode the closing edge (gq_{T-1}, gk_0)
-    gets its gradient through the holonomy."""
+    gets its gradient through the holonomy. dropout_p > 0 runs
+    holo_attn_masked_dropout_bwd with the forward's dropout_p, seed, offset."""
     _one_gpu("attention_masked_backward", qh, kh, vh_t, P, hol, lse, o, dout, dq, dk, dv, gq, gk, dgq, dgk, mask,
              workspace)
-    lib = _lib.load()
     what = "attention_masked_backward"
+    dropout_p, seed, offset = _dropout_args(what, dropout_p, seed, offset)
+    lib = _lib.load()
     *_, m8, m_rs = _masked_inputs(what, qh, kh, vh_t, P, hol, d, mode, mask)
     B, H, T, nb, dev, dt, views, gv = _bwd_inputs(what, gq, gk, qh, kh, vh_t, P, lse, o, dout, d, dq, dk, dv, dgq, dgk)
     need = int(lib.holo_attn_masked_bwd_workspace_size(B, T, H, d, _DT[dt], _MODE[mode], int(mask is not None)))
     workspace = _workspace(what, workspace, need, dev)
     gm = _lib.HOLO_GEN_ADDITIVE if gk is not None else _lib.HOLO_GEN_DIRECT
-    rc = lib.holo_attn_masked_bwd(B, T, H, d, gm, float(edge_scale), _DT[dt], _lib.HOLO_F32, _MODE[mode],
-                                  float(scale), _ptr(gq), *gv[0], _ptr(gk), *gv[1],
-                                  _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
-                                  _ptr(hol) if mode == "causal" else None, _ptr(lse), _ptr(m8), m_rs,
-                                  _ptr(o), *views[0], _ptr(dout), *views[1],
-                                  _ptr(dq), *views[2], _ptr(dk), *views[3], _ptr(dv), *views[4],
-                                  _ptr(dgq), *gv[2], _ptr(dgk), *gv[3],
-                                  _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(dev))
-    _lib.check(rc, "holo_attn_masked_bwd")
+    head = (B, T, H, d, gm, float(edge_scale), _DT[dt], _lib.HOLO_F32, _MODE[mode], float(scale))
+    tail = (_ptr(gq), *gv[0], _ptr(gk), *gv[1],
+            _ptr(qh), _ptr(kh), _ptr(vh_t), _ptr(P) if nb else None,
+            _ptr(hol) if mode == "causal" else None, _ptr(lse), _ptr(m8), m_rs,
+            _ptr(o), *views[0], _ptr(dout), *views[1],
+            _ptr(dq), *views[2], _ptr(dk), *views[3], _ptr(dv), *views[4],
+            _ptr(dgq), *gv[2], _ptr(dgk), *gv[3],
+            _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(dev))
+    if dropout_p > 0.0:
+        rc = lib.holo_attn_masked_dropout_bwd(*head, dropout_p, seed, offset, *tail)
+        _lib.check(rc, "holo_attn_masked_dropout_bwd")
+    else:
+        rc = lib.holo_attn_masked_bwd(*head, *tail)
+        _lib.check(rc, "holo_attn_masked_bwd")
 
 
 def quat_to_dense(quat: torch.Tensor, d: int) -> torch.Tensor:

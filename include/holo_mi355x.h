@@ -27,7 +27,12 @@
  *   holo_attn_masked_train_fwd, holo_attn_masked_bwd
  *                       the exact path's forward with its log-sum-exp and its
  *                       backward (torch autograd through kernel/attention_fast.py:
- *                       78-166 in the reference).
+ *                       78-166 in the reference);
+ *   holo_attn_masked_dropout_fwd, holo_attn_masked_dropout_bwd,
+ *   holo_dropout_keep_mask
+ *                       the same pair with attention dropout (the nn.Dropout on
+ *                       the softmax weights, kernel/attention_fast.py:160), and
+ *                       the keep mask it draws.
  *
  * Conventions
  *   - Every pointer is a device pointer owned by the caller; no entry point
@@ -386,6 +391,57 @@ HOLO_API int holo_attn_masked_bwd(int B, int64_t T, int H, int d, int gen_mode, 
                   float* dgq, int64_t dgq_row_stride, int64_t dgq_head_stride,
                   float* dgk, int64_t dgk_row_stride, int64_t dgk_head_stride,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Attention dropout of the exact path (kernel/attention_fast.py:160, an
+ * nn.Dropout(p) on the softmax weights, active in training; core/attention.py:
+ * 190). Pair (i, j) of head bh = b*H + h is kept when word j % 4 of
+ * Philox4x32-10 (Salmon et al., SC 2011) at counter (i, j / 4, bh, offset)
+ * under key (seed mod 2^32, seed / 2^32) is >= round(p * 2^32); kept weights
+ * are multiplied by 1 / (1 - p). The mask is a function of (seed, offset)
+ * and is never stored: the forward and the backward regenerate it, so a
+ * backward must be given the forward's p, seed and offset. 0 <= p < 1.
+ *
+ * holo_attn_masked_dropout_fwd: holo_attn_masked_train_fwd with dropout: o_i
+ * takes a_ij * keep_ij / (1 - p) in place of a_ij; lse is the softmax's, as
+ * without dropout.
+ */
+HOLO_API int holo_attn_masked_dropout_fwd(int B, int64_t T, int H, int d, int dtype, int mode, float scale,
+                         float dropout_p, uint64_t seed, uint32_t offset,
+                         const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
+                         const uint8_t* mask, int64_t mask_row_stride,
+                         void* o, int64_t o_row_stride, int64_t o_head_stride, float* lse,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * holo_attn_masked_dropout_bwd: holo_attn_masked_bwd for the output of
+ * holo_attn_masked_dropout_fwd (same dropout_p, seed and offset); the
+ * workspace is holo_attn_masked_bwd_workspace_size's.
+ */
+HOLO_API int holo_attn_masked_dropout_bwd(int B, int64_t T, int H, int d, int gen_mode, float edge_scale,
+                  int io_dtype, int gen_dtype, int mode, float scale,
+                  float dropout_p, uint64_t seed, uint32_t offset,
+                  const void* gq, int64_t gq_row_stride, int64_t gq_head_stride,
+                  const void* gk, int64_t gk_row_stride, int64_t gk_head_stride,
+                  const void* qh, const void* kh, const void* vh_t, const float* P, const float* hol,
+                  const float* lse, const uint8_t* mask, int64_t mask_row_stride,
+                  const void* o, int64_t o_row_stride, int64_t o_head_stride,
+                  const void* dout, int64_t dout_row_stride, int64_t dout_head_stride,
+                  void* dq, int64_t dq_row_stride, int64_t dq_head_stride,
+                  void* dk, int64_t dk_row_stride, int64_t dk_head_stride,
+                  void* dv, int64_t dv_row_stride, int64_t dv_head_stride,
+                  float* dgq, int64_t dgq_row_stride, int64_t dgq_head_stride,
+                  float* dgk, int64_t dgk_row_stride, int64_t dgk_head_stride,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * holo_dropout_keep_mask: writes keep (B, H, T, T) uint8, element (b, h, i, j)
+ * at keep[((b*H + h)*T + i)*T + j]: 1 where the calls above with the same
+ * dropout_p, seed and offset keep pair (i, j), else 0 (for inspection and
+ * tests).
+ */
+HOLO_API int holo_dropout_keep_mask(int B, int64_t T, int H, float dropout_p, uint64_t seed, uint32_t offset,
+                                    uint8_t* keep, void* stream);
 
 /*
  * Incremental decode (no counterpart in the reference, which only runs whole

@@ -52,6 +52,16 @@ Pinning (every function has at least one independent check in tests/):
            mask, random and ring masks, the closing edge included); under
            tril the tril backward oracle (pinned to torch autograd);
            planted mistakes fail (tests/test_oracle_exact_backward.py).
+  philox4x32_10 -> the published known-answer vectors of Philox4x32-10
+           (Random123: zero, all-ones and pi-digit counters and keys);
+  dropout_keep -> kept fraction within binomial bounds, rows independent of
+           the row subset asked for, p = 0 keeps everything;
+  exact_attention64 / exact_backward64 with keep -> p = 0 gives the
+           dropout-free result; with drop_scale = 1 the outputs of a keep
+           mask and of its complement sum to the dropout-free output
+           (dropout acts on the softmax weights of both branches); the
+           gradients by central differences under a fixed keep mask, with
+           planted mistakes failing (tests/test_oracle_dropout.py).
   decoder_forward -> at edge_scale = 0 (P = I) a stack of torch's own pre-LN
            nn.TransformerEncoderLayer (GELU, causal mask, zero attention
            biases, the per-head interleaved qkv rows reordered into torch's
@@ -341,7 +351,8 @@ def ring_mask(T: int) -> np.ndarray:
 
 
 def exact_attention64(q: np.ndarray, k: np.ndarray, v: np.ndarray, P: np.ndarray, Hol: np.ndarray,
-                      scale: float, mask: Optional[np.ndarray] = None, mode: str = "causal") -> np.ndarray:
+                      scale: float, mask: Optional[np.ndarray] = None, mode: str = "causal",
+                      keep: Optional[np.ndarray] = None, drop_scale: float = 1.0) -> np.ndarray:
     """Per-head outputs (B, H, T, d) of the reference's exact path for any
     mask and mode (kernel/attention_fast.py:129-162, which
     kernel/attention_kernel.py:211-213 runs for every call off the kernel
@@ -357,7 +368,10 @@ def exact_attention64(q: np.ndarray, k: np.ndarray, v: np.ndarray, P: np.ndarray
               o_i  = P_i (sum_{j<=i} a_ij v^_j + Hol sum_{j>i} a_ij v^_j)
       inert:  s_ij = q'_i . k'_j,   o_i = P_i^T sum_j a_ij v'_j
     q, k, v (B, H, T, d); P (B, H, T, nb, 3, 3); Hol (B, H, nb, 3, 3);
-    mask (T, T) bool or None (everything allowed)."""
+    mask (T, T) bool or None (everything allowed). Attention dropout
+    (kernel/attention_fast.py:160, an nn.Dropout on the softmax weights):
+    keep (B, H, T, T) bool (dropout_keep) multiplies a_ij by
+    keep_ij * drop_scale (1 / (1 - p)) after the softmax."""
     T = q.shape[-2]
     allowed = np.ones((T, T), dtype=bool) if mask is None else np.asarray(mask, dtype=bool)
     if mode == "causal":
@@ -377,11 +391,69 @@ def exact_attention64(q: np.ndarray, k: np.ndarray, v: np.ndarray, P: np.ndarray
         s = s - s.max(axis=-1, keepdims=True)
         p = np.exp(s)
         p = p / p.sum(axis=-1, keepdims=True)
+    if keep is not None:
+        p = np.where(keep, p * drop_scale, 0.0)
     if mode == "causal":
         oh = np.einsum("...ij,...jd->...id", np.where(base, p, 0.0), vh) + \
             np.einsum("...ij,...jd->...id", np.where(base, 0.0, p), vhw)
         return apply_blocks(P, oh)
     return apply_blocks_T(P, np.einsum("...ij,...jd->...id", p, vh))
+
+
+# --------------------------------------------------------------------------
+# attention dropout's keep mask
+# --------------------------------------------------------------------------
+# Philox4x32-10 (Salmon, Moraes, Dror and Shaw, "Parallel random numbers: as
+# easy as 1, 2, 3", SC 2011): ten rounds of two 32x32->64-bit products on a
+# 128-bit counter under a 64-bit key bumped by Weyl increments.
+PHILOX_M = (0xD2511F53, 0xCD9E8D57)
+PHILOX_W = (0x9E3779B9, 0xBB67AE85)
+
+
+def philox4x32_10(ctr: np.ndarray, key: Tuple[int, int]) -> np.ndarray:
+    """Philox4x32-10 of counters ctr (..., 4) uint32 under key (k0, k1):
+    (..., 4) uint32. Each round maps (c0, c1, c2, c3) to
+    (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0)) and then
+    bumps the key by PHILOX_W."""
+    ctr = np.asarray(ctr, dtype=np.uint32)
+    c = [ctr[..., i].astype(np.uint64) for i in range(4)]
+    m32 = np.uint64(0xFFFFFFFF)
+    k0, k1 = np.uint64(int(key[0]) & 0xFFFFFFFF), np.uint64(int(key[1]) & 0xFFFFFFFF)
+    M0, M1 = np.uint64(PHILOX_M[0]), np.uint64(PHILOX_M[1])
+    for _ in range(10):
+        p0, p1 = M0 * c[0], M1 * c[2]                 # exact: both factors below 2^32
+        c = [(p1 >> np.uint64(32)) ^ c[1] ^ k0, p1 & m32, (p0 >> np.uint64(32)) ^ c[3] ^ k1, p0 & m32]
+        k0 = (k0 + np.uint64(PHILOX_W[0])) & m32
+        k1 = (k1 + np.uint64(PHILOX_W[1])) & m32
+    return np.stack(c, -1).astype(np.uint32)
+
+
+def dropout_threshold(p: float) -> int:
+    """The 32-bit threshold of drop probability p (0 <= p < 1, taken as a
+    float32): a pair is kept when its random word is >= round(p * 2^32)
+    (ties to even), capped at 2^32 - 1."""
+    t = float(np.float32(p)) * 4294967296.0
+    return min(int(round(t)), 0xFFFFFFFF)
+
+
+def dropout_keep(B: int, H: int, T: int, p: float, seed: int, offset: int = 0,
+                 rows: Optional[np.ndarray] = None) -> np.ndarray:
+    """Keep mask (B, H, T, T) bool of attention dropout with probability p:
+    pair (i, j) of head (b, h) is kept when word j % 4 of
+    philox4x32_10((i, j // 4, b H + h, offset), (seed mod 2^32, seed // 2^32))
+    is >= dropout_threshold(p). rows (optional index array) limits i to
+    those rows: (B, H, len(rows), T)."""
+    i = np.arange(T, dtype=np.uint64) if rows is None else np.asarray(rows, dtype=np.uint64)
+    j = np.arange(T, dtype=np.uint64)
+    bh = np.arange(B * H, dtype=np.uint64).reshape(B, H, 1, 1)
+    ctr = np.empty((B, H, len(i), (T + 3) // 4, 4), dtype=np.uint32)
+    ctr[..., 0] = i.reshape(1, 1, -1, 1)
+    ctr[..., 1] = np.arange((T + 3) // 4, dtype=np.uint64).reshape(1, 1, 1, -1)
+    ctr[..., 2] = bh
+    ctr[..., 3] = int(offset) & 0xFFFFFFFF
+    words = philox4x32_10(ctr, (int(seed) & 0xFFFFFFFF, (int(seed) >> 32) & 0xFFFFFFFF))
+    words = words.reshape(B, H, len(i), -1)[..., :T]
+    return words >= np.uint32(dropout_threshold(p))
 
 
 def geometry_blocks(a: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
@@ -608,7 +680,8 @@ def _link_param_grad(a: np.ndarray, g: np.ndarray) -> np.ndarray:
 
 
 def exact_backward64(q: np.ndarray, k: np.ndarray, v: np.ndarray, a: np.ndarray, do: np.ndarray, scale: float,
-                     mask: Optional[np.ndarray] = None, mode: str = "causal", plant: str = "") -> Dict[str, np.ndarray]:
+                     mask: Optional[np.ndarray] = None, mode: str = "causal", plant: str = "",
+                     keep: Optional[np.ndarray] = None, drop_scale: float = 1.0) -> Dict[str, np.ndarray]:
     """Gradients of <do, exact_attention64(q, k, v, P(a), Hol(a), ...)>
     (the exact path for any mask and mode) with respect to q, k, v (B,H,T,d)
     and the link parameters a (B,H,T,m) of all T edges, in float64. Rows
@@ -628,6 +701,10 @@ def exact_backward64(q: np.ndarray, k: np.ndarray, v: np.ndarray, a: np.ndarray,
     Inert mode is the same algebra with P replaced by Q = P^T (u' = P u): the
     cross sums c'_t in the primed frame give c_t = -P_t^T c'_t, and there is
     no holonomy (the closing edge's gradient is zero).
+    With attention dropout (keep, drop_scale as for exact_attention64) the
+    output weights are A = p z, z = keep * drop_scale: dv^ and dvw take A in
+    place of p, the gradient of p is z dA, and delta_i = sum_j p_ij z_ij dA_ij
+    is still do^_i . u_i, since u is formed with A.
     `plant` (tests only) introduces one named mistake, so that the tests can
     show their checks detect it."""
     T = q.shape[-2]
@@ -655,22 +732,28 @@ def exact_backward64(q: np.ndarray, k: np.ndarray, v: np.ndarray, a: np.ndarray,
     s = np.where(allowed, s, -np.inf)
     p = np.exp(s - s.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
-    pb, pw = np.where(base, p, 0.0), np.where(base, 0.0, p)
+    z = 1.0 if keep is None else np.where(keep, drop_scale, 0.0)
+    if plant == "dropout_before_softmax" and keep is not None:
+        p = np.where(keep, p, 0.0)
+        p = p / p.sum(-1, keepdims=True)
+        z = 1.0
+    A = p * z
+    Ab, Aw = np.where(base, A, 0.0), np.where(base, 0.0, A)
     if mode == "causal":
         dA = np.where(base, dot(doh, vh), dot(dow, vh))
-        u = mm(pb, vh) + apply_blocks(Hb, mm(pw, vh))
+        u = mm(Ab, vh) + apply_blocks(Hb, mm(Aw, vh))
     else:
         dA = dot(doh, vh)
-        u = mm(p, vh)
+        u = mm(A, vh)
     delta = (doh * u).sum(-1, keepdims=True)
-    dS = p * (dA - delta)
+    dS = p * ((dA if plant == "dropout_grad_unscaled" else z * dA) - delta)
     dSb, dSw = np.where(base, dS, 0.0), np.where(base, 0.0, dS)
     dqh = scale * mm(dSb, kh)
     dkh = scale * mmT(dSb, qh)
-    dvh = mmT(pb, doh)
+    dvh = mmT(Ab, doh)
     if mode == "causal":
         dqh = dqh + apply_blocks(Hb, scale * mm(dSw, kh))
-        dkw, dvw = scale * mmT(dSw, qw), mmT(pw, dow)
+        dkw, dvw = scale * mmT(dSw, qw), mmT(Aw, dow)
         dkh, dvh = dkh + dkw, dvh + dvw
     c = (np.cross(b3(u), b3(doh)) + np.cross(b3(dqh), b3(qh)) + np.cross(b3(dkh), b3(kh))
          + np.cross(b3(dvh), b3(vh)))

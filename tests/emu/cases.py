@@ -259,6 +259,9 @@ def case_edge(emu: Emu, p):
     if not samp:
         assert wq_.all() and wh_.all(), "unwritten outputs"
     rq, rh = (np.flatnonzero(w.any(1)) for w in (wq_, wh_))
+    if p.get("check_rows"):                 # a full grid at full size: check these rows
+        pick = np.unique(np.linspace(0, M - 1, int(p["check_rows"])).astype(np.int64))
+        rq, rh = np.intersect1d(rq, pick), np.intersect1d(rh, pick)
     x, W1 = h["x"], h["w1"]
     xn = np.roll(x.reshape(B, T, K), -1, axis=1).reshape(M, K)
     # hidden layer
@@ -294,6 +297,8 @@ def case_edge(emu: Emu, p):
     if not samp:
         assert wg_.all(), "unwritten outputs"
     rg = np.flatnonzero(wg_.any(1))
+    if p.get("check_rows"):
+        rg = np.intersect1d(rg, pick)
     hh = emu.host(hid, "bf16")[rg]
     w2 = h["w2"]
     ref_g, mag_g = hh @ w2.T, np.abs(hh) @ np.abs(w2).T
@@ -533,7 +538,13 @@ def case_masked_bwd(emu: Emu, p):
     holo_attn_masked_fwd's) -> holo_attn_masked_bwd, against
     oracle.exact_backward64 on the same q, k, v and generator: dq, dk, dv and
     the generator gradients dgq, dgk (the closing edge's included), each
-    relative to its largest entry, and lse against the float64 value."""
+    relative to its largest entry, and lse against the float64 value.
+    "check": False runs the launches only (bounds at full size). "drop":
+    {"p", "seed", "offset"} runs the dropout pair instead
+    (holo_attn_masked_dropout_fwd / _bwd): the keep mask of
+    holo_dropout_keep_mask against oracle.dropout_keep bit for bit, o against
+    exact_attention64 with that mask, the gradients against exact_backward64
+    with it."""
     B, T, H, d = p["B"], p["T"], p["H"], p["d"]
     io = p.get("io", F32)
     mode = MODE_INERT if p.get("mode") == "inert" else MODE_CAUSAL
@@ -553,8 +564,22 @@ def case_masked_bwd(emu: Emu, p):
     lse = emu.empty((B, H, Tp), np.float32)
     args = (s["qh"].ptr, s["kh"].ptr, s["vh"].ptr, s["P"].ptr if nb else None, hol,
             md.ptr if md else None, T if md else 0)
-    emu.check(emu.lib.holo_attn_masked_train_fwd(B, T, H, d, io, mode, scale, *args, o.ptr, H * d, d, lse.ptr,
-                                                 wsf.ptr, n, None), "holo_attn_masked_train_fwd")
+    drop = p.get("drop")
+    keep, dscale = None, 1.0
+    if drop:
+        dp, dseed, doff = float(drop["p"]), int(drop["seed"]), int(drop.get("offset", 0))
+        dscale = float(np.float32(1.0) / (np.float32(1.0) - np.float32(dp)))
+        keep_dev = emu.empty((B, H, T, T), np.uint8)
+        emu.check(emu.lib.holo_dropout_keep_mask(B, T, H, dp, dseed, doff, keep_dev.ptr, None),
+                  "holo_dropout_keep_mask")
+        keep = R.dropout_keep(B, H, T, dp, dseed, doff)
+        keep_identical = bool(np.array_equal(keep_dev.a.astype(bool), keep))
+        emu.check(emu.lib.holo_attn_masked_dropout_fwd(B, T, H, d, io, mode, scale, dp, dseed, doff, *args, o.ptr,
+                                                       H * d, d, lse.ptr, wsf.ptr, n, None),
+                  "holo_attn_masked_dropout_fwd")
+    else:
+        emu.check(emu.lib.holo_attn_masked_train_fwd(B, T, H, d, io, mode, scale, *args, o.ptr, H * d, d, lse.ptr,
+                                                     wsf.ptr, n, None), "holo_attn_masked_train_fwd")
     emu.check(emu.lib.holo_attn_masked_fwd(B, T, H, d, io, QUAT_F32, mode, scale, *args, o_ref_kernel.ptr, H * d, d,
                                            wsf.ptr, n, None), "holo_attn_masked_fwd")
     rng = np.random.default_rng(p.get("seed", 8) + 100)
@@ -567,21 +592,26 @@ def case_masked_bwd(emu: Emu, p):
     dgk = emu.empty((B, T, H, m), np.float32) if add else None
     nw = int(emu.lib.holo_attn_masked_bwd_workspace_size(B, T, H, d, io, mode, int(mask is not None)))
     ws = emu.empty((max(nw, 1),), np.uint8)
-    emu.check(emu.lib.holo_attn_masked_bwd(
-        B, T, H, d, gen, float(es), io, F32, mode, scale,
+    bwd = emu.lib.holo_attn_masked_dropout_bwd if drop else emu.lib.holo_attn_masked_bwd
+    dargs = (dp, dseed, doff) if drop else ()
+    emu.check(bwd(
+        B, T, H, d, gen, float(es), io, F32, mode, scale, *dargs,
         s["gq"].ptr, H * m, m, s["gk"].ptr if add else None, H * m if add else 0, m if add else 0,
         s["qh"].ptr, s["kh"].ptr, s["vh"].ptr, s["P"].ptr if nb else None, hol, lse.ptr,
         md.ptr if md else None, T if md else 0,
         o.ptr, H * d, d, dout.ptr, H * d, d,
         dq.ptr, H * d, d, dk.ptr, H * d, d, dv.ptr, H * d, d,
         dgq.ptr, H * m, m, dgk.ptr if add else None, H * m if add else 0, m if add else 0, ws.ptr, nw, None),
-        "holo_attn_masked_bwd")
+        "holo_attn_masked_dropout_bwd" if drop else "holo_attn_masked_bwd")
     st = emu.empty((1,), np.uint32)
     emu.check(emu.lib.holo_workspace_status(ws.ptr, ws.nbytes, st.ptr, None), "holo_workspace_status")
+    if not p.get("check", True):              # bounds only (sizes whose float64 T x T arrays do not fit)
+        finite = all(bool(np.isfinite(emu.host(b_, _dtype(io))).all()) for b_ in (dq, dk, dv))
+        return {"status": int(st.a[0]), "finite": finite and bool(np.isfinite(dgq.a).all())}
     bh = lambda u: u.transpose(0, 2, 1, 3)
     mname = "inert" if mode == MODE_INERT else "causal"
     a = L.a(gen)
-    g = R.exact_backward64(bh(L.q), bh(L.k), bh(L.v), a, bh(do_h), scale, mask, mname)
+    g = R.exact_backward64(bh(L.q), bh(L.k), bh(L.v), a, bh(do_h), scale, mask, mname, keep=keep, drop_scale=dscale)
     Pr, Holr = R.geometry_blocks(a)
     # lse (log2 domain of the scaled scores) from the float64 scores
     if mname == "causal":
@@ -607,10 +637,23 @@ def case_masked_bwd(emu: Emu, p):
     digest = hashlib.sha256()
     for b_ in (dq, dk, dv, dgq) + ((dgk,) if add else ()):
         digest.update(b_.a.tobytes())
-    res = {"status": int(st.a[0]), "o_identical": bool(np.array_equal(o.a, o_ref_kernel.a)),
+    if drop:
+        # with dropout o differs from holo_attn_masked_fwd's: against the oracle
+        o_ref = R.exact_attention64(bh(L.q), bh(L.k), bh(L.v), Pr, Holr, scale, mask, mname, keep=keep,
+                                    drop_scale=dscale)
+        o_got = bh(emu.host(o, _dtype(io)))
+        o_identical = None
+    else:
+        o_identical = bool(np.array_equal(o.a, o_ref_kernel.a))
+    res = {"status": int(st.a[0]), "o_identical": o_identical,
            "lse_err": float(np.abs(lse.a[:, :, :T] - lse_ref).max()),
            "closing_edge_max": float(np.abs(ref["dgq"][:, :, -1]).max()),
            "grad_sha256": digest.hexdigest()}
+    if drop:
+        res["keep_identical"] = keep_identical
+        res["keep_frac"] = float(keep.mean())
+        res["keep_n"] = int(keep.size)
+        res["o_drop_rel"] = float(np.abs(o_got - o_ref).max() / max(1.0, np.abs(o_ref).max()))
     # errors over each gradient's scale: its largest entry, at least 5% of
     # the largest entry of any of the five (a gradient that is 0 exactly,
     # e.g. dq at T = 1, where dS = dA - delta cancels, is then held to the
@@ -630,7 +673,7 @@ def case_masked_bwd(emu: Emu, p):
             u = unpack_vh(u.reshape(B, H, Tp // 64, Dp, 64), T) if tr else u.reshape(B, H, Tp, Dp)[:, :, :T]
             u = u[..., :d]
             own.append(R.apply_blocks(Pr, u) if mname == "causal" else R.apply_blocks_T(Pr, u))
-        g2 = R.exact_backward64(*own, a, bh(do_h), scale, mask, mname)
+        g2 = R.exact_backward64(*own, a, bh(do_h), scale, mask, mname, keep=keep, drop_scale=dscale)
         ref2 = {"dq": g2["dq"], "dk": g2["dk"], "dv": g2["dv"], "dgq": es * g2["da"]}
         for k_, r_ in ref2.items():
             res[k_ + "_fro_own"] = float(np.linalg.norm(got[k_] - r_) / max(np.linalg.norm(r_), 0.05 * scale_all))

@@ -18,11 +18,15 @@ def test_multi_gpu_request_exits_with_message():
 
 def test_contradictory_options_exit_before_any_gpu_work():
     """--fused-interaction needs the interaction generator; training off the
-    tril path needs --exact-backward, which applies to nothing else."""
+    tril path needs --exact-backward, which applies to nothing else;
+    --dropout needs --train with --exact-backward and 0 <= P < 1."""
     for argv, needle in ((["--fused-interaction"], "--link interaction"),
                          (["--train", "--mask", "ring"], "--exact-backward"),
                          (["--train", "--mode", "inert"], "--exact-backward"),
-                         (["--exact-backward"], "applies to --train")):
+                         (["--exact-backward"], "applies to --train"),
+                         (["--train", "--exact-backward"], "applies to --train"),
+                         (["--train", "--dropout", "0.1"], "--dropout"),
+                         (["--train", "--exact-backward", "--dropout", "1.0"], "--dropout")):
         r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), *argv],
                            capture_output=True, text=True, timeout=120)
         assert r.returncode == 2 and needle in r.stderr and r.stdout == "", (argv, r.stderr)

@@ -34,6 +34,9 @@ Tolerances (written per case below):
                  rounding bounds of tests/test_gpu_edge_mlp.py (err / bound
                  <= 1); the hidden-only launch bit-identical to the combined
                  one; the chained interaction layer's per-head o within 2e-3.
+  dropout     -- the keep mask bit-identical to oracle.dropout_keep; o with
+                 dropout and every gradient to the exact-path backward's
+                 bars against the oracle given that mask.
   exact path  -- fp32 max-abs 2e-5; bf16 max-abs 2.5e-2 and relative
                  Frobenius 1e-2; NaN rows exactly where the oracle's are.
   backward    -- fp32: each gradient within 2e-5 of its largest entry; bf16:
@@ -321,6 +324,55 @@ def mbwd_results():
 def test_emulated_exact_path_backward(mbwd_results, cid):
     check = next(c[3] for c in MBWD if c[0] == cid)
     r = mbwd_results[cid]
+    assert r["stats"]["launches"] > 0
+    check(r)
+
+
+# ---- attention dropout on the exact path (holo_attn_masked_dropout_fwd / _bwd) ----
+def _drop(io, wrap_pairs, p):
+    def check(r):
+        assert r["status"] == 0 and r["keep_identical"], r
+        assert abs(r["keep_frac"] - (1 - p)) <= 5 * (p * (1 - p) / r["keep_n"]) ** 0.5, r
+        if io == F32:
+            assert r["o_drop_rel"] <= 2e-5 and r["lse_err"] <= 1e-5, r
+            assert all(v <= 2e-5 for k, v in r.items() if k.endswith("_rel") and k != "o_drop_rel"), r
+        else:
+            assert r["o_drop_rel"] <= 2.5e-2 and r["lse_err"] <= 2e-2, r
+            assert all(r[k + "_fro"] <= 1.5e-2 for k in ("dq", "dk", "dv")), r
+            assert r["dgq_fro"] <= 3e-2 and r.get("dgk_fro", 0.0) <= 3e-2, r
+        assert (r["closing_edge_max"] > 1e-3) == wrap_pairs, r
+    return check
+
+
+DROP = []
+for i, (B, T, H, d, mode, mask, io, es, p, gen) in enumerate([
+        (1, 70, 2, 12, "causal", "none", F32, 0.9, 0.2, 0), (2, 130, 3, 16, "inert", "ring", F32, 0.9, 0.5, 0),
+        (1, 65, 2, 48, "causal", "random", F32, 0.9, 0.1, 0), (1, 129, 2, 96, "causal", "tril", F32, 0.9, 0.3, 0),
+        (1, 1, 2, 12, "causal", "none", F32, 0.9, 0.25, 0), (2, 100, 2, 24, "causal", "random", F32, 0.5, 0.4, 1),
+        (1, 300, 2, 96, "causal", "none", BF16, 0.05, 0.1, 0), (1, 300, 2, 96, "inert", "ring", BF16, 0.05, 0.1, 0),
+        (1, 300, 2, 96, "causal", "tril", BF16, 0.05, 0.1, 0)]):
+    wrap_pairs = mode == "causal" and mask != "tril" and T > 1
+    drop = {"p": p, "seed": 0x9E3779B97F4A7C15 + 1000 * i, "offset": i}
+    DROP.append((f"dropout_{mode}_{mask}_{'bf16' if io == BF16 else 'f32'}_T{T}_d{d}_p{p}{'_direct' if gen else ''}",
+                 "masked_bwd", dict(B=B, T=T, H=H, d=d, mode=mode, mask=mask, io=io, es=es, gen=gen, drop=drop),
+                 _drop(io, wrap_pairs, p)))
+jobs.register("dropout", [(name, params) for _, name, params, _ in DROP], timeout=900)
+
+
+@pytest.fixture(scope="module")
+def drop_results():
+    rc, out, res = jobs.result("dropout")
+    if rc != 0 or res is None:
+        pytest.fail(f"emulated run failed (status {rc}):\n{out[-12000:]}")
+    assert len(res["cases"]) == len(DROP)
+    return {cid: r for (cid, *_), r in zip(DROP, res["cases"])}
+
+
+@pytest.mark.emu_jobs("dropout")
+@pytest.mark.parametrize("cid", [c[0] for c in DROP])
+def test_emulated_exact_path_dropout(drop_results, cid):
+    check = next(c[3] for c in DROP if c[0] == cid)
+    r = drop_results[cid]
     assert r["stats"]["launches"] > 0
     check(r)
 

@@ -20,7 +20,8 @@ the batch offset, which config 2's B = 16 run and the B = 64 GEMM and
 attention exercise); the exact-path and interaction layouts run at B = 4 of
 config 2, the training step's backward at one batch row and two heads of
 config 2's head size (also the exact path's training pair, off in the
-module). The fused interaction generator's two GEMMs (off in the module) run
+module, with and without attention dropout). The fused interaction
+generator's two GEMMs (off in the module) run
 at config 2's shape with sampled workgroups.
 """
 from __future__ import annotations
@@ -50,6 +51,11 @@ CHECKS = [
                                                                mode="causal", mask="ring")),
     ("cfg2_exact_train_backward_inert_bf16", "masked_bwd", dict(B=1, T=1024, H=2, d=96, io=1, es=0.05,
                                                                 mode="inert")),
+    # the same pair with attention dropout (p = 0.1, the keep-mask kernel
+    # too) under tril(T), the mask of a causal training step
+    ("cfg2_dropout_train_backward_tril_bf16", "masked_bwd", dict(B=1, T=1024, H=2, d=96, io=1, es=0.05,
+                                                                 mode="causal", mask="tril",
+                                                                 drop={"p": 0.1, "seed": 2024, "offset": 1})),
     # the fused interaction generator (off in the module): first and last
     # four and every 997th workgroup of both GEMMs, written entries checked
     ("cfg2_fused_interaction_gemms", "edge", dict(B=16, T=2048, K=1536, H=16, sample=[4, 4, 997])),
@@ -108,6 +114,10 @@ def test_launch_in_bounds(checked, cid):
     if cid.startswith("cfg2_exact_train_backward"):
         assert r["o_identical"] and all(v <= 3e-2 for k, v in r.items() if "_fro" in k), r
         assert (r["closing_edge_max"] > 1e-3) == ("ring" in cid), r
+    if cid == "cfg2_dropout_train_backward_tril_bf16":
+        assert r["keep_identical"] and r["o_drop_rel"] <= 2.5e-2, r
+        assert all(v <= 3e-2 for k, v in r.items() if "_fro" in k), r
+        assert r["closing_edge_max"] <= 1e-3, r
     if cid == "cfg2_fused_interaction_gemms":
         assert r["hid_err_over_bound"] <= 1.0 and r["qkv_err_over_bound"] <= 1.0 and r["g_err_over_bound"] <= 1.0, r
         assert r["written_hid"] > 0 and r["written_qkv"] > 0 and r["written_g"] > 0, r

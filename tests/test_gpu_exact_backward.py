@@ -8,7 +8,11 @@ holonomy and for inert mode, with no mask, the ring mask and a random mask.
 Bars (written in the tests): fp32 every gradient within 2e-5 of its scale
 (its largest entry); bf16 relative Frobenius 1.5e-2 for dq, dk, dv and 3e-2
 for the generator gradients (the tril backward's bf16 bar); the training
-forward's o equal to attention_masked's.
+forward's o equal to attention_masked's. With attention dropout
+(holo_attn_masked_dropout_fwd / _bwd): the keep mask of
+kernels.dropout_keep_mask bit-identical to oracle.dropout_keep, o against
+exact_attention64 with that mask (fp32 within 1e-5 of max(1, max|o|), bf16
+2.5e-2), every gradient to the bars above against exact_backward64 with it.
 """
 from __future__ import annotations
 
@@ -70,6 +74,51 @@ def test_exact_path_gradients_against_the_oracle(mode, mask_kind, dtype):
     bh = lambda t: t.double().cpu().numpy().transpose(0, 2, 1, 3)
     a = es * (bh(gq) + np.roll(bh(gk), -1, axis=2))
     g = R.exact_backward64(bh(q), bh(k), bh(v), a, bh(do), scale, None if mask is None else mask.numpy(), mode)
+    ref = {"dq": g["dq"], "dk": g["dk"], "dv": g["dv"], "dgq": es * g["da"], "dgk": np.roll(es * g["da"], 1, axis=2)}
+    got = {"dq": bh(dq), "dk": bh(dk), "dv": bh(dv), "dgq": bh(dgq), "dgk": bh(dgk)}
+    for name, r in ref.items():
+        err = got[name] - r
+        if dtype == torch.float32:
+            assert np.abs(err).max() <= 2e-5 * np.abs(r).max(), name
+        else:
+            bar = 3e-2 if name.startswith("dg") else 1.5e-2
+            assert np.linalg.norm(err) <= bar * np.linalg.norm(r), name
+
+
+@pytest.mark.parametrize("mode,mask_kind", [("causal", "none"), ("causal", "tril"), ("inert", "ring")])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_exact_path_dropout_against_the_oracle(mode, mask_kind, dtype):
+    B, T, H, d, es, p, seed, offset = 2, 300, 2, 96, 0.05, 0.2, 0x0123456789ABCDEF, 5
+    q, k, v, gq, gk, do = _inputs(9, B, T, H, d, dtype, es)
+    mask = None
+    if mask_kind == "ring":
+        mask = torch.as_tensor(R.ring_mask(T))
+    elif mask_kind == "tril":
+        mask = torch.ones(T, T, dtype=torch.bool).tril()
+    qd, kd, vd, gqd, gkd, dod = (t.to(DEV) for t in (q, k, v, gq, gk, do))
+    md = None if mask is None else mask.to(DEV)
+    scale = 1.0 / math.sqrt(d)
+    keep = kernels.dropout_keep_mask(B, T, H, p, seed, offset, device=DEV)
+    qh, kh, vh_t, P, hol = kernels.geom_scan(qd, kd, vd, gqd, gkd, es, want_hol=mode == "causal", p_format="f32",
+                                             mode=mode)
+    o, lse = kernels.attention_masked_train(qh, kh, vh_t, P, hol, d, scale, mode=mode, mask=md, dropout_p=p,
+                                            seed=seed, offset=offset)
+    dq, dk, dv = (torch.empty_like(qd) for _ in range(3))
+    dgq, dgk = torch.empty_like(gqd), torch.empty_like(gkd)
+    kernels.attention_masked_backward(gqd, gkd, es, qh, kh, vh_t, P, hol, lse, o, dod, d, scale, dq, dk, dv, dgq, dgk,
+                                      mode=mode, mask=md, dropout_p=p, seed=seed, offset=offset)
+    torch.cuda.synchronize()
+    keep_ref = R.dropout_keep(B, H, T, p, seed, offset)
+    assert np.array_equal(keep.cpu().numpy(), keep_ref)
+    ds = float(np.float32(1) / (np.float32(1) - np.float32(p)))
+    bh = lambda t: t.double().cpu().numpy().transpose(0, 2, 1, 3)
+    a = es * (bh(gq) + np.roll(bh(gk), -1, axis=2))
+    mk = None if mask is None else mask.numpy()
+    Pr, Holr = R.geometry_blocks(a)
+    o_ref = R.exact_attention64(bh(q), bh(k), bh(v), Pr, Holr, scale, mk, mode, keep=keep_ref, drop_scale=ds)
+    o_err = np.abs(bh(o) - o_ref).max() / max(1.0, np.abs(o_ref).max())
+    assert o_err <= (1e-5 if dtype == torch.float32 else 2.5e-2), o_err
+    g = R.exact_backward64(bh(q), bh(k), bh(v), a, bh(do), scale, mk, mode, keep=keep_ref, drop_scale=ds)
     ref = {"dq": g["dq"], "dk": g["dk"], "dv": g["dv"], "dgq": es * g["da"], "dgk": np.roll(es * g["da"], 1, axis=2)}
     got = {"dq": bh(dq), "dk": bh(dk), "dv": bh(dv), "dgq": bh(dgq), "dgk": bh(dgk)}
     for name, r in ref.items():

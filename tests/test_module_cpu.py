@@ -57,9 +57,9 @@ def test_dispatch_between_tril_and_exact_paths():
 
 @pytest.mark.parametrize("kind", ["cpu", "inert", "nomask", "ring", "dropout", "dtype"])
 def test_unsupported_calls_raise(kind):
-    """No CPU path and no dropout: such calls raise NotImplementedError (the
-    guarded reference's exception, kernel/attention_fast_chunked.py:106-114)
-    whatever the mask and mode."""
+    """No CPU path, and no attention dropout unless exact_backward is on: such
+    calls raise NotImplementedError (the guarded reference's exception,
+    kernel/attention_fast_chunked.py:106-114) whatever the mask and mode."""
     T = 6
     m = PathOrderedGeometricMHA(24, n_heads=2, mode="inert" if kind == "inert" else "causal",
                                 dropout=0.1 if kind == "dropout" else 0.0)
@@ -245,13 +245,15 @@ def test_exact_backward_option_routes_autograd_through_the_exact_path(monkeypatc
         hol = torch.zeros(B, H, d // 3, 4) if want_hol else None
         return torch.zeros(1), torch.zeros(1), torch.zeros(1), P, hol
 
-    def fake_train(qh, kh, vh_t, P, hol, d_, scale, mode="causal", mask=None):
+    def fake_train(qh, kh, vh_t, P, hol, d_, scale, mode="causal", mask=None, dropout_p=0.0, seed=0, offset=0):
         seen["train"] = (mode, None if mask is None else mask.clone(), hol is not None)
+        seen["train_drop"] = (dropout_p, seed, offset)
         return torch.ones(B, T, H, d_), torch.zeros(B, H, 64)
 
     def fake_bwd(gq, gk, es, qh, kh, vh_t, P, hol, lse, o, dout, d_, scale, dq, dk, dv, dgq, dgk, mode="causal",
-                 mask=None, workspace=None):
+                 mask=None, workspace=None, dropout_p=0.0, seed=0, offset=0):
         seen["bwd"] = (mode, None if mask is None else mask.clone(), tuple(dout.shape))
+        seen["bwd_drop"] = (dropout_p, seed, offset)
         for t in (dq, dk, dv, dgq) + ((dgk,) if dgk is not None else ()):
             t.fill_(1.0)
 
@@ -272,10 +274,34 @@ def test_exact_backward_option_routes_autograd_through_the_exact_path(monkeypatc
         assert seen["train"][0] == mode and torch.equal(seen["train"][1], ring) and seen["train"][2] == (mode == "causal")
         y.sum().backward()
         assert seen["bwd"][0] == mode and torch.equal(seen["bwd"][1], ring) and seen["bwd"][2] == (B, T, H, d)
+        assert seen["train_drop"] == seen["bwd_drop"] == (0.0, 0, 0)
         assert x.grad is not None and m.qkv.weight.grad is not None
         assert (m.gqproj.weight.grad if link == "additive" else m.edge_mlp[0].weight.grad) is not None
     m = PathOrderedGeometricMHA(D, n_heads=H)
     assert m.exact_backward is False
+
+    # active attention dropout: every mask (tril included) runs the exact
+    # pair with the module's p and one fresh seed, which the backward gets
+    # too; the seed comes from torch's CPU generator (repeatable under
+    # torch.manual_seed)
+    tril = torch.ones(T, T, dtype=torch.bool).tril()
+    m = PathOrderedGeometricMHA(D, n_heads=H, dropout=0.25)
+    assert m._dropout_active() and not m.eval()._dropout_active()
+    m.train()
+    m.exact_backward = True
+    seeds = []
+    for rep in range(3):
+        seen.clear()
+        if rep < 2:
+            torch.manual_seed(11)
+        x = torch.randn(B, T, D, requires_grad=True)
+        y, geo = m._forward_dropout(x, tril, False)
+        assert geo is None and torch.equal(seen["train"][1], tril) and seen["train"][0] == "causal"
+        y.sum().backward()
+        p_, seed, off = seen["train_drop"]
+        assert p_ == 0.25 and off == 0 and 0 <= seed < 2 ** 63 and seen["bwd_drop"] == (p_, seed, off)
+        seeds.append(seed)
+    assert seeds[0] == seeds[1] != seeds[2]
 
 
 def test_forward_only_outputs_without_exact_backward():
