@@ -255,6 +255,8 @@ class PathOrderedGeometricMHA(nn.Module):
     def _unsupported_reason(self, x, attn_mask, causal_implied: bool = False) -> Optional[str]:
         if not x.is_cuda:
             return "input is not on the GPU"
+        if self._dropout_active() and causal_implied:
+            return "attention dropout is active (prefill and decode apply none)"
         if self._dropout_active() and not getattr(self, "exact_backward", False):
             return ("attention dropout is active (the exact path's dropout kernels run it when exact_backward "
                     "is on)")
@@ -655,6 +657,9 @@ class PathOrderedGeometricMHA(nn.Module):
         B, L, D = x_t.shape
         if L != 1:
             raise ValueError("decode_step takes one token per sequence (B, 1, D)")
+        if self._dropout_active():
+            raise NotImplementedError("holonomyawareattention_amd decode_step: attention dropout is active "
+                                      "(prefill and decode apply none)")
         t = state.t
         if t >= state.capacity:
             raise ValueError(f"decode cache full ({state.capacity} positions)")

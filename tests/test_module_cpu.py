@@ -302,6 +302,17 @@ def test_exact_backward_option_routes_autograd_through_the_exact_path(monkeypatc
         assert p_ == 0.25 and off == 0 and 0 <= seed < 2 ** 63 and seen["bwd_drop"] == (p_, seed, off)
         seeds.append(seed)
     assert seeds[0] == seeds[1] != seeds[2]
+    # prefill and decode apply no dropout: they refuse it, exact_backward or not
+    # (a stand-in for a GPU tensor: the reason is decided before any data is read)
+    import types
+    gpu_like = types.SimpleNamespace(is_cuda=True, dtype=torch.float32, shape=(B, T, D))
+    assert "prefill and decode" in m._unsupported_reason(gpu_like, None, causal_implied=True)
+    with pytest.raises(NotImplementedError, match="dropout"):
+        m.decode_step(torch.randn(B, 1, D), None)
+    m.exact_backward = False
+    assert "exact_backward" in m._unsupported_reason(gpu_like, None)
+    m.eval()
+    assert m._unsupported_reason(gpu_like, None) is None
 
 
 def test_forward_only_outputs_without_exact_backward():
