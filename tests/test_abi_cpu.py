@@ -332,3 +332,32 @@ def test_exact_path_training_argument_validation(lib):
                         16, 24, 12, lse, 16, 1 << 20, None)
     assert t(*args(None)) == _lib.HOLO_ERR_INVALID_ARG                    # the LSE is the point of this call
     assert t(*args(8)) == _lib.HOLO_ERR_INVALID_ARG                       # misaligned LSE
+
+
+def test_dropout_argument_validation(lib):
+    """The dropout entry points refuse a probability outside [0, 1) (NaN
+    included), a null LSE or keep buffer and the exact path's other invalid
+    arguments before any launch."""
+    f = lib.holo_attn_masked_dropout_fwd
+    fargs = lambda p, lse=16, B=1: (B, 8, 2, 12, _lib.HOLO_F32, _lib.HOLO_MODE_CAUSAL, 0.3, p, 2 ** 64 - 1, 7,
+                                    16, 16, 16, 16, 16, 16, 8, 16, 24, 12, lse, 16, 1 << 20, None)
+    for p in (-0.1, 1.0, 1.5, float("nan"), float("inf")):
+        assert f(*fargs(p)) == _lib.HOLO_ERR_INVALID_ARG, p
+        assert "dropout probability" in lib.holo_last_error().decode()
+    assert f(*fargs(0.1, lse=None)) == _lib.HOLO_ERR_INVALID_ARG
+    assert f(*fargs(0.1, lse=8)) == _lib.HOLO_ERR_INVALID_ARG            # misaligned LSE
+    assert f(*fargs(0.1, B=0)) == _lib.HOLO_ERR_BAD_SHAPE
+    b = lib.holo_attn_masked_dropout_bwd
+    bargs = lambda p, **kw: (1, 8, 2, 12, 0, 0.1, _lib.HOLO_F32, _lib.HOLO_F32, kw.get("mode", _lib.HOLO_MODE_CAUSAL),
+                             0.3, p, 5, 0, 16, 64, 24, 16, 64, 24, 16, 16, 16, 16, kw.get("hol", 16), 16, 16, 8,
+                             16, 64, 24, 16, 64, 24, 16, 64, 24, 16, 64, 24, 16, 64, 24, 16, 64, 24, 16, 64, 24,
+                             16, 1 << 30, None)
+    assert b(*bargs(1.0)) == _lib.HOLO_ERR_INVALID_ARG
+    assert b(*bargs(-1e-7)) == _lib.HOLO_ERR_INVALID_ARG
+    assert b(*bargs(0.2, mode=3)) == _lib.HOLO_ERR_INVALID_ARG
+    assert b(*bargs(0.2, hol=None)) == _lib.HOLO_ERR_INVALID_ARG
+    k = lib.holo_dropout_keep_mask
+    assert k(1, 8, 2, 0.1, 1, 0, None, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert k(1, 8, 2, 1.0, 1, 0, 16, None) == _lib.HOLO_ERR_INVALID_ARG
+    assert k(0, 8, 2, 0.1, 1, 0, 16, None) == _lib.HOLO_ERR_BAD_SHAPE
+    assert k(1, 0, 2, 0.1, 1, 0, 16, None) == _lib.HOLO_ERR_BAD_SHAPE
