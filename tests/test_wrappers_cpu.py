@@ -38,6 +38,14 @@ CALLS = {
                                                          _t(B, H, nb, 4), 0, d, 0.5),
     "add_layernorm": lambda: kernels.add_layernorm(_t(4, 8), _t(4, 8), _t(8), _t(8)),
     "workspace_status": lambda: kernels.workspace_status(_t(64, dtype=torch.uint8), _t(1, dtype=torch.int32)),
+    "attention_masked_train": lambda: kernels.attention_masked_train(
+        _t(B, H, Tp, Dp), _t(B, H, Tp, Dp), _t(B, H, 1, Dp, 64), _t(B, H, T, nb, 4), _t(B, H, nb, 4), d, 0.5,
+        dropout_p=0.1, seed=3),
+    "attention_masked_backward": lambda: kernels.attention_masked_backward(
+        _t(B, T, H, d), None, 0.1, _t(B, H, Tp, Dp), _t(B, H, Tp, Dp), _t(B, H, 1, Dp, 64), _t(B, H, T, nb, 4),
+        _t(B, H, nb, 4), _t(B, H, Tp), _t(B, T, H, d), _t(B, T, H, d), d, 0.5, _t(B, T, H, d), _t(B, T, H, d),
+        _t(B, T, H, d), _t(B, T, H, d), None, dropout_p=0.1, seed=3),
+    "dropout_keep_mask": lambda: kernels.dropout_keep_mask(B, T, H, 0.1, 3, device="cpu"),
 }
 
 
@@ -52,3 +60,13 @@ def test_one_gpu_reports_the_offending_tensor():
         kernels._one_gpu("probe", None, torch.zeros(1))
     with pytest.raises(ValueError, match="no tensor"):
         kernels._one_gpu("probe", None)
+
+
+def test_dropout_arguments_are_checked_on_the_host():
+    """dropout_p outside [0, 1), a seed beyond 64 bits or an offset beyond 32
+    bits fail as ValueError before the library is called."""
+    for p, seed, off in ((1.0, 0, 0), (-0.5, 0, 0), (float("nan"), 0, 0), (0.1, -1, 0), (0.1, 2 ** 64, 0),
+                         (0.1, 0, 2 ** 32)):
+        with pytest.raises(ValueError, match="dropout_p|seed"):
+            kernels._dropout_args("probe", p, seed, off)
+    assert kernels._dropout_args("probe", 0.25, 2 ** 64 - 1, 2 ** 32 - 1) == (0.25, 2 ** 64 - 1, 2 ** 32 - 1)
