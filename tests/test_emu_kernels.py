@@ -350,7 +350,9 @@ for i, (B, T, H, d, mode, mask, io, es, p, gen) in enumerate([
         (1, 65, 2, 48, "causal", "random", F32, 0.9, 0.1, 0), (1, 129, 2, 96, "causal", "tril", F32, 0.9, 0.3, 0),
         (1, 1, 2, 12, "causal", "none", F32, 0.9, 0.25, 0), (2, 100, 2, 24, "causal", "random", F32, 0.5, 0.4, 1),
         (1, 300, 2, 96, "causal", "none", BF16, 0.05, 0.1, 0), (1, 300, 2, 96, "inert", "ring", BF16, 0.05, 0.1, 0),
-        (1, 300, 2, 96, "causal", "tril", BF16, 0.05, 0.1, 0)]):
+        (1, 300, 2, 96, "causal", "tril", BF16, 0.05, 0.1, 0), (2, 200, 2, 64, "causal", "random", BF16, 0.9, 0.3, 0),
+        (2, 64, 1, 5, "inert", "none", F32, 0.9, 0.6, 0), (1, 100, 2, 34, "causal", "random", F32, 0.9, 0.15, 1),
+        (1, 129, 2, 96, "inert", "ring", F32, 0.9, 0.2, 1)]):
     wrap_pairs = mode == "causal" and mask != "tril" and T > 1
     drop = {"p": p, "seed": 0x9E3779B97F4A7C15 + 1000 * i, "offset": i}
     DROP.append((f"dropout_{mode}_{mask}_{'bf16' if io == BF16 else 'f32'}_T{T}_d{d}_p{p}{'_direct' if gen else ''}",
