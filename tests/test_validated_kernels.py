@@ -1,11 +1,12 @@
 """Every kernel of the GPU-validated build compiles to the same gfx950
 instructions in the library as built now (the fingerprints of
 holonomyawareattention_amd/kernel_code.py against
-tests/validated_kernels.json), so changes made without a GPU run --
-new kernels, new template modes -- provably leave the validated kernels as
-they were. A kernel may change its symbol (e.g. a new template parameter
-with the old behaviour as one value); it is matched by its instructions.
-Kernels added since are listed, not checked."""
+tests/validated_kernels.json), with the same code-object metadata
+(register, LDS and scratch counts, argument layout), so changes made without
+a GPU run -- new kernels, new template modes -- provably leave the validated
+kernels as they were. A kernel may change its symbol (e.g. a new template
+parameter with the old behaviour as one value); it is matched by its
+instructions and metadata. Kernels added since are listed, not checked."""
 from __future__ import annotations
 
 import json
@@ -32,3 +33,9 @@ def test_validated_kernels_unchanged():
     added = sorted(set(now) - {n for h in ref.values() for n in by_hash.get(h, [])})
     print(f"{len(ref)} validated kernels, {len(renamed)} under a new symbol, {len(added)} added: {added}")
     assert not missing, f"validated kernels whose instructions changed: {missing}"
+    desc_ref = json.load(open(os.path.join(REPO, "tests", "validated_kernels.json")))["descriptors"]
+    desc_now = kernel_code.descriptors(LIB)
+    assert set(desc_now) == set(now) and len(set(desc_now.values())) > len(now) // 4   # not a constant hash
+    pairs = {(now[n], desc_now[n]) for n in now}
+    changed = [name for name, h in ref.items() if (h, desc_ref[name]) not in pairs]
+    assert not changed, f"validated kernels whose register, LDS or argument metadata changed: {changed}"
