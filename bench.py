@@ -144,6 +144,25 @@ def library_code():
     return _LIB_CODE["v"]
 
 
+def _base_name(name):
+    """A profiler's kernel name without template arguments and parameters
+    ("void holo::gemm_qkvg<256, ...>(holo::QkvgArgs)" -> "holo::gemm_qkvg");
+    mangled names are returned as they are."""
+    n = name.split("(")[0].split("<")[0]
+    return n.split(" ")[-1]
+
+
+def _same_code(code, name, sha):
+    """True when the library's kernel `name` has instruction fingerprint
+    `sha`, or, if no kernel has that name any more (a template parameter
+    added with the old code as one of its values), when exactly one kernel of
+    the same base name has it."""
+    if name in code:
+        return code[name] == sha
+    hits = {n for n, h in code.items() if h == sha and _base_name(n) == _base_name(name) and "(" in n}
+    return len(hits) == 1
+
+
 def traffic_from_profile(config, kernel_prefix):
     """(HBM bytes per launch, source) of the kernels whose name contains any
     of `kernel_prefix` (summed), from the committed
@@ -165,7 +184,7 @@ def traffic_from_profile(config, kernel_prefix):
                if any(p in name for p in kernel_prefix) and "fetch_size_bytes" in e and "write_size_bytes" in e}
     code = library_code()
     same = bool(matched) and code is not None and all(
-        e.get("code_sha256") is not None and code.get(name) == e["code_sha256"] for name, e in matched.items())
+        e.get("code_sha256") is not None and _same_code(code, name, e["code_sha256"]) for name, e in matched.items())
     src = {"profile": rel, "kernels": sorted(matched), "same_code": same,
            "measured_sources_sha": data.get("sources_sha"), "library_sources_sha": lib_sha,
            "measured_in_this_run": False}

@@ -58,19 +58,33 @@ def test_traffic_is_reported_only_for_the_profiled_machine_code(monkeypatch):
     monkeypatch.setattr(bench, "library_code", lambda: code)
     assert bench.traffic_from_profile("cfg2", ["rocclr_copyBuffer"])[0] is None   # no fingerprint recorded
     assert bench.traffic_from_profile("cfg9", ["attn_fwd_h16"])[0] is None
+    # a kernel renamed by a new template parameter keeps its figure when
+    # exactly one kernel of the same base name has the profiled code
+    gname = next(n for n in code if "gemm_qkvg" in n)
+    renamed = {k: v for k, v in code.items() if k != gname}
+    renamed["void holo::gemm_qkvg<256, 256, 4, 2, 64, 2, 2, 0>(holo::GemmArgsOf<0>::type)"] = code[gname]
+    monkeypatch.setattr(bench, "library_code", lambda: renamed)
+    assert bench.traffic_from_profile("cfg2", ["gemm_qkvg"])[0] > 1e9
+    renamed["void holo::gemm_qkvg<256, 256, 4, 2, 64, 2, 2, 1>(holo::GemmArgsOf<1>::type)"] = code[gname]
+    assert bench.traffic_from_profile("cfg2", ["gemm_qkvg"])[0] is None          # ambiguous
+    other = {k: v for k, v in renamed.items() if "gemm_qkvg" not in k}
+    other["void holo::other_gemm<0>(holo::GemmArgsOf<0>::type)"] = code[gname]
+    monkeypatch.setattr(bench, "library_code", lambda: other)
+    assert bench.traffic_from_profile("cfg2", ["gemm_qkvg"])[0] is None          # another kernel's name
 
 
 def test_profiled_kernels_match_the_library_as_built():
-    """The library as built now holds the profiled attention and scan kernels
-    with the fingerprints the profile recorded, so the bench line carries
-    their traffic."""
+    """The library as built now holds the profiled attention, scan and
+    projection kernels with the fingerprints the profile recorded (the
+    projection GEMM under the symbol its mode parameter gave it), so the bench
+    line carries their traffic."""
     sys.path.insert(0, REPO)
     import bench
     from holonomyawareattention_amd import _lib, kernel_code
     if not (os.path.exists(_lib.LIB_PATH) and kernel_code.tools_present()):
         import pytest
         pytest.skip("library not built or ROCm's disassembler absent")
-    for prefix in (["attn_fwd_h16"], ["scan_reset", "chunk_apply"]):
+    for prefix in (["attn_fwd_h16"], ["scan_reset", "chunk_apply"], ["gemm_qkvg"]):
         t, src = bench.traffic_from_profile("cfg2", prefix)
         assert t is not None and src["same_code"], src
 
