@@ -7,7 +7,8 @@ the float64 oracle, with the bounds checks of tests/test_emu_kernels.py and
 its tolerances (the check functions are that file's): the scan + causal
 attention (fp32 and fp16 operands), the exact path (both modes, five masks),
 the fused backward, the exact path's training pair with and without
-attention dropout, and incremental decode.
+attention dropout, incremental decode, the projection GEMM and the fused
+interaction generator's two GEMMs.
 
 The fixed shapes of the other emulation tests follow the GPU tests; these
 add the shapes in between, where index arithmetic on partial tiles, padded
@@ -20,8 +21,8 @@ import numpy as np
 import pytest
 
 from tests.emu import build_emu, jobs
-from tests.test_emu_kernels import (BF16, F16, F32, S16, _bwd, _decode, _drop, _fp32_scan_attn, _h16, _masked,
-                                    _mbwd)
+from tests.test_emu_kernels import (BF16, F16, F32, S16, _bwd, _decode, _drop, _edge, _fp32_scan_attn, _gemm, _h16,
+                                    _masked, _mbwd)
 
 pytestmark = pytest.mark.skipif(not (os.path.exists(build_emu.CLANG) and os.path.exists(build_emu.ASAN_RT)),
                                 reason="the CPU emulation needs ROCm's clang and its AddressSanitizer runtime")
@@ -75,6 +76,23 @@ for i in range(4):
     T0 = int(_rng.integers(1, T))
     FUZZ.append((f"decode_f32_{i}_B{B}_T{T}_T0{T0}_H{H}_d{d}", "decode",
                  dict(B=B, T=T, H=H, d=d, T0=T0, es=0.7, seed=600 + i), _decode(F32)))
+def _gemm_shape():
+    """(B, T, D, H): D a multiple of 64 (the GEMMs' K), H dividing D with the
+    generator width H * 3 floor(D / 3H) a multiple of 4 (the ABI's limits)."""
+    while True:
+        D = 64 * int(_rng.integers(1, 7))
+        H = int(_rng.choice([h for h in (1, 2, 3, 4, 6, 8) if D % h == 0]))
+        if (H * 3 * (D // H // 3)) % 4 == 0:
+            return int(_rng.integers(1, 4)), int(_rng.integers(1, 301)), D, H
+
+
+for i in range(5):
+    B, T, D, H = _gemm_shape()
+    FUZZ.append((f"gemm_{i}_B{B}_T{T}_D{D}_H{H}", "gemm",
+                 dict(B=B, T=T, K=D, n_qkv=3 * D, n_gen=H * 3 * (D // H // 3), seed=700 + i), _gemm))
+for i in range(3):
+    B, T, D, H = _gemm_shape()
+    FUZZ.append((f"edge_{i}_B{B}_T{T}_D{D}_H{H}", "edge", dict(B=B, T=T, K=D, H=H, seed=800 + i), _edge))
 jobs.register("fuzz_shapes", [(name, params) for _, name, params, _ in FUZZ], timeout=1500)
 
 
