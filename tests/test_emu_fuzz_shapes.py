@@ -22,7 +22,7 @@ import pytest
 
 from tests.emu import build_emu, jobs
 from tests.test_emu_kernels import (BF16, F16, F32, S16, _bwd, _decode, _drop, _edge, _fp32_scan_attn, _gemm, _h16,
-                                    _masked, _mbwd)
+                                    _masked, _mbwd, _norm)
 
 pytestmark = pytest.mark.skipif(not (os.path.exists(build_emu.CLANG) and os.path.exists(build_emu.ASAN_RT)),
                                 reason="the CPU emulation needs ROCm's clang and its AddressSanitizer runtime")
@@ -93,6 +93,29 @@ for i in range(5):
 for i in range(3):
     B, T, D, H = _gemm_shape()
     FUZZ.append((f"edge_{i}_B{B}_T{T}_D{D}_H{H}", "edge", dict(B=B, T=T, K=D, H=H, seed=800 + i), _edge))
+# longer sequences (one or two heads): more key tiles per query tile, the
+# chained scan over more chunks
+for i in range(4):
+    T, H, d = int(_rng.integers(300, 2100)), int(_rng.integers(1, 3)), int(_rng.integers(3, 97))
+    if i == 0:
+        FUZZ.append((f"long_scan_attn_f16_T{T}_H{H}_d{d}", "scan_attn",
+                     dict(B=1, T=T, H=H, d=d, io=BF16, op=F16, pf=S16, out=F32, es=0.3, seed=900 + i), _h16(F32)))
+    elif i == 1:
+        FUZZ.append((f"long_masked_causal_ring_bf16_T{T}_H{H}_d{d}", "masked",
+                     dict(B=1, T=T, H=H, d=d, io=BF16, mode="causal", mask="ring", pf=S16, seed=900 + i),
+                     _masked(BF16)))
+    elif i == 2:
+        FUZZ.append((f"long_bwd_f32_T{T}_H{H}_d{d}", "bwd", dict(B=1, T=T, H=H, d=d, es=0.5, seed=900 + i), _bwd(F32)))
+    else:
+        p = round(float(_rng.uniform(0.05, 0.5)), 3)
+        FUZZ.append((f"long_dropout_inert_random_T{T}_H{H}_d{d}_p{p}", "masked_bwd",
+                     dict(B=1, T=T, H=H, d=d, mode="inert", mask="random", io=F32, es=0.5, seed=900 + i,
+                          drop={"p": p, "seed": 11, "offset": 2}), _drop(F32, False, p)))
+for i in range(3):
+    io = F32 if i % 2 == 0 else BF16
+    e16 = 4 if io == F32 else 8                     # elements per 16 bytes: d a multiple of it
+    n, dd = int(_rng.integers(1, 5000)), e16 * int(_rng.integers(1, 600))
+    FUZZ.append((f"norm_{i}_io{io}_n{n}_d{dd}", "norm", dict(n=n, d=dd, io=io, seed=1000 + i), _norm(io)))
 jobs.register("fuzz_shapes", [(name, params) for _, name, params, _ in FUZZ], timeout=1500)
 
 
