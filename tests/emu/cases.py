@@ -659,6 +659,10 @@ def case_masked_bwd(emu: Emu, p):
            "grad_sha256": digest.hexdigest()}
     if drop:
         res["keep_identical"] = keep_identical
+        # the same gradient without dropout: how far the kernel's dv is from
+        # it shows that the comparison above can tell the two apart
+        g0 = R.exact_backward64(bh(L.q), bh(L.k), bh(L.v), a, bh(do_h), scale, mask, mname)
+        res["dv_rel_nodrop"] = float(np.abs(got["dv"] - g0["dv"]).max() / max(np.abs(g0["dv"]).max(), 1e-30))
         res["keep_frac"] = float(keep.mean())
         res["keep_n"] = int(keep.size)
         res["o_drop_rel"] = float(np.abs(o_got - o_ref).max() / max(1.0, np.abs(o_ref).max()))

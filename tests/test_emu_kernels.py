@@ -333,6 +333,8 @@ def _drop(io, wrap_pairs, p):
     def check(r):
         assert r["status"] == 0 and r["keep_identical"], r
         assert abs(r["keep_frac"] - (1 - p)) <= 5 * (p * (1 - p) / r["keep_n"]) ** 0.5, r
+        if r["keep_n"] >= 100:                 # dropout visibly changes dv (not at T = 1, where a row
+            assert r["dv_rel_nodrop"] > 1e-2, r   # of one key keeps or drops its only weight)
         if io == F32:
             assert r["o_drop_rel"] <= 2e-5 and r["lse_err"] <= 1e-5, r
             assert all(v <= 2e-5 for k, v in r.items() if k.endswith("_rel") and k != "o_drop_rel"), r
