@@ -1015,8 +1015,9 @@ def case_layer_paths(emu: Emu, p):
     the edge MLP's unbiased output gq (B, T, Hm) fp32 and its bias broadcast
     as gk with row stride 0, fp16 operands, int16 quaternions; "exact" -- the
     fused GEMM's layout (direct generator), bf16 operands, int16 quaternions,
-    the scan in `mode` and holo_attn_masked_fwd with `mask` ("none" or
-    "ring"). Attention workgroups may be sampled; the scan runs whole."""
+    the scan in `mode` and holo_attn_masked_fwd with `mask` ("none", "ring"
+    or a dense "random" one). Attention workgroups may be sampled; the scan
+    runs whole."""
     B, T, D, H = p["B"], p["T"], p["D"], p["H"]
     d = D // H
     nb, m = d // 3, 3 * (d // 3)
@@ -1078,6 +1079,9 @@ def case_layer_paths(emu: Emu, p):
     if path == "exact":               # the exact path's kernel on these operands
         kind = p.get("mask", "none")
         mask = R.ring_mask(T) if kind == "ring" else None
+        if kind == "random":                  # dense: every tile open, the mask read per element
+            mask = np.random.default_rng(5).random((T, T)) < 0.5
+            mask[np.arange(T), np.arange(T)] = True
         md = emu.to_dev(mask.astype(np.uint8), np.uint8) if mask is not None else None
         om = emu.empty((B, T, H, d), _dtype(io))
         nm = int(emu.lib.holo_attn_masked_workspace_size(B, T, H, d, io, mode, int(mask is not None)))

@@ -44,6 +44,8 @@ CHECKS = [
     ("cfg2_exact_no_mask_causal", "layer_paths", dict(B=4, **CFG2, path="exact", mask="none", sample_attn=S)),
     ("cfg2_exact_ring_inert", "layer_paths", dict(B=4, **CFG2, path="exact", mask="ring", mode="inert",
                                                   sample_attn=S)),
+    ("cfg2_exact_random_causal", "layer_paths", dict(B=4, **CFG2, path="exact", mask="random", mode="causal",
+                                                     sample_attn=S)),
     ("cfg2_train_backward_bf16", "bwd", dict(B=1, T=1024, H=2, d=96, io=1, es=0.05)),
     # the exact path's training pair (off in the module) at the same head
     # shape: causal mode with the ring mask (wrap pairs open), inert mode
